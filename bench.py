@@ -1,0 +1,202 @@
+"""Benchmark the complete LSSO mixer forward on one MI355X.
+
+Workload (BASELINE.json metric "mixer fwd tokens/s @B64 D256 H8 r32 L4096
+fp16"): LSSO(LSSOConfig(256, 8, 32, bias=True)) with seeded random
+compact-core parameters, x ~ N(0, 1) FP16 [64, 4096, 256], shared default
+positions, no mask.  One step is one forward x -> y including both
+projections (reference protocol: benchmarks/benchmark_ball.py:156-208).
+
+Prints one JSON line with the driver's fields plus
+  roofline      the dominant kernel (the input projection) from HIP events
+                recorded around its launches inside the timed region;
+  cpu_baseline  the CPU oracle (FP32 restatement of the reference CPU path)
+                timed on this host on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse_args() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--batch", type=int, default=64)
+    parser.add_argument("--length", type=int, default=4096)
+    parser.add_argument("--cpu-samples", type=int, default=8,
+                        help="sequences of the workload timed on the CPU oracle (0 skips)")
+    parser.add_argument("--cpu-repeats", type=int, default=3)
+    return parser.parse_args()
+
+
+def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> dict:
+    """Time the CPU oracle (reference CPU path restated, FP32) on `samples`
+    sequences of the workload; tokens/s is scaled by the sample size."""
+
+    from oracle import lsso_reference as oracle
+
+    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "1024")))
+    torch.set_num_threads(cores)
+    params = {name: p.detach().float().cpu() for name, p in layer.named_parameters()}
+    config = {"dim": layer.config.dim, "num_heads": layer.config.num_heads,
+              "rank": layer.config.rank, "bias": layer.config.bias}
+    x = x_cpu[:samples].contiguous()
+    with torch.no_grad():
+        oracle.lsso_forward(params, config, x)  # warmup
+        times = []
+        for _ in range(repeats):
+            start = time.perf_counter()
+            oracle.lsso_forward(params, config, x)
+            times.append(time.perf_counter() - start)
+    seconds = statistics.median(times)
+    tokens = x.shape[0] * x.shape[1]
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as handle:
+            for line in handle:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": tokens / seconds,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{x.shape[0]} of {x_cpu.shape[0]} sequences x {x.shape[1]} tokens, FP32 CPU oracle "
+                  f"(oracle/lsso_reference.py), median of {repeats} after 1 warmup, "
+                  f"{seconds * 1e3:.1f} ms per sample batch",
+        "cpu": model,
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+            "(every GPU box in this build has one MI355X).",
+            file=sys.stderr,
+        )
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm device", file=sys.stderr)
+        return 2
+
+    from lsso_amd import LSSO, LSSOConfig
+    from lsso_amd.ball import hip
+
+    hip.load()
+    device = torch.device("cuda", 0)
+    batch, length, dim, heads, rank = args.batch, args.length, 256, 8, 32
+    torch.manual_seed(0)
+    layer = LSSO(LSSOConfig(dim=dim, num_heads=heads, rank=rank, bias=True))
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.05)
+        layer.core_drive_weight.normal_(std=0.05)
+    layer = layer.to(device).eval()
+    x_cpu = torch.randn(batch, length, dim, generator=torch.Generator().manual_seed(1)).half()
+    x = x_cpu.to(device)
+
+    w_bc, b_bc = layer.w_bc.weight, layer.w_bc.bias
+    w_o, b_o = layer.w_o.weight, layer.w_o.bias
+    base, drive, eta_raw = layer.core_base_raw, layer.core_drive_weight, layer.eta_raw
+
+    # The step is exactly the module's native forward for an unmasked input
+    # with default positions (lsso_amd/ball/model.py, _forward_native),
+    # unrolled so that events bracket the input projection.
+    events = []
+
+    def step(record: bool) -> torch.Tensor:
+        if record:
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+        projected = hip.linear(x, w_bc, b_bc, torch.bfloat16)
+        if record:
+            stop.record()
+            events.append((start, stop))
+        mixed = hip.fast_mix(projected, base, drive, eta_raw)
+        return hip.linear(mixed, w_o, b_o, x.dtype)
+
+    with torch.inference_mode():
+        reference_out = layer(x, implementation="hip")
+        check = step(False)
+        if not torch.equal(check, reference_out):
+            print("unrolled step differs from LSSO.forward(implementation='hip')", file=sys.stderr)
+            return 1
+        for _ in range(args.warmup):
+            step(False)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(args.steps):
+            step(True)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+
+    ms_per_step = 1e3 * elapsed / args.steps
+    tokens = batch * length
+    value = tokens * args.steps / elapsed
+    projection_ms = statistics.mean(s.elapsed_time(e) for s, e in events)
+    width = heads * rank + dim
+    # Algorithmic bytes of the input projection per launch: x read (FP16) +
+    # packed write (BF16) + weights (FP32) + bias.
+    projection_bytes = tokens * (dim * 2 + width * 2) + width * dim * 4 + width * 4
+    achieved = projection_bytes / (projection_ms * 1e-3) / 1e9
+    chain_bytes = tokens * 5120
+    result = {
+        "metric": "mixer fwd tokens/s @B64 D256 H8 r32 L4096 fp16; % HBM roofline",
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: x ~ N(0,1) fp16, seeded random-init weights",
+        "config": {
+            "workload": "lsso_mixer_forward",
+            "batch": batch,
+            "length": length,
+            "dim": dim,
+            "heads": heads,
+            "rank": rank,
+            "bias": True,
+            "io_dtype": "fp16",
+            "positions": "default",
+            "mask": False,
+            "chain_hbm_fraction": chain_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "linear_kernel (input projection x -> packed)",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": None,
+            "avg_ms": projection_ms,
+        },
+    }
+    if args.cpu_samples > 0:
+        result["cpu_baseline"] = cpu_baseline(layer, x_cpu, min(args.cpu_samples, batch), args.cpu_repeats)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

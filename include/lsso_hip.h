@@ -1,0 +1,137 @@
+/*
+ * lsso_hip.h -- C ABI of the MI355X (gfx950) native LSSO mixer library.
+ *
+ * The library implements the DYNAMIC + Rank-Rotary LSSO mixer and its two
+ * biased projections as hand-written CDNA4 kernels.  Every entry point takes
+ * plain device pointers, sizes and a hipStream_t; the library never allocates
+ * device memory.  Callers size the scratch buffers with the *_workspace_bytes
+ * queries and own every allocation.  All launches are asynchronous and
+ * stream-ordered; no entry point synchronizes the host.
+ *
+ * Return values: 0 on success, a negative LSSO_HIP_E* code on failure.  The
+ * message of the most recent failure on the calling thread is available from
+ * lsso_hip_last_error().
+ *
+ * Each declaration cites the reference interface it replaces.  Reference
+ * paths are relative to the Yang916-yy/LSSO source tree.
+ */
+#ifndef LSSO_HIP_H_
+#define LSSO_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LSSO_HIP_CONTRACT_VERSION 1
+
+/* Error codes. */
+#define LSSO_HIP_OK 0
+#define LSSO_HIP_EINVAL (-1)      /* invalid shape, pointer or size */
+#define LSSO_HIP_EUNSUPPORTED (-2) /* valid input outside the native contract */
+#define LSSO_HIP_ERUNTIME (-3)    /* a HIP runtime call or launch failed */
+
+/* Element types accepted by the projection entry point. */
+#define LSSO_HIP_F16 1
+#define LSSO_HIP_BF16 2
+
+/* Position metadata layouts for the mixer (reference csrc/ball/common.cuh:245-257). */
+#define LSSO_HIP_POSITIONS_DEFAULT 0 /* p_t = t - (N - 1) / 2, computed on device */
+#define LSSO_HIP_POSITIONS_SHARED 1  /* centered float32 [N]                      */
+#define LSSO_HIP_POSITIONS_BATCHED 2 /* centered float32 [B, N]                   */
+
+/* Geometry of one mixer call.  `projected` is [batch, length, heads*rank +
+ * heads*head_dim] bfloat16, the output is [batch, length, heads*head_dim]
+ * bfloat16 (reference csrc/ball/common.cuh:60-67, FastPathShape). */
+typedef struct lsso_hip_mixer_shape {
+    int64_t batch;
+    int64_t length;
+    int64_t heads;
+    int64_t rank;
+    int64_t head_dim;
+} lsso_hip_mixer_shape;
+
+/* Native contract version of this library.
+ * Replaces: torch.ops.lsso_equilibrium.contract_version
+ * (csrc/ball/binding.cpp:72-74, lsso/ball/cuda.py:28-54). */
+int lsso_hip_contract_version(void);
+
+/* Offload target the library was compiled for ("gfx950").
+ * Replaces: the per-SM artifact name check (lsso/ball/cuda.py:200-208). */
+const char* lsso_hip_target(void);
+
+/* Message of the most recent failure on the calling thread ("" if none).
+ * Replaces: TORCH_CHECK messages (csrc/ball/common.cuh:194-269). */
+const char* lsso_hip_last_error(void);
+
+/* Validate a mixer geometry on the host without touching the GPU.
+ * Replaces: validate_fast_inputs shape checks (csrc/ball/common.cuh:194-269). */
+int lsso_hip_mixer_validate(const lsso_hip_mixer_shape* shape, int positions_mode);
+
+/* Device scratch bytes needed by lsso_hip_mixer_forward for this geometry.
+ * Replaces: the at::empty workspace allocations of launch_generic_forward
+ * (csrc/ball/forward.cu:1227-1449). */
+int lsso_hip_mixer_workspace_bytes(const lsso_hip_mixer_shape* shape,
+                                   int positions_mode, size_t* bytes);
+
+/* Number of float32 values in the per-call training tape (0 if the caller
+ * passes tape == NULL).  The tape holds only compact per-(sample, head)
+ * state; no token-sized frame is stored.
+ * Replaces: training_tape_layout (csrc/ball/common.cuh:84-108). */
+int lsso_hip_mixer_tape_floats(const lsso_hip_mixer_shape* shape, size_t* floats);
+
+/* Complete DYNAMIC + Rank-Rotary mixer forward:
+ *   mixed = eta C + P [2 (I + K)^-1 Z - (1 + eta) Z],  Z = P^T C,
+ * evaluated through P = A L^-T with L L^T = A^T A + I.
+ * inverse_frequency: optional host array of rank/2 float32 rotary
+ * frequencies (NULL: computed as 10000^(-j/(rank/2)) in float32).
+ * valid_counts: optional device float32 [batch] (>= 1) when a mask is used;
+ * masked rows of `projected` must be zero.  tape: optional device buffer of
+ * lsso_hip_mixer_tape_floats() floats that receives the compact state.
+ * Replaces: torch.ops.lsso_equilibrium.forward_inference / forward_train
+ * (csrc/ball/binding.cpp:84-90, csrc/ball/forward.cu:1505-1556,
+ *  lsso/ball/cuda.py:283-323). */
+int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape,
+                           const void* projected,
+                           const float* core_base_raw,
+                           const float* core_drive_weight,
+                           const float* eta_raw,
+                           const float* inverse_frequency,
+                           const float* centered_positions,
+                           int positions_mode,
+                           const float* valid_counts,
+                           void* output,
+                           float* tape,
+                           void* workspace,
+                           size_t workspace_bytes,
+                           void* stream);
+
+/* Device scratch bytes needed by lsso_hip_linear. */
+int lsso_hip_linear_workspace_bytes(int64_t rows, int64_t in_features,
+                                    int64_t out_features, size_t* bytes);
+
+/* Biased projection y = cast(bf16(x) bf16(W)^T + b): BF16 multiplicands,
+ * FP32 accumulation, FP32 bias added before one final FP16/BF16 store.
+ * x: [rows, in_features] with row stride x_row_stride elements (unit column
+ * stride), dtype x_dtype.  weight: float32 [out_features, in_features]
+ * contiguous.  bias: float32 [out_features] or NULL.  row_mask: optional
+ * device uint8 [rows]; rows whose byte is 0 are not read and are written as
+ * zeros (the masked-token contract of the reference's native forward,
+ * lsso/ball/model.py:371-383, 402-404).  y: contiguous [rows, out_features]
+ * of dtype y_dtype.
+ * Replaces: tensor_core_linear / _biased_gemm (lsso/ball/reference.py:20-75,
+ * 78-97, 347-408). */
+int lsso_hip_linear(const void* x, int x_dtype, int64_t rows,
+                    int64_t in_features, int64_t x_row_stride,
+                    const float* weight, const float* bias,
+                    const uint8_t* row_mask, int64_t out_features,
+                    void* y, int y_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LSSO_HIP_H_ */

@@ -1,0 +1,537 @@
+"""Strict loader and PyTorch boundary of the gfx950 native library.
+
+Mirrors the reference's native boundary ``lsso.ball.cuda``
+(lsso/ball/cuda.py:57-326): an explicit ``load()``, ``is_available()``,
+``require_available()`` and ``fast_mix()`` with train/inference selection,
+plus the biased projection that replaces the reference's Triton GEMM
+(lsso/ball/reference.py:20-75).  The library is the C ABI declared in
+``include/lsso_hip.h``; PyTorch only supplies device memory and the current
+stream.  There is no fallback: every entry point raises when the library is
+not loaded or an input is outside the native contract.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from threading import Lock
+
+import torch
+
+from .reference import rotary_inverse_frequency
+
+_LOAD_LOCK = Lock()
+_NATIVE_CONTRACT_VERSION = 1
+_SUPPORTED_ARCHITECTURES = frozenset(("gfx950",))
+_LOADED_ARCHITECTURE: str | None = None
+_LIBRARY: ctypes.CDLL | None = None
+_INVERSE_FREQUENCY: dict[int, ctypes.Array] = {}
+
+_F16 = 1
+_BF16 = 2
+_POSITIONS_DEFAULT = 0
+_POSITIONS_SHARED = 1
+_POSITIONS_BATCHED = 2
+
+_SYMBOLS = (
+    "lsso_hip_contract_version",
+    "lsso_hip_target",
+    "lsso_hip_last_error",
+    "lsso_hip_mixer_validate",
+    "lsso_hip_mixer_workspace_bytes",
+    "lsso_hip_mixer_tape_floats",
+    "lsso_hip_mixer_forward",
+    "lsso_hip_linear_workspace_bytes",
+    "lsso_hip_linear",
+)
+
+
+class MixerShape(ctypes.Structure):
+    """``lsso_hip_mixer_shape`` (include/lsso_hip.h)."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("length", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("rank", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+    ]
+
+
+def _declare(library: ctypes.CDLL) -> None:
+    vp = ctypes.c_void_p
+    i64 = ctypes.c_int64
+    shape_p = ctypes.POINTER(MixerShape)
+    size_p = ctypes.POINTER(ctypes.c_size_t)
+    library.lsso_hip_contract_version.restype = ctypes.c_int
+    library.lsso_hip_contract_version.argtypes = []
+    library.lsso_hip_target.restype = ctypes.c_char_p
+    library.lsso_hip_target.argtypes = []
+    library.lsso_hip_last_error.restype = ctypes.c_char_p
+    library.lsso_hip_last_error.argtypes = []
+    library.lsso_hip_mixer_validate.restype = ctypes.c_int
+    library.lsso_hip_mixer_validate.argtypes = [shape_p, ctypes.c_int]
+    library.lsso_hip_mixer_workspace_bytes.restype = ctypes.c_int
+    library.lsso_hip_mixer_workspace_bytes.argtypes = [shape_p, ctypes.c_int, size_p]
+    library.lsso_hip_mixer_tape_floats.restype = ctypes.c_int
+    library.lsso_hip_mixer_tape_floats.argtypes = [shape_p, size_p]
+    library.lsso_hip_mixer_forward.restype = ctypes.c_int
+    library.lsso_hip_mixer_forward.argtypes = [
+        shape_p, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp, ctypes.c_size_t, vp,
+    ]
+    library.lsso_hip_linear_workspace_bytes.restype = ctypes.c_int
+    library.lsso_hip_linear_workspace_bytes.argtypes = [i64, i64, i64, size_p]
+    library.lsso_hip_linear.restype = ctypes.c_int
+    library.lsso_hip_linear.argtypes = [
+        vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, i64, vp, ctypes.c_int, vp, ctypes.c_size_t, vp,
+    ]  # x, x_dtype, rows, in, stride, weight, bias, row_mask, out, y, y_dtype, ws, ws_bytes, stream
+
+
+def default_library_path() -> Path:
+    """``LSSO_HIP_LIBRARY`` or the in-tree build (reference cuda.py:165-175)."""
+
+    override = os.environ.get("LSSO_HIP_LIBRARY")
+    if override:
+        return Path(override).expanduser()
+    return Path(__file__).resolve().parents[1] / "_lib" / "liblsso_hip_gfx950.so"
+
+
+def open_library(path: str | os.PathLike[str] | None = None) -> ctypes.CDLL:
+    """dlopen the library and declare its C ABI without touching a GPU.
+
+    PyTorch is imported first so that the HIP runtime it carries (same
+    SONAME) serves the library as well.
+    """
+
+    library_path = Path(path) if path is not None else default_library_path()
+    if not library_path.is_file():
+        raise RuntimeError(
+            f"the LSSO HIP library was not found at {library_path}; build it with "
+            "`python -m lsso_amd.build` or pass its path to load()"
+        )
+    library = ctypes.CDLL(str(library_path.resolve()))
+    _declare(library)
+    return library
+
+
+def _native_contract_version(library: ctypes.CDLL | None) -> int | None:
+    if library is None:
+        return None
+    return int(library.lsso_hip_contract_version())
+
+
+def is_available() -> bool:
+    """Whether the strict DYNAMIC + Rank-Rotary library is loaded (cuda.py:57-63)."""
+
+    return _LIBRARY is not None and _native_contract_version(_LIBRARY) == _NATIVE_CONTRACT_VERSION
+
+
+def require_available() -> None:
+    """Reject a native request until the library is loaded (cuda.py:66-80)."""
+
+    if _LOADED_ARCHITECTURE is not None:
+        return
+    with _LOAD_LOCK:
+        if _LOADED_ARCHITECTURE is not None:
+            return
+        raise RuntimeError(
+            "the LSSO accretive-equilibrium HIP extension is not loaded; build it with "
+            "`python -m lsso_amd.build`, then call lsso_amd.ball.hip.load(); "
+            f"native contract version {_NATIVE_CONTRACT_VERSION} is required"
+        )
+
+
+def _device_architecture(device: torch.device | int | None = None) -> str:
+    """gfx target of the requested device (cuda.py:83-110)."""
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("the LSSO HIP fast path requires an available ROCm device")
+    if device is None:
+        resolved = torch.device("cuda", torch.cuda.current_device())
+    elif isinstance(device, int):
+        resolved = torch.device("cuda", device)
+    else:
+        resolved = torch.device(device)
+    if resolved.type != "cuda":
+        raise ValueError(f"the LSSO HIP fast path requires a ROCm device, got {resolved}")
+    if resolved.index is None:
+        resolved = torch.device("cuda", torch.cuda.current_device())
+    name = str(getattr(torch.cuda.get_device_properties(resolved), "gcnArchName", ""))
+    architecture = name.split(":")[0]
+    if architecture not in _SUPPORTED_ARCHITECTURES:
+        raise RuntimeError(
+            f"the LSSO HIP fast path supports gfx950 (MI355X); got {architecture or 'unknown'}"
+        )
+    return architecture
+
+
+def load(path: str | os.PathLike[str] | None = None, *, device: torch.device | int | None = None) -> None:
+    """Load the one strict gfx950 library for this process (cuda.py:178-217)."""
+
+    global _LIBRARY, _LOADED_ARCHITECTURE
+    requested = _device_architecture(device)
+    with _LOAD_LOCK:
+        if _LIBRARY is not None:
+            if _LOADED_ARCHITECTURE is not None and _LOADED_ARCHITECTURE != requested:
+                raise RuntimeError(
+                    f"the loaded LSSO HIP library targets {_LOADED_ARCHITECTURE}, "
+                    f"not requested {requested}"
+                )
+            return
+        library_path = Path(path) if path is not None else default_library_path()
+        expected = f"liblsso_hip_{requested}.so"
+        if library_path.name != expected:
+            raise RuntimeError(
+                f"the strict LSSO HIP fast path requires {expected} for {requested}, "
+                f"got {library_path.name}"
+            )
+        library = open_library(library_path)
+        version = _native_contract_version(library)
+        if version != _NATIVE_CONTRACT_VERSION:
+            raise RuntimeError(
+                f"the LSSO HIP library has native contract version {version}, but this "
+                f"package requires {_NATIVE_CONTRACT_VERSION}; rebuild it with "
+                "`python -m lsso_amd.build` and restart the process"
+            )
+        target = library.lsso_hip_target().decode()
+        if target != requested:
+            raise RuntimeError(f"the LSSO HIP library targets {target}, not requested {requested}")
+        _LIBRARY = library
+        _LOADED_ARCHITECTURE = requested
+
+
+def _library() -> ctypes.CDLL:
+    require_available()
+    assert _LIBRARY is not None
+    return _LIBRARY
+
+
+def _check(status: int, library: ctypes.CDLL) -> None:
+    if status != 0:
+        message = library.lsso_hip_last_error().decode()
+        if status == -2:
+            raise ValueError(message)
+        raise RuntimeError(message)
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _inverse_frequency(rank: int) -> ctypes.Array:
+    """Host FP32 frequencies computed exactly as the reference does (reference.py:704-707)."""
+
+    cached = _INVERSE_FREQUENCY.get(rank)
+    if cached is None:
+        values = rotary_inverse_frequency(rank, torch.float32).tolist()
+        cached = (ctypes.c_float * len(values))(*values)
+        _INVERSE_FREQUENCY[rank] = cached
+    return cached
+
+
+def _require_device_tensor(value: torch.Tensor, name: str, device: torch.device) -> None:
+    if value.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a CUDA (ROCm device) tensor")
+    if value.device != device:
+        raise RuntimeError(f"{name} must share projected.device() (got {value.device} vs {device})")
+
+
+def _validate_mixer(
+    projected: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None,
+    valid_counts: torch.Tensor | None,
+) -> tuple[MixerShape, int]:
+    """Tensor-level checks of the native contract (csrc/ball/common.cuh:194-269)."""
+
+    if projected.device.type != "cuda":
+        raise RuntimeError("projected must be a CUDA (ROCm device) tensor")
+    if projected.dim() != 3:
+        raise RuntimeError(f"projected must have shape [B, N, H*R + D], got {tuple(projected.shape)}")
+    if not projected.is_contiguous():
+        raise RuntimeError("projected must be contiguous [B, N, H*R + D]")
+    if projected.dtype != torch.bfloat16:
+        raise RuntimeError(
+            "projected must use bfloat16 under the mixed precision HIP contract, "
+            f"got {projected.dtype}"
+        )
+    device = projected.device
+    for name, value in (
+        ("core_base_raw", core_base_raw),
+        ("core_drive_weight", core_drive_weight),
+        ("eta_raw", eta_raw),
+    ):
+        if not value.is_contiguous():
+            raise RuntimeError(f"{name} must be contiguous")
+        _require_device_tensor(value, name, device)
+        if value.dtype != torch.float32:
+            raise RuntimeError(f"{name} must use float32")
+    if core_base_raw.dim() != 3 or core_base_raw.shape[1] != core_base_raw.shape[2]:
+        raise RuntimeError(f"core_base_raw must have shape [H, R, R], got {tuple(core_base_raw.shape)}")
+    batch, length, width = projected.shape
+    heads, rank = core_base_raw.shape[0], core_base_raw.shape[1]
+    if batch <= 0 or length <= 0 or heads <= 0:
+        raise RuntimeError("B, N, and H must be positive")
+    if rank not in (16, 32, 48, 64):
+        raise RuntimeError(f"the HIP fast path supports rank in {{16, 32, 48, 64}}, got {rank}")
+    if width <= heads * rank:
+        raise RuntimeError("projected width must exceed H*R for a nonempty content channel")
+    dim = width - heads * rank
+    if dim % heads:
+        raise RuntimeError("projected content width D must be divisible by H")
+    head_dim = dim // heads
+    if tuple(core_drive_weight.shape) != (heads, head_dim, rank):
+        raise RuntimeError(
+            f"core_drive_weight must have shape [H, D/H, R], got {tuple(core_drive_weight.shape)}"
+        )
+    if tuple(eta_raw.shape) != (heads,):
+        raise RuntimeError(f"eta_raw must have shape [H], got {tuple(eta_raw.shape)}")
+    mode = _POSITIONS_DEFAULT
+    if centered_positions is not None:
+        _require_device_tensor(centered_positions, "centered_positions", device)
+        if not centered_positions.is_contiguous():
+            raise RuntimeError("centered_positions must be contiguous")
+        if centered_positions.dtype != torch.float32:
+            raise RuntimeError("centered_positions must use float32")
+        if centered_positions.dim() == 1 and centered_positions.shape[0] == length:
+            mode = _POSITIONS_SHARED
+        elif centered_positions.dim() == 2 and tuple(centered_positions.shape) == (batch, length):
+            mode = _POSITIONS_BATCHED
+        else:
+            raise RuntimeError(
+                f"centered_positions must have shape [N] or [B, N], got {tuple(centered_positions.shape)}"
+            )
+    if valid_counts is not None:
+        _require_device_tensor(valid_counts, "valid_counts", device)
+        if not valid_counts.is_contiguous():
+            raise RuntimeError("valid_counts must be contiguous")
+        if valid_counts.dtype != torch.float32:
+            raise RuntimeError("valid_counts must use float32")
+        if valid_counts.dim() != 1 or valid_counts.shape[0] != batch:
+            raise RuntimeError(f"valid_counts must have shape [B], got {tuple(valid_counts.shape)}")
+    return MixerShape(batch, length, heads, rank, head_dim), mode
+
+
+def _mixer_forward(
+    projected: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None,
+    valid_counts: torch.Tensor | None,
+    record_tape: bool,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    library = _library()
+    shape, mode = _validate_mixer(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+    )
+    device = projected.device
+    workspace_bytes = ctypes.c_size_t()
+    _check(library.lsso_hip_mixer_workspace_bytes(ctypes.byref(shape), mode, ctypes.byref(workspace_bytes)), library)
+    output = torch.empty(
+        (shape.batch, shape.length, shape.heads * shape.head_dim), dtype=torch.bfloat16, device=device
+    )
+    workspace = torch.empty(workspace_bytes.value, dtype=torch.uint8, device=device)
+    tape = None
+    if record_tape:
+        floats = ctypes.c_size_t()
+        _check(library.lsso_hip_mixer_tape_floats(ctypes.byref(shape), ctypes.byref(floats)), library)
+        tape = torch.empty(floats.value, dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        status = library.lsso_hip_mixer_forward(
+            ctypes.byref(shape),
+            projected.data_ptr(),
+            core_base_raw.data_ptr(),
+            core_drive_weight.data_ptr(),
+            eta_raw.data_ptr(),
+            ctypes.cast(_inverse_frequency(shape.rank), ctypes.c_void_p),
+            None if centered_positions is None else centered_positions.data_ptr(),
+            mode,
+            None if valid_counts is None else valid_counts.data_ptr(),
+            output.data_ptr(),
+            None if tape is None else tape.data_ptr(),
+            workspace.data_ptr(),
+            workspace_bytes.value,
+            _stream(device),
+        )
+    _check(status, library)
+    return output, tape
+
+
+def _any_requires_grad(*values: torch.Tensor | None) -> bool:
+    return any(value is not None and value.requires_grad for value in values)
+
+
+def forward_inference(
+    projected: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None = None,
+    valid_counts: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Inference-only native mixer (csrc/ball/binding.cpp:16-42)."""
+
+    if torch.is_grad_enabled() and _any_requires_grad(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+    ):
+        raise RuntimeError(
+            "lsso_hip forward_inference is an inference-only entry point and cannot "
+            "participate in autograd directly; use lsso_amd.ball.hip.fast_mix()"
+        )
+    output, _tape = _mixer_forward(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts, False
+    )
+    return output
+
+
+def forward_train(
+    projected: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None = None,
+    valid_counts: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Tape-producing native mixer (csrc/ball/binding.cpp:44-70)."""
+
+    if torch.is_grad_enabled() and _any_requires_grad(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+    ):
+        raise RuntimeError(
+            "lsso_hip forward_train is a private tape-producing entry point and cannot "
+            "participate in autograd directly; use lsso_amd.ball.hip.fast_mix()"
+        )
+    output, tape = _mixer_forward(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts, True
+    )
+    assert tape is not None
+    return output, tape
+
+
+class _FastMix(torch.autograd.Function):
+    """First-order autograd boundary of the native mixer (cuda.py:220-280)."""
+
+    @staticmethod
+    def forward(ctx, projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts):
+        with torch.no_grad():
+            output, tape = forward_train(
+                projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+            )
+        ctx.save_for_backward(projected, core_base_raw, core_drive_weight, eta_raw, tape)
+        return output
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_output):
+        raise NotImplementedError(
+            "the native LSSO HIP mixer backward is not built yet; train with "
+            "implementation='reference'"
+        )
+
+
+def fast_mix(
+    projected: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None = None,
+    valid_counts: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Run the strict native mixer, selecting the inference or training entry
+    from autograd state (cuda.py:283-323)."""
+
+    if centered_positions is not None and centered_positions.requires_grad:
+        raise ValueError(
+            "the LSSO HIP fast path does not support gradients for centered_positions"
+        )
+    if valid_counts is not None and valid_counts.requires_grad:
+        raise ValueError("the LSSO HIP fast path does not support gradients for valid_counts")
+    require_available()
+    if not torch.is_grad_enabled() or not _any_requires_grad(
+        projected, core_base_raw, core_drive_weight, eta_raw
+    ):
+        return forward_inference(
+            projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+        )
+    return _FastMix.apply(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+    )
+
+
+def linear(
+    value: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    output_dtype: torch.dtype,
+    row_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Native biased projection cast(bf16(x) bf16(W)^T + b) (reference.py:20-75, 347-408).
+
+    value: [..., K] float16/bfloat16 with unit feature stride; weight: float32
+    [N, K]; bias: float32 [N] or None; output: contiguous [..., N].
+    ``row_mask`` (bool, value.shape[:-1]) zeroes the output rows it excludes.
+    """
+
+    library = _library()
+    if value.device.type != "cuda":
+        raise RuntimeError("value must be a CUDA (ROCm device) tensor")
+    dtype_codes = {torch.float16: _F16, torch.bfloat16: _BF16}
+    if value.dtype not in dtype_codes or output_dtype not in dtype_codes:
+        raise TypeError("the HIP projection supports float16/bfloat16 activations and outputs")
+    if weight.dtype != torch.float32 or weight.dim() != 2:
+        raise TypeError("the HIP projection requires a float32 [out, in] weight")
+    if bias is not None and (bias.dtype != torch.float32 or tuple(bias.shape) != (weight.shape[0],)):
+        raise TypeError("the HIP projection requires a float32 [out] bias")
+    weight = weight.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    in_features = value.shape[-1]
+    if weight.shape[1] != in_features:
+        raise ValueError(
+            f"projection input and weight features must agree, got {in_features} and {weight.shape[1]}"
+        )
+    flat = value.reshape(-1, in_features)
+    if flat.stride(-1) != 1:
+        flat = flat.contiguous()
+    rows = flat.shape[0]
+    out_features = weight.shape[0]
+    output = torch.empty(value.shape[:-1] + (out_features,), dtype=output_dtype, device=value.device)
+    mask_ptr = None
+    if row_mask is not None:
+        if row_mask.dtype != torch.bool or tuple(row_mask.shape) != tuple(value.shape[:-1]):
+            raise ValueError("row_mask must be a bool tensor shaped like the leading dimensions")
+        row_mask = row_mask.contiguous()
+        mask_ptr = row_mask.data_ptr()
+    with torch.cuda.device(value.device):
+        status = library.lsso_hip_linear(
+            flat.data_ptr(),
+            dtype_codes[value.dtype],
+            rows,
+            in_features,
+            flat.stride(0) if rows > 0 else in_features,
+            weight.data_ptr(),
+            None if bias is None else bias.data_ptr(),
+            mask_ptr,
+            out_features,
+            output.data_ptr(),
+            dtype_codes[output_dtype],
+            None,
+            0,
+            _stream(value.device),
+        )
+    _check(status, library)
+    return output
+
+
+__all__ = [
+    "fast_mix",
+    "forward_inference",
+    "forward_train",
+    "is_available",
+    "linear",
+    "load",
+    "require_available",
+]

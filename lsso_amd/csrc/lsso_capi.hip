@@ -1,0 +1,359 @@
+// C ABI of the gfx950 LSSO library: host-side validation, workspace
+// planning and stream-ordered launches.  Nothing here allocates device
+// memory or synchronizes the host.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+#include "lsso_hip.h"
+#include "lsso_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message) {
+    g_last_error = message;
+    return code;
+}
+
+int hip_failure(hipError_t error, const char* where) {
+    return fail(LSSO_HIP_ERUNTIME,
+                std::string(where) + " failed: " + hipGetErrorString(error));
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+size_t align_up(size_t value) { return (value + 255) & ~static_cast<size_t>(255); }
+
+constexpr int64_t kReduceTargetWaves = 2048;
+constexpr int64_t kApplyTargetWaves = 4096;
+
+struct MixerPlan {
+    int64_t batch, length, heads, rank, head_dim;
+    int64_t width, out_width, pairs, phase_batches;
+    int cpw;
+    int64_t column_groups, reduce_chunks, reduce_chunk_tokens;
+    int nfbw;
+    int64_t feature_blocks, block_groups, apply_chunks, apply_chunk_tokens;
+    int64_t partial_stride, tape_stride;
+    size_t off_phases, off_partials, off_zbuf, off_mop, total;
+};
+
+void plan_chunks(int64_t length, int64_t waves_per_chunk, int64_t target_waves,
+                 int64_t granularity, int64_t* chunks, int64_t* chunk_tokens) {
+    const int64_t max_chunks = ceil_div(length, granularity);
+    int64_t wanted = ceil_div(target_waves, waves_per_chunk);
+    if (wanted < 1) wanted = 1;
+    if (wanted > max_chunks) wanted = max_chunks;
+    const int64_t tokens = ceil_div(ceil_div(length, wanted), granularity) * granularity;
+    *chunk_tokens = tokens;
+    *chunks = ceil_div(length, tokens);
+}
+
+int make_plan(const lsso_hip_mixer_shape* shape, int positions_mode, MixerPlan* p) {
+    if (shape == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "shape must not be NULL");
+    }
+    p->batch = shape->batch;
+    p->length = shape->length;
+    p->heads = shape->heads;
+    p->rank = shape->rank;
+    p->head_dim = shape->head_dim;
+    if (p->batch <= 0 || p->length <= 0 || p->heads <= 0) {
+        return fail(LSSO_HIP_EINVAL, "B, N, and H must be positive");
+    }
+    if (p->rank != 16 && p->rank != 32 && p->rank != 48 && p->rank != 64) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "the HIP fast path supports rank in {16, 32, 48, 64}, got " +
+                        std::to_string(p->rank));
+    }
+    if (p->head_dim <= 0) {
+        return fail(LSSO_HIP_EINVAL,
+                    "projected width must exceed H*R for a nonempty content channel");
+    }
+    if (positions_mode != LSSO_HIP_POSITIONS_DEFAULT &&
+        positions_mode != LSSO_HIP_POSITIONS_SHARED &&
+        positions_mode != LSSO_HIP_POSITIONS_BATCHED) {
+        return fail(LSSO_HIP_EINVAL, "positions_mode must be 0 (default), 1 ([N]) or 2 ([B, N])");
+    }
+    p->width = p->heads * (p->rank + p->head_dim);
+    p->out_width = p->heads * p->head_dim;
+    p->pairs = p->rank / 2;
+    p->phase_batches = positions_mode == LSSO_HIP_POSITIONS_BATCHED ? p->batch : 1;
+
+    p->cpw = p->head_dim > 32 ? 2 : 1;
+    p->column_groups = ceil_div(p->head_dim, 32 * p->cpw);
+    plan_chunks(p->length, p->batch * p->heads * p->column_groups, kReduceTargetWaves, 32,
+                &p->reduce_chunks, &p->reduce_chunk_tokens);
+
+    p->feature_blocks = ceil_div(p->head_dim, 16);
+    p->nfbw = p->feature_blocks >= 4 ? 4 : (p->feature_blocks == 3 ? 4 : static_cast<int>(p->feature_blocks));
+    p->block_groups = ceil_div(p->feature_blocks, p->nfbw);
+    plan_chunks(p->length, p->batch * p->heads * p->block_groups, kApplyTargetWaves, 16,
+                &p->apply_chunks, &p->apply_chunk_tokens);
+
+    p->partial_stride = p->rank * p->rank + p->rank * p->head_dim;
+    p->tape_stride = 3 * p->rank * p->rank + p->rank + 2 * p->rank * p->head_dim;
+
+    const int64_t systems = p->batch * p->heads;
+    size_t offset = 0;
+    p->off_phases = offset;
+    offset = align_up(offset + sizeof(uint32_t) * p->phase_batches * p->length * p->pairs);
+    p->off_partials = offset;
+    offset = align_up(offset + sizeof(float) * systems * p->reduce_chunks * p->partial_stride);
+    p->off_zbuf = offset;
+    offset = align_up(offset + sizeof(float) * systems * p->rank * p->head_dim);
+    p->off_mop = offset;
+    offset = align_up(offset + sizeof(uint16_t) * systems * p->feature_blocks * 64 * (p->rank / 2));
+    p->total = offset;
+    return LSSO_HIP_OK;
+}
+
+bool aligned(const void* pointer, uintptr_t bytes) {
+    return (reinterpret_cast<uintptr_t>(pointer) % bytes) == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lsso_hip_contract_version(void) { return LSSO_HIP_CONTRACT_VERSION; }
+
+const char* lsso_hip_target(void) { return "gfx950"; }
+
+const char* lsso_hip_last_error(void) { return g_last_error.c_str(); }
+
+int lsso_hip_mixer_validate(const lsso_hip_mixer_shape* shape, int positions_mode) {
+    MixerPlan plan;
+    return make_plan(shape, positions_mode, &plan);
+}
+
+int lsso_hip_mixer_workspace_bytes(const lsso_hip_mixer_shape* shape, int positions_mode,
+                                   size_t* bytes) {
+    if (bytes == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "bytes must not be NULL");
+    }
+    MixerPlan plan;
+    const int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    *bytes = plan.total;
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_mixer_tape_floats(const lsso_hip_mixer_shape* shape, size_t* floats) {
+    if (floats == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "floats must not be NULL");
+    }
+    MixerPlan plan;
+    const int status = make_plan(shape, LSSO_HIP_POSITIONS_DEFAULT, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    *floats = static_cast<size_t>(plan.batch * plan.heads * plan.tape_stride);
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projected,
+                           const float* core_base_raw, const float* core_drive_weight,
+                           const float* eta_raw, const float* inverse_frequency,
+                           const float* centered_positions, int positions_mode,
+                           const float* valid_counts, void* output, float* tape,
+                           void* workspace, size_t workspace_bytes, void* stream_handle) {
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    if (projected == nullptr || core_base_raw == nullptr || core_drive_weight == nullptr ||
+        eta_raw == nullptr || output == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "projected, parameters and output must not be NULL");
+    }
+    if (positions_mode != LSSO_HIP_POSITIONS_DEFAULT && centered_positions == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "centered_positions must not be NULL for this positions_mode");
+    }
+    if (workspace == nullptr || workspace_bytes < plan.total) {
+        return fail(LSSO_HIP_EINVAL, "workspace is smaller than lsso_hip_mixer_workspace_bytes()");
+    }
+    if (!aligned(workspace, 256)) {
+        return fail(LSSO_HIP_EINVAL, "workspace must be 256-byte aligned");
+    }
+    if (!aligned(projected, 2) || !aligned(output, 2)) {
+        return fail(LSSO_HIP_EINVAL, "projected and output must be 2-byte aligned bfloat16 buffers");
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    char* ws = static_cast<char*>(workspace);
+    uint32_t* phases = reinterpret_cast<uint32_t*>(ws + plan.off_phases);
+    float* partials = reinterpret_cast<float*>(ws + plan.off_partials);
+    float* zbuf = reinterpret_cast<float*>(ws + plan.off_zbuf);
+    uint16_t* mop = reinterpret_cast<uint16_t*>(ws + plan.off_mop);
+
+    lsso_hip::PhaseArgs phase{};
+    phase.positions = positions_mode == LSSO_HIP_POSITIONS_DEFAULT ? nullptr : centered_positions;
+    phase.phases = phases;
+    phase.count = plan.phase_batches * plan.length * plan.pairs;
+    phase.length = plan.length;
+    phase.pairs = static_cast<int>(plan.pairs);
+    for (int j = 0; j < plan.pairs; ++j) {
+        phase.inverse_frequency[j] = inverse_frequency != nullptr
+            ? inverse_frequency[j]
+            : std::pow(10000.0f, -static_cast<float>(j) / static_cast<float>(plan.pairs));
+    }
+    hipError_t error = lsso_hip::launch_phase(phase, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "phase_kernel launch");
+    }
+
+    const bool vec = plan.width % 8 == 0 && plan.head_dim % 4 == 0 && aligned(projected, 16) &&
+                     aligned(output, 16);
+    const int64_t phase_stride =
+        positions_mode == LSSO_HIP_POSITIONS_BATCHED ? plan.length * plan.pairs : 0;
+
+    lsso_hip::ReduceArgs reduce{};
+    reduce.projected = static_cast<const uint16_t*>(projected);
+    reduce.phases = phases;
+    reduce.partials = partials;
+    reduce.batch = plan.batch;
+    reduce.length = plan.length;
+    reduce.heads = plan.heads;
+    reduce.head_dim = plan.head_dim;
+    reduce.width = plan.width;
+    reduce.phase_batch_stride = phase_stride;
+    reduce.chunks = plan.reduce_chunks;
+    reduce.chunk_tokens = plan.reduce_chunk_tokens;
+    reduce.column_groups = plan.column_groups;
+    reduce.partial_stride = plan.partial_stride;
+    reduce.total_waves = plan.batch * plan.heads * plan.reduce_chunks * plan.column_groups;
+    error = lsso_hip::launch_reduce(static_cast<int>(plan.rank), reduce, plan.cpw, vec, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "reduce_kernel launch");
+    }
+
+    lsso_hip::SolveArgs solve{};
+    solve.partials = partials;
+    solve.chunks = plan.reduce_chunks;
+    solve.partial_stride = plan.partial_stride;
+    solve.batch = plan.batch;
+    solve.length = plan.length;
+    solve.heads = plan.heads;
+    solve.head_dim = plan.head_dim;
+    solve.base = core_base_raw;
+    solve.drive = core_drive_weight;
+    solve.eta_raw = eta_raw;
+    solve.valid_counts = valid_counts;
+    solve.zbuf = zbuf;
+    solve.mop = mop;
+    solve.tape = tape;
+    solve.tape_stride = plan.tape_stride;
+    error = lsso_hip::launch_solve(static_cast<int>(plan.rank), solve, plan.batch * plan.heads,
+                                   stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "solve_kernel launch");
+    }
+
+    lsso_hip::ApplyArgs apply{};
+    apply.projected = static_cast<const uint16_t*>(projected);
+    apply.phases = phases;
+    apply.mop = mop;
+    apply.eta_raw = eta_raw;
+    apply.output = static_cast<uint16_t*>(output);
+    apply.batch = plan.batch;
+    apply.length = plan.length;
+    apply.heads = plan.heads;
+    apply.head_dim = plan.head_dim;
+    apply.width = plan.width;
+    apply.out_width = plan.out_width;
+    apply.phase_batch_stride = phase_stride;
+    apply.chunks = plan.apply_chunks;
+    apply.chunk_tokens = plan.apply_chunk_tokens;
+    apply.feature_blocks = plan.feature_blocks;
+    apply.block_groups = plan.block_groups;
+    apply.total_waves = plan.batch * plan.heads * plan.apply_chunks * plan.block_groups;
+    error = lsso_hip::launch_apply(static_cast<int>(plan.rank), apply, plan.nfbw, vec, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "apply_kernel launch");
+    }
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_linear_workspace_bytes(int64_t rows, int64_t in_features, int64_t out_features,
+                                    size_t* bytes) {
+    if (bytes == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "bytes must not be NULL");
+    }
+    if (rows < 0 || in_features <= 0 || out_features <= 0) {
+        return fail(LSSO_HIP_EINVAL, "rows must be >= 0 and features must be positive");
+    }
+    *bytes = 0;
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_linear(const void* x, int x_dtype, int64_t rows, int64_t in_features,
+                    int64_t x_row_stride, const float* weight, const float* bias,
+                    const uint8_t* row_mask, int64_t out_features, void* y, int y_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream_handle) {
+    (void)workspace;
+    (void)workspace_bytes;
+    if (rows < 0 || in_features <= 0 || out_features <= 0) {
+        return fail(LSSO_HIP_EINVAL, "rows must be >= 0 and features must be positive");
+    }
+    if ((x_dtype != LSSO_HIP_F16 && x_dtype != LSSO_HIP_BF16) ||
+        (y_dtype != LSSO_HIP_F16 && y_dtype != LSSO_HIP_BF16)) {
+        return fail(LSSO_HIP_EUNSUPPORTED, "projection dtypes must be float16 or bfloat16");
+    }
+    if (x_row_stride < in_features) {
+        return fail(LSSO_HIP_EINVAL, "x_row_stride must be >= in_features");
+    }
+    const int tier = lsso_hip::linear_k_tier(in_features);
+    if (tier == 0) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "the HIP projection supports in_features <= 512, got " +
+                        std::to_string(in_features));
+    }
+    if (rows == 0) {
+        return LSSO_HIP_OK;
+    }
+    if (x == nullptr || weight == nullptr || y == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "x, weight and y must not be NULL");
+    }
+    int device = 0;
+    hipError_t error = hipGetDevice(&device);
+    if (error != hipSuccess) {
+        return hip_failure(error, "hipGetDevice");
+    }
+    int units = 0;
+    error = hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device);
+    if (error != hipSuccess) {
+        return hip_failure(error, "hipDeviceGetAttribute");
+    }
+    lsso_hip::LinearArgs args{};
+    args.x = x;
+    args.rows = rows;
+    args.in_features = in_features;
+    args.x_stride = x_row_stride;
+    args.weight = weight;
+    args.bias = bias;
+    args.row_mask = row_mask;
+    args.out_features = out_features;
+    args.y = y;
+    args.tiles = ceil_div(rows, lsso_hip::linear_tile_rows());
+    args.column_groups = ceil_div(out_features, lsso_hip::linear_columns_per_group(tier));
+    args.x_vector = (in_features % 8 == 0 && x_row_stride % 8 == 0 && aligned(x, 16)) ? 1 : 0;
+    args.y_vector = (out_features % 4 == 0 && aligned(y, 8)) ? 1 : 0;
+    int64_t groups = units / args.column_groups;
+    if (groups < 1) groups = 1;
+    if (groups > args.tiles) groups = args.tiles;
+    error = lsso_hip::launch_linear(args, tier, x_dtype, y_dtype, static_cast<int>(groups), stream_handle
+                                        ? static_cast<hipStream_t>(stream_handle)
+                                        : nullptr);
+    if (error != hipSuccess) {
+        return hip_failure(error, "linear_kernel launch");
+    }
+    return LSSO_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+// Device-side helpers shared by the gfx950 LSSO kernels: bit-exact BF16/FP16
+// conversions, MFMA operand types and the bounded complement.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace lsso_hip {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 1 - 2^-23: the one-ULP interior scale of the complement
+// (reference lsso/ball/reference.py:464, csrc/ball/common.cuh:23).
+constexpr float kInteriorScale = 1.0f - 0x1.0p-23f;
+// log(e - 1), rounded to float32 as torch adds the Python double to a
+// float32 tensor (reference lsso/ball/reference.py:13, 493).
+constexpr float kSoftplusOneOffset = 0.541324854612918f;
+
+__device__ __forceinline__ float bf16_lo(uint32_t packed) {
+    return __uint_as_float(packed << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t packed) {
+    return __uint_as_float(packed & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_bits_to_float(uint16_t bits) {
+    return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+__device__ __forceinline__ float f16_lo(uint32_t packed) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(packed & 0xffffu)));
+}
+__device__ __forceinline__ float f16_hi(uint32_t packed) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(packed >> 16)));
+}
+__device__ __forceinline__ float f16_bits_to_float(uint16_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
+// Round two floats to BF16 (round to nearest even, v_cvt_pk_bf16_f32) and
+// pack them, first value in the low half.
+__device__ __forceinline__ uint32_t pack_bf16(float low, float high) {
+    const bf16x2 value = __builtin_convertvector((f32x2){low, high}, bf16x2);
+    return __builtin_bit_cast(uint32_t, value);
+}
+__device__ __forceinline__ uint16_t to_bf16_bits(float value) {
+    return static_cast<uint16_t>(pack_bf16(value, 0.0f) & 0xffffu);
+}
+__device__ __forceinline__ uint16_t to_f16_bits(float value) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(value));
+}
+__device__ __forceinline__ uint32_t pack_f16(float low, float high) {
+    return static_cast<uint32_t>(to_f16_bits(low)) |
+           (static_cast<uint32_t>(to_f16_bits(high)) << 16);
+}
+
+// Split two floats into BF16 high parts and BF16 residuals so that
+// hi + lo carries ~16 mantissa bits; products of split operands accumulated
+// as hi*hi + hi*lo + lo*hi reproduce FP32 products to ~2^-17 relative.
+__device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hi, uint32_t& lo) {
+    hi = pack_bf16(a, b);
+    lo = pack_bf16(a - bf16_lo(hi), b - bf16_hi(hi));
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x16(const u32x2& a, const u32x2& b, const f32x4& c) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+        __builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// eta = (1 - 2^-23) tanh(raw) through the sign-split logistic identity
+// (reference lsso/ball/reference.py:450-471).
+__device__ __forceinline__ float bounded_complement(float raw) {
+    const bool positive = raw >= 0.0f;
+    const float exponent = positive ? expf(-2.0f * raw) : expf(2.0f * raw);
+    const float numerator = positive ? 1.0f - exponent : exponent - 1.0f;
+    return kInteriorScale * (numerator / (1.0f + exponent));
+}
+
+// torch.nn.functional.softplus with beta=1, threshold=20.
+__device__ __forceinline__ float softplus_one(float raw) {
+    const float shifted = raw + kSoftplusOneOffset;
+    return shifted > 20.0f ? shifted : log1pf(expf(shifted));
+}
+
+// Rotate one (even, odd) relation pair by an FP16 (cos, sin) phase.  The
+// BF16 x FP16 products are exact in FP32, so the one rounding of each sum
+// matches the reference's FP32 rotation (reference.py:719-723).
+__device__ __forceinline__ void rotate_pair(uint32_t relation_pair, uint32_t phase,
+                                            float& even_out, float& odd_out) {
+    const float even = bf16_lo(relation_pair);
+    const float odd = bf16_hi(relation_pair);
+    const float cosine = f16_lo(phase);
+    const float sine = f16_hi(phase);
+    even_out = even * cosine - odd * sine;
+    odd_out = even * sine + odd * cosine;
+}
+
+}  // namespace lsso_hip

@@ -1,0 +1,106 @@
+// Kernel argument blocks and launchers shared between the kernel translation
+// units and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace lsso_hip {
+
+constexpr int kMaxPairs = 32;
+
+struct PhaseArgs {
+    const float* positions;  // centered positions or nullptr (default grid)
+    uint32_t* phases;        // packed FP16 (cos, sin), [count]
+    int64_t count;           // (batches) * length * pairs
+    int64_t length;
+    int pairs;
+    float inverse_frequency[kMaxPairs];
+};
+
+struct ReduceArgs {
+    const uint16_t* projected;  // BF16 [B, N, width]
+    const uint32_t* phases;
+    float* partials;            // [B, H, chunks, partial_stride]
+    int64_t batch;
+    int64_t length;
+    int64_t heads;
+    int64_t head_dim;
+    int64_t width;              // heads * rank + heads * head_dim
+    int64_t phase_batch_stride; // 0 (shared) or length * pairs
+    int64_t chunks;
+    int64_t chunk_tokens;       // multiple of 32
+    int64_t column_groups;
+    int64_t partial_stride;     // rank * rank + rank * head_dim
+    int64_t total_waves;
+};
+
+struct SolveArgs {
+    const float* partials;
+    int64_t chunks;
+    int64_t partial_stride;
+    int64_t batch;
+    int64_t length;
+    int64_t heads;
+    int64_t head_dim;
+    const float* base;          // [H, R, R]
+    const float* drive;         // [H, d, R]
+    const float* eta_raw;       // [H]
+    const float* valid_counts;  // [B] or nullptr
+    float* zbuf;                // [B*H, R, d]
+    uint16_t* mop;              // apply operand records
+    float* tape;                // optional
+    int64_t tape_stride;
+};
+
+struct ApplyArgs {
+    const uint16_t* projected;
+    const uint32_t* phases;
+    const uint16_t* mop;
+    const float* eta_raw;
+    uint16_t* output;           // BF16 [B, N, H*d]
+    int64_t batch;
+    int64_t length;
+    int64_t heads;
+    int64_t head_dim;
+    int64_t width;
+    int64_t out_width;
+    int64_t phase_batch_stride;
+    int64_t chunks;
+    int64_t chunk_tokens;       // multiple of 16
+    int64_t feature_blocks;     // ceil(head_dim / 16)
+    int64_t block_groups;       // ceil(feature_blocks / NFBW)
+    int64_t total_waves;
+};
+
+struct LinearArgs {
+    const void* x;
+    int64_t rows;
+    int64_t in_features;
+    int64_t x_stride;
+    const float* weight;        // FP32 [out, in]
+    const float* bias;          // FP32 [out] or nullptr
+    const uint8_t* row_mask;    // [rows] or nullptr; 0 rows are zeroed
+    int64_t out_features;
+    void* y;
+    int64_t tiles;              // ceil(rows / tile_rows)
+    int64_t column_groups;
+    int x_vector;               // 16-byte x loads are legal
+    int y_vector;               // 8-byte y stores are legal
+};
+
+hipError_t launch_phase(const PhaseArgs& a, hipStream_t stream);
+hipError_t launch_reduce(int rank, const ReduceArgs& a, int cpw, bool vec, hipStream_t stream);
+hipError_t launch_solve(int rank, const SolveArgs& a, int64_t systems, hipStream_t stream);
+hipError_t launch_apply(int rank, const ApplyArgs& a, int nfbw, bool vec, hipStream_t stream);
+
+// Projection launcher; k_steps = ceil(in_features / 16) rounded to a
+// compiled tier.  Returns hipErrorInvalidValue for an unsupported tier.
+hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,
+                         int grid_groups, hipStream_t stream);
+int linear_tile_rows();
+int linear_columns_per_group(int k_steps);
+int linear_k_tier(int64_t in_features);
+
+}  // namespace lsso_hip

@@ -1,0 +1,394 @@
+"""Parity of the gfx950 native path against the CPU oracle (GPU).
+
+Bar (reference docs/CUDA_CONTRACT.md:93-101): every tensor finite and the
+relative L2 error against the FP64 oracle at most 5e-3 for forward outputs.
+Projections keep the reference's exact known answers
+(tests/core/test_reference.py:536-614 in the reference) and otherwise agree
+with a plain FP32 torch evaluation of the same BF16 operands within one
+output rounding step.  Full-size configurations are checked on a slice of
+the batch against the oracle and through size-independent properties
+(batch independence, permutation equivariance, determinism, exact zeros of
+all-masked samples).
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from lsso_amd import LSSO, LSSOConfig
+from oracle import lsso_reference as oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel_l2(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    actual = actual.detach().to(device="cpu", dtype=torch.float64)
+    expected = expected.detach().to(device="cpu", dtype=torch.float64)
+    return float((actual - expected).norm() / expected.norm().clamp_min(1e-12))
+
+
+def _mixer_inputs(batch, rank, heads, head_dim, length, seed, scale=0.05):
+    generator = torch.Generator().manual_seed(seed)
+    projected = torch.randn(batch, length, heads * (rank + head_dim), generator=generator).bfloat16()
+    base = scale * torch.randn(heads, rank, rank, generator=generator)
+    drive = scale * torch.randn(heads, head_dim, rank, generator=generator)
+    eta_raw = scale * torch.randn(heads, generator=generator)
+    return projected, base, drive, eta_raw
+
+
+def _run_mixer(native, projected, base, drive, eta_raw, positions=None, counts=None):
+    args = [t.cuda() for t in (projected, base, drive, eta_raw)]
+    with torch.no_grad():
+        return native.fast_mix(
+            *args,
+            None if positions is None else positions.cuda(),
+            None if counts is None else counts.cuda(),
+        )
+
+
+@pytest.mark.parametrize("length", (31, 32, 33, 65, 127, 128, 129, 255, 256, 257, 511, 512, 513))
+def test_mixer_lengths_match_fp64_oracle(native, length: int) -> None:
+    projected, base, drive, eta_raw = _mixer_inputs(1, 16, 2, 16, length, seed=19, scale=0.1)
+    positions = torch.arange(length, dtype=torch.float32)
+    positions = positions - positions.mean()
+    out = _run_mixer(native, projected, base, drive, eta_raw, positions)
+    expected = oracle.fast_mix_fp64(projected, base, drive, eta_raw, positions)
+    assert out.dtype == torch.bfloat16
+    assert torch.isfinite(out).all()
+    assert _rel_l2(out, expected) <= 5e-3
+
+
+# Reference tests/cuda/test_fast_path.py:859-952 shape sweep (forward).
+EXPANDED = [
+    (1, 16, 1, 1, 31), (1, 16, 1, 15, 31), (1, 16, 1, 17, 31), (1, 16, 1, 31, 33),
+    (1, 16, 1, 32, 33), (1, 16, 1, 33, 33), (1, 16, 1, 257, 33), (1, 16, 1, 512, 33),
+    (1, 32, 2, 48, 31), (2, 32, 3, 17, 35), (1, 48, 2, 96, 33), (1, 64, 1, 33, 33),
+    (1, 64, 1, 257, 33), (1, 16, 1, 17, 2048), (1, 32, 1, 17, 2048), (1, 48, 1, 17, 2048),
+    (1, 64, 1, 17, 2048), (1, 16, 1, 17, 2017), (1, 64, 1, 17, 2017), (1, 64, 1, 17, 4096),
+    (1, 32, 8, 32, 4096), (1, 16, 4, 32, 4776), (1, 32, 1, 17, 8193),
+]
+
+
+@pytest.mark.parametrize(("batch", "rank", "heads", "head_dim", "length"), EXPANDED)
+def test_mixer_expanded_shapes_match_fp64_oracle(native, batch, rank, heads, head_dim, length) -> None:
+    projected, base, drive, eta_raw = _mixer_inputs(batch, rank, heads, head_dim, length,
+                                                    seed=71 + batch + rank + head_dim)
+    positions = torch.arange(length, dtype=torch.float32)
+    positions = positions - positions.mean()
+    out = _run_mixer(native, projected, base, drive, eta_raw, positions)
+    expected = oracle.fast_mix_fp64(projected, base, drive, eta_raw, positions)
+    assert torch.isfinite(out).all()
+    assert _rel_l2(out, expected) <= 5e-3
+
+
+@pytest.mark.parametrize(
+    ("rank", "head_dim", "length"),
+    [(16, 17, 35), (32, 64, 35), (48, 96, 35), (64, 257, 35), (16, 17, 2048), (64, 17, 2017)],
+)
+def test_mixer_masked_batched_positions_match_fp64_oracle(native, rank, head_dim, length) -> None:
+    """Reference tests/cuda/test_fast_path.py:955-1063: gapped mask, an
+    all-masked sample, per-sample integer positions."""
+
+    batch, heads = 2, 2
+    pattern = torch.tensor([True, False, True, True, False, True, True])
+    first = pattern.repeat((length + 6) // 7)[:length]
+    mask = torch.stack((first, torch.zeros(length, dtype=torch.bool)))
+    position_ids = torch.stack((3 * torch.arange(length) + 7, 5 * torch.arange(length) + 101))
+    centered = oracle.center_positions(position_ids, mask, dtype=torch.float32, all_valid=False)
+    counts = mask.sum(dim=-1).to(torch.float32).clamp_min(1.0)
+    projected, base, drive, eta_raw = _mixer_inputs(batch, rank, heads, head_dim, length,
+                                                    seed=97 + rank + head_dim)
+    projected = torch.where(mask[:, :, None], projected, torch.zeros_like(projected))
+    out = _run_mixer(native, projected, base, drive, eta_raw, centered, counts)
+    expected = oracle.fast_mix_fp64(projected, base, drive, eta_raw, centered, counts)
+    assert torch.count_nonzero(out.cpu()[~mask]) == 0
+    assert torch.isfinite(out).all()
+    assert _rel_l2(out, expected) <= 5e-3
+
+
+@pytest.mark.parametrize("scale", (0.001, 64.0))
+def test_mixer_relation_scale_extremes(native, scale: float) -> None:
+    """Reference tests/cuda/test_fast_path.py:1482-1509 (forward part)."""
+
+    generator = torch.Generator().manual_seed(711)
+    length, rank, head_dim = 33, 32, 17
+    projected = torch.randn(1, length, rank + head_dim, generator=generator)
+    projected[..., :rank] *= scale
+    projected = projected.bfloat16()
+    base = 0.1 * torch.randn(1, rank, rank, generator=generator)
+    drive = 0.1 * torch.randn(1, head_dim, rank, generator=generator)
+    eta_raw = torch.tensor([0.7])
+    out = _run_mixer(native, projected, base, drive, eta_raw)
+    expected = oracle.fast_mix_fp64(projected, base, drive, eta_raw)
+    assert _rel_l2(out, expected) <= (1e-2 if scale > 1 else 5e-3)
+
+
+def test_mixer_bf16_content_beyond_fp16_range(native) -> None:
+    """Reference tests/cuda/test_fast_path.py:1460-1479."""
+
+    generator = torch.Generator().manual_seed(101)
+    projected = torch.randn(1, 33, 32, generator=generator)
+    projected[:, :, 16:] *= 131072
+    projected = projected.bfloat16()
+    base = torch.zeros(1, 16, 16)
+    drive = torch.zeros(1, 16, 16)
+    eta_raw = torch.tensor([0.7])
+    out = _run_mixer(native, projected, base, drive, eta_raw)
+    expected = oracle.fast_mix_fp64(projected, base, drive, eta_raw)
+    assert out.float().abs().max() > torch.finfo(torch.float16).max
+    assert _rel_l2(out, expected) <= 5e-3
+
+
+def test_mixer_is_deterministic_batch_independent_and_permutation_equivariant(native) -> None:
+    projected, base, drive, eta_raw = _mixer_inputs(6, 32, 4, 32, 1000, seed=5)
+    full = _run_mixer(native, projected, base, drive, eta_raw)
+    again = _run_mixer(native, projected, base, drive, eta_raw)
+    assert torch.equal(full, again)
+    order = torch.tensor([3, 0, 5, 1, 4, 2])
+    permuted = _run_mixer(native, projected[order], base, drive, eta_raw)
+    assert torch.equal(permuted, full[order.cuda()])
+    # A smaller batch changes the token-chunk plan (FP32 summation grouping),
+    # so a single sample agrees to rounding, not bitwise.
+    single = _run_mixer(native, projected[2:3], base, drive, eta_raw)
+    assert _rel_l2(single, full[2:3]) <= 1e-3
+
+
+def test_mixer_rejects_non_bf16_packed_input(native) -> None:
+    projected = torch.randn(1, 5, 32, device="cuda", dtype=torch.float16)
+    base = torch.zeros(1, 16, 16, device="cuda")
+    drive = torch.zeros(1, 16, 16, device="cuda")
+    eta = torch.zeros(1, device="cuda")
+    with pytest.raises(RuntimeError, match="mixed precision HIP contract"):
+        native.fast_mix(projected, base, drive, eta)
+
+
+def test_forward_inference_rejects_direct_autograd(native) -> None:
+    projected = torch.zeros(1, 5, 32, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    base = torch.zeros(1, 16, 16, device="cuda", requires_grad=True)
+    drive = torch.zeros(1, 16, 16, device="cuda")
+    eta = torch.zeros(1, device="cuda")
+    with pytest.raises(RuntimeError, match="inference-only entry point"):
+        native.forward_inference(projected, base, drive, eta)
+    with pytest.raises(RuntimeError, match="private tape-producing entry point"):
+        native.forward_train(projected, base, drive, eta)
+
+
+# -- projections -------------------------------------------------------------
+def _torch_linear(value, weight, bias, output_dtype):
+    out = value.to(torch.bfloat16).float() @ weight.to(torch.bfloat16).float().T
+    if bias is not None:
+        out = out + bias
+    return out.to(output_dtype)
+
+
+@pytest.mark.parametrize("with_bias", (False, True))
+def test_linear_wide_range_bf16_known_answer(native, with_bias: bool) -> None:
+    value = torch.full((2, 16), 131072.0, device="cuda", dtype=torch.bfloat16)
+    weight = torch.full((3, 16), 2.0, device="cuda")
+    bias = torch.full((3,), 262144.0, device="cuda") if with_bias else None
+    out = native.linear(value, weight, bias, torch.bfloat16)
+    expected = 4456448.0 if with_bias else 4194304.0
+    torch.testing.assert_close(out, torch.full_like(out, expected), rtol=0, atol=0)
+
+
+def test_linear_bf16_store_keeps_fp32_accumulation(native) -> None:
+    value = torch.full((2, 256), 32768.0, device="cuda", dtype=torch.bfloat16)
+    weight = torch.ones(3, 256, device="cuda")
+    out = native.linear(value, weight, None, torch.bfloat16)
+    torch.testing.assert_close(out, torch.full_like(out, 8388608.0), rtol=0, atol=0)
+
+
+def test_linear_fp16_output_does_not_round_through_bf16(native) -> None:
+    value = torch.ones(1, 2, device="cuda", dtype=torch.bfloat16)
+    weight = torch.tensor([[1.0, 1.0 / 512]], device="cuda")
+    out = native.linear(value, weight, None, torch.float16)
+    torch.testing.assert_close(out, torch.full_like(out, 1.0 + 1.0 / 512), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_linear_fp32_bias_is_added_before_rounding(native, dtype) -> None:
+    value = torch.ones(3, 1, device="cuda", dtype=dtype)
+    weight = torch.ones(1, 1, device="cuda")
+    bias = torch.tensor([-1.0 + 2.0 ** -9], device="cuda")
+    out = native.linear(value, weight, bias, dtype)
+    torch.testing.assert_close(out, torch.full_like(out, 2.0 ** -9), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_linear_strides_and_tails(native, dtype) -> None:
+    generator = torch.Generator(device="cuda").manual_seed(123)
+    value = torch.randn(2, 67, 70, device="cuda", generator=generator).to(dtype)[..., ::2]
+    weight = torch.randn(35, 51, device="cuda", generator=generator).T
+    bias = torch.randn(102, device="cuda", generator=generator)[::2]
+    out = native.linear(value, weight, bias, dtype)
+    expected = _torch_linear(value, weight, bias, dtype)
+    torch.testing.assert_close(out, expected, rtol=torch.finfo(dtype).eps, atol=0)
+
+
+@pytest.mark.parametrize(
+    ("rows", "in_features", "out_features", "x_dtype", "y_dtype"),
+    [
+        (65536, 256, 512, torch.float16, torch.bfloat16),
+        (65536, 256, 256, torch.bfloat16, torch.float16),
+        (4099, 384, 768, torch.bfloat16, torch.bfloat16),
+        (520, 192, 240, torch.float16, torch.bfloat16),
+        (77, 96, 144, torch.float16, torch.float16),
+        (130, 512, 64, torch.bfloat16, torch.bfloat16),
+        (33, 34, 98, torch.float16, torch.bfloat16),
+    ],
+)
+def test_linear_matches_fp32_evaluation_of_bf16_operands(
+    native, rows, in_features, out_features, x_dtype, y_dtype
+) -> None:
+    generator = torch.Generator(device="cuda").manual_seed(rows + in_features)
+    value = torch.randn(rows, in_features, device="cuda", generator=generator).to(x_dtype)
+    bound = in_features ** -0.5
+    weight = (torch.rand(out_features, in_features, device="cuda", generator=generator) * 2 - 1) * bound
+    bias = (torch.rand(out_features, device="cuda", generator=generator) * 2 - 1) * bound
+    out = native.linear(value, weight, bias, y_dtype)
+    expected = _torch_linear(value, weight, bias, y_dtype)
+    # Different FP32 summation orders may straddle one output rounding step.
+    torch.testing.assert_close(out, expected, rtol=torch.finfo(y_dtype).eps, atol=1e-6)
+
+
+def test_linear_row_mask_zeroes_and_skips_rows(native) -> None:
+    value = torch.randn(100, 64, device="cuda", dtype=torch.float16)
+    mask = torch.rand(100, device="cuda") > 0.3
+    value[~mask] = float("nan")
+    weight = torch.randn(48, 64, device="cuda") * 0.1
+    bias = torch.randn(48, device="cuda")
+    out = native.linear(value, weight, bias, torch.bfloat16, row_mask=mask)
+    assert torch.count_nonzero(out[~mask]) == 0
+    expected = _torch_linear(value[mask], weight, bias, torch.bfloat16)
+    torch.testing.assert_close(out[mask], expected, rtol=torch.finfo(torch.bfloat16).eps, atol=1e-6)
+
+
+# -- complete module -----------------------------------------------------------
+def _oracle_params(layer: LSSO) -> dict[str, torch.Tensor]:
+    return {name: p.detach().double().cpu() for name, p in layer.named_parameters()}
+
+
+def _config_dict(config: LSSOConfig) -> dict:
+    return {"dim": config.dim, "num_heads": config.num_heads, "rank": config.rank, "bias": config.bias}
+
+
+@pytest.mark.parametrize(("dim", "heads", "rank"), [(32, 2, 16), (128, 1, 64), (192, 3, 16), (96, 2, 48)])
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_module_matches_fp64_oracle(native, dim, heads, rank, dtype) -> None:
+    torch.manual_seed(59 + rank)
+    config = LSSOConfig(dim=dim, num_heads=heads, rank=rank, bias=True)
+    layer = LSSO(config).cuda().eval()
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.05)
+        layer.core_drive_weight.normal_(std=0.05)
+    length = 33
+    position_ids = 3 * torch.arange(length, dtype=torch.int64) + 7
+    x = torch.randn(2, length, dim, dtype=dtype)
+    with torch.no_grad():
+        out = layer(x.cuda(), position_ids=position_ids.cuda(), implementation="hip")
+    expected = oracle.lsso_forward(_oracle_params(layer), _config_dict(config), x.double(),
+                                   position_ids=position_ids)
+    assert out.dtype == dtype
+    assert torch.isfinite(out).all()
+    assert _rel_l2(out, expected) <= 5e-3
+
+
+def test_module_masked_batch_matches_fp64_oracle(native) -> None:
+    """Reference tests/cuda/test_fast_path.py:1066-1128 (forward part)."""
+
+    torch.manual_seed(109)
+    config = LSSOConfig(dim=34, num_heads=2, rank=16, bias=True)
+    layer = LSSO(config).cuda().eval()
+    mask = torch.tensor([[True, False, True, True, False, True, True] * 5, [False] * 35])
+    position_ids = torch.stack((3 * torch.arange(35) + 7, 5 * torch.arange(35) + 101))
+    x = torch.randn(2, 35, config.dim, dtype=torch.float16)
+    x[~mask] = float("nan")
+    with torch.no_grad():
+        out = layer(x.cuda(), valid_mask=mask.cuda(), position_ids=position_ids.cuda(), implementation="hip")
+    expected = oracle.lsso_forward(_oracle_params(layer), _config_dict(config), x.double(), mask, position_ids)
+    assert torch.isfinite(out).all()
+    assert torch.count_nonzero(out[1]) == 0
+    assert _rel_l2(out, expected) <= 5e-3
+
+
+def test_module_float64_positions_preserve_relative_coordinates(native) -> None:
+    torch.manual_seed(113)
+    layer = LSSO(LSSOConfig(dim=32, num_heads=2, rank=16)).cuda().eval()
+    x = torch.randn(1, 9, 32, device="cuda", dtype=torch.float16)
+    positions = torch.arange(9, device="cuda", dtype=torch.float64)
+    with torch.no_grad():
+        shifted = layer(x, position_ids=positions + 1e12, implementation="hip")
+        plain = layer(x, position_ids=positions, implementation="hip")
+    torch.testing.assert_close(shifted, plain, rtol=1e-5, atol=1e-6)
+
+
+def test_module_c1_config_matches_reference_golden(native) -> None:
+    """C1 (dim 192, heads 3, rank 16, default init) against the golden FP64
+    output the reference produced in the build container."""
+
+    import numpy as np
+    from pathlib import Path
+
+    with np.load(Path(__file__).resolve().parent / "golden" / "c1_default.npz") as data:
+        x = torch.from_numpy(data["x"])
+        y64 = torch.from_numpy(data["y64"])
+        state = {k.split(":", 1)[1]: torch.from_numpy(data[k]) for k in data.files if k.startswith("param:")}
+    layer = LSSO(LSSOConfig(dim=192, num_heads=3, rank=16))
+    with torch.no_grad():
+        for name, parameter in layer.named_parameters():
+            parameter.copy_(state[name])
+    layer = layer.cuda().eval()
+    with torch.no_grad():
+        out = layer(x.cuda().half(), implementation="hip")
+    assert _rel_l2(out, y64) <= 5e-3
+
+
+@pytest.mark.parametrize("length", (1024, 4096))
+def test_headline_shell_slice_matches_oracle(native, length: int) -> None:
+    """B=64, D=256, H=8, r=32, FP16 (BASELINE configs C2/C3): the full batch
+    runs on the GPU; samples 0, 17 and 63 are checked against the FP64
+    oracle, and the full batch is checked for determinism."""
+
+    torch.manual_seed(0)
+    layer = LSSO(LSSOConfig(dim=256, num_heads=8, rank=32, bias=True)).cuda().eval()
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.05)
+        layer.core_drive_weight.normal_(std=0.05)
+    x = torch.randn(64, length, 256, generator=torch.Generator().manual_seed(1)).half()
+    xd = x.cuda()
+    with torch.no_grad():
+        out = layer(xd, implementation="hip")
+        again = layer(xd, implementation="hip")
+    assert torch.equal(out, again)
+    assert torch.isfinite(out).all()
+    picks = [0, 17, 63]
+    expected = oracle.lsso_forward(_oracle_params(layer), _config_dict(layer.config), x[picks].double())
+    assert _rel_l2(out[picks], expected) <= 5e-3
+
+
+def test_masked_bf16_config_c4_slice(native) -> None:
+    """C4: B=32, D=384, H=6 (d=64), r=64, BF16, trailing-padding masks with
+    valid lengths in [L/4, L], per-sample positions start ~ U[0, 1024)."""
+
+    length, batch = 4096, 32
+    generator = torch.Generator().manual_seed(4)
+    torch.manual_seed(4)
+    layer = LSSO(LSSOConfig(dim=384, num_heads=6, rank=64, bias=True)).cuda().eval()
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.05)
+        layer.core_drive_weight.normal_(std=0.05)
+    lengths = torch.randint(length // 4, length + 1, (batch,), generator=generator)
+    mask = torch.arange(length)[None, :] < lengths[:, None]
+    starts = torch.randint(0, 1024, (batch,), generator=generator)
+    position_ids = starts[:, None] + torch.arange(length)[None, :]
+    x = torch.randn(batch, length, 384, generator=generator).bfloat16()
+    with torch.no_grad():
+        out = layer(x.cuda(), valid_mask=mask.cuda(), position_ids=position_ids.cuda(), implementation="hip")
+    assert torch.count_nonzero(out.cpu()[~mask]) == 0
+    picks = [int(lengths.argmin()), int(lengths.argmax()), 5]
+    expected = oracle.lsso_forward(_oracle_params(layer), _config_dict(layer.config), x[picks].double(),
+                                   mask[picks], position_ids[picks])
+    assert _rel_l2(out[picks], expected) <= 5e-3
