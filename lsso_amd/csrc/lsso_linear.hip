@@ -101,6 +101,7 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     constexpr int kChunksPerThread = kLinearTileRows * kChunksPerRow / kThreads;
     static_assert(kLinearTileRows * kChunksPerRow % kThreads == 0, "tile split");
     __shared__ __attribute__((aligned(16))) uint16_t s_x[2][kLinearTileRows * KP];
+    __shared__ __attribute__((aligned(16))) float s_bias[kGroupColumns];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -113,21 +114,33 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     const int64_t K = a.in_features;
     const int64_t N = a.out_features;
 
-    // W slice: lane holds row n0 + lane%32, k = 16 ks + 8 half + 0..7.
+    // W slice: lane holds row n0 + lane%32, k = 16 ks + 8 half + 0..7.  Rows
+    // are read as float4 pairs when K is a multiple of 4 (16-byte rows).
     u32x4 wreg[KSTEPS];
     {
         const int64_t n = n0 + (lane & 31);
         const bool nv = n < N;
         const float* wrow = a.weight + (nv ? n : 0) * K;
+        const bool vector_rows = (K % 4) == 0;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             const int64_t k0 = 16 * ks + 8 * half;
             float v[8];
+            if (vector_rows && nv && k0 + 8 <= K) {
+                const f32x4 lo = *reinterpret_cast<const f32x4*>(wrow + k0);
+                const f32x4 hi = *reinterpret_cast<const f32x4*>(wrow + k0 + 4);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const bool live = nv && k0 + i < K;
-                const float value = wrow[live ? k0 + i : 0];
-                v[i] = live ? value : 0.0f;
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = lo[i];
+                    v[4 + i] = hi[i];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const bool live = nv && k0 + i < K;
+                    const float value = wrow[live ? k0 + i : 0];
+                    v[i] = live ? value : 0.0f;
+                }
             }
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
@@ -137,6 +150,10 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
             // being hoisted next to the whole BF16 slice.
             __builtin_amdgcn_sched_barrier(0);
         }
+    }
+    for (int c = tid; c < kGroupColumns; c += kThreads) {
+        const int64_t n = cg * kGroupColumns + c;
+        s_bias[c] = (a.bias != nullptr && n < N) ? a.bias[n] : 0.0f;
     }
 
     u32x4 stage[kChunksPerThread];
@@ -179,24 +196,32 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
                 acc[mb][i] = 0.0f;
             }
         }
-        // Operand reads go in groups of four K steps so that at most eight
-        // x fragments are live next to the resident W slice.
+        // Operand reads run one group of two K steps ahead of the MFMAs, so
+        // at most eight x fragments are live next to the resident W slice.
+        constexpr int kGroup = 2;
+        u32x4 xb[2][kGroup][2];
+        auto read_group = [&](int slot, int k_base) {
 #pragma unroll
-        for (int k4 = 0; k4 < KSTEPS; k4 += 4) {
-            u32x4 xb[4][2];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
+            for (int ks = 0; ks < kGroup; ++ks) {
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
-                    xb[ks][mb] = *reinterpret_cast<const u32x4*>(
-                        &s_x[buf][(mb * 32 + (lane & 31)) * KP + 16 * (k4 + ks) + 8 * half]);
+                    xb[slot][ks][mb] = *reinterpret_cast<const u32x4*>(
+                        &s_x[buf][(mb * 32 + (lane & 31)) * KP + 16 * (k_base + ks) + 8 * half]);
                 }
             }
+        };
+        read_group(0, 0);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
+        for (int k2 = 0; k2 < KSTEPS; k2 += kGroup) {
+            const int slot = (k2 / kGroup) & 1;
+            if (k2 + kGroup < KSTEPS) {
+                read_group(slot ^ 1, k2 + kGroup);
+            }
+#pragma unroll
+            for (int ks = 0; ks < kGroup; ++ks) {
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
-                    acc[mb] = mfma32x32x16(wreg[k4 + ks], xb[ks][mb], acc[mb]);
+                    acc[mb] = mfma32x32x16(wreg[k2 + ks], xb[slot][ks][mb], acc[mb]);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -212,11 +237,8 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
                     const int64_t n = n0 + 8 * qd + 4 * half;
-                    float bias[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        bias[r] = (a.bias != nullptr && n + r < N) ? a.bias[n + r] : 0.0f;
-                    }
+                    const f32x4 bias = *reinterpret_cast<const f32x4*>(
+                        &s_bias[wave * 32 + 8 * qd + 4 * half]);
                     const float v0 = keep ? acc[mb][4 * qd + 0] + bias[0] : 0.0f;
                     const float v1 = keep ? acc[mb][4 * qd + 1] + bias[1] : 0.0f;
                     const float v2 = keep ? acc[mb][4 * qd + 2] + bias[2] : 0.0f;

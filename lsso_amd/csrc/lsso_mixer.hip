@@ -48,22 +48,25 @@ struct ReduceLayout {
     }
 };
 
-// Apply: the rank dimension is the MFMA K index.  K32 steps cover 32 ranks
-// (lane group g holds ranks base + 8g .. +7), an optional K16 tail covers 16
-// (ranks base + 4g .. +3).  Per lane the M' operand holds, per step, the hi
-// values followed by the lo values.
+// Apply: the rank dimension is the MFMA K index.  Ranks that are multiples
+// of 32 use K32 steps (16x16x32; lane group g holds ranks base + 8g .. +7),
+// the others K16 steps (16x16x16; ranks base + 4g .. +3).  One accumulation
+// chain never mixes the two MFMA shapes: a 16x16x32 result consumed as SrcC
+// of a 16x16x16 produced wrong accumulators on gfx950 with this toolchain.
+// Per lane the M' operand holds, per step, the hi values followed by the lo
+// values.
 template <int R>
 struct ApplyLayout {
-    static constexpr int kSteps32 = R / 32;
-    static constexpr bool kTail16 = (R % 32) != 0;
+    static constexpr bool kWide = (R % 32) == 0;
+    static constexpr int kSteps32 = kWide ? R / 32 : 0;
+    static constexpr int kSteps16 = kWide ? 0 : R / 16;
     static constexpr int kLaneValues = R / 4;          // per hi or lo part
     static constexpr int kLaneHalfs = 2 * kLaneValues;  // bf16 per lane per block
-    // rank of value `i` of lane group `g` in K32 step `s`
     __device__ static constexpr int rank32(int s, int g, int i) { return 32 * s + 8 * g + i; }
-    __device__ static constexpr int rank16(int g, int i) { return 32 * kSteps32 + 4 * g + i; }
-    // offset (in bf16) of the hi part of K32 step s inside a lane record
+    __device__ static constexpr int rank16(int s, int g, int i) { return 16 * s + 4 * g + i; }
+    // offsets (in bf16) of the hi part of a step inside a lane record
     __device__ static constexpr int offset32(int s) { return 16 * s; }
-    __device__ static constexpr int offset16() { return 16 * kSteps32; }
+    __device__ static constexpr int offset16(int s) { return 8 * s; }
 };
 
 // ---------------------------------------------------------------------------
@@ -332,10 +335,13 @@ template <int R>
 __global__ __launch_bounds__(64) void solve_kernel(SolveArgs a) {
     using AL = ApplyLayout<R>;
     constexpr int LD = R + 1;
+    constexpr int PLD = kSolvePanel + 1;
+    constexpr int kBlock = R / 8;  // Theta tile per lane: kBlock x kBlock
     __shared__ float s_chol[R * LD];
     __shared__ float s_lu[R * LD];
     __shared__ float s_theta[R * LD];
-    __shared__ float s_panel[R * (kSolvePanel + 1)];
+    __shared__ float s_panel[R * PLD];
+    __shared__ float s_drive[kSolvePanel * LD];
     __shared__ float s_diag[R];
     __shared__ int s_perm[R];
 
@@ -349,16 +355,62 @@ __global__ __launch_bounds__(64) void solve_kernel(SolveArgs a) {
     const float eta = bounded_complement(a.eta_raw[h]);
     const float* part = a.partials + system * a.chunks * a.partial_stride;
 
-    // G / n + I, summed over token chunks in ascending order.
-    for (int idx = tid; idx < R * R; idx += 64) {
-        const int r = idx / R;
-        const int c = idx - r * R;
-        float sum = 0.0f;
-        for (int64_t ch = 0; ch < a.chunks; ++ch) {
-            sum += part[ch * a.partial_stride + idx];
+    // G / n + I, summed over token chunks in ascending order.  partial_stride
+    // is a multiple of 4 (R is a multiple of 16), so the G block is read as
+    // float4 with every chunk's loads of a group in flight together.
+    {
+        constexpr int kG4 = R * R / 4;
+        constexpr int kPer = (kG4 + 63) / 64;
+        f32x4 acc[kPer];
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            acc[p] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
         }
-        s_chol[r * LD + c] = sum / count + (r == c ? 1.0f : 0.0f);
-        s_theta[r * LD + c] = 0.0f;
+        int64_t ch = 0;
+        for (; ch + 4 <= a.chunks; ch += 4) {
+            f32x4 v[4][kPer];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                for (int p = 0; p < kPer; ++p) {
+                    const int vec = tid + 64 * p;
+                    v[u][p] = vec < kG4 ? *reinterpret_cast<const f32x4*>(part + (ch + u) * a.partial_stride + 4 * vec)
+                                        : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                for (int p = 0; p < kPer; ++p) {
+                    acc[p] += v[u][p];
+                }
+            }
+        }
+        for (; ch < a.chunks; ++ch) {
+#pragma unroll
+            for (int p = 0; p < kPer; ++p) {
+                const int vec = tid + 64 * p;
+                if (vec < kG4) {
+                    acc[p] += *reinterpret_cast<const f32x4*>(part + ch * a.partial_stride + 4 * vec);
+                }
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            const int vec = tid + 64 * p;
+            if (vec < kG4) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int idx = 4 * vec + e;
+                    const int r = idx / R;
+                    const int c = idx - r * R;
+                    s_chol[r * LD + c] = acc[p][e] / count + (r == c ? 1.0f : 0.0f);
+                }
+            }
+        }
+        for (int idx = tid; idx < R * LD; idx += 64) {
+            s_theta[idx] = 0.0f;
+        }
     }
     __syncthreads();
 
@@ -391,28 +443,30 @@ __global__ __launch_bounds__(64) void solve_kernel(SolveArgs a) {
     }
     __syncthreads();
 
-    // Z = L^-1 S panel by panel; Theta accumulates Z W_drive.
+    // Z = L^-1 S panel by panel (lane = column: S summed over chunks straight
+    // into registers, then forward substitution); Theta accumulates Z W_drive
+    // from LDS copies of the panel and of W_drive's rows.
     float* zbuf = a.zbuf + system * R * d;
     const float* drive = a.drive + h * d * R;
+    const float* part_s = part + R * R;
     for (int64_t c0 = 0; c0 < d; c0 += kSolvePanel) {
         const int64_t width = d - c0 < kSolvePanel ? d - c0 : kSolvePanel;
-        for (int idx = tid; idx < R * kSolvePanel; idx += 64) {
-            const int r = idx / kSolvePanel;
-            const int c = idx - r * kSolvePanel;
-            float sum = 0.0f;
-            if (c < width) {
-                for (int64_t ch = 0; ch < a.chunks; ++ch) {
-                    sum += part[ch * a.partial_stride + R * R + r * d + c0 + c];
-                }
-            }
-            s_panel[r * (kSolvePanel + 1) + c] = sum / root;
-        }
-        __syncthreads();
         if (tid < width) {
             float z[R];
 #pragma unroll
             for (int i = 0; i < R; ++i) {
-                float value = s_panel[i * (kSolvePanel + 1) + tid];
+                z[i] = 0.0f;
+            }
+            for (int64_t ch = 0; ch < a.chunks; ++ch) {
+                const float* column = part_s + ch * a.partial_stride + c0 + tid;
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    z[i] += column[i * d];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                float value = z[i] / root;
 #pragma unroll
                 for (int k = 0; k < i; ++k) {
                     value -= s_chol[i * LD + k] * z[k];
@@ -421,19 +475,50 @@ __global__ __launch_bounds__(64) void solve_kernel(SolveArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < R; ++i) {
-                s_panel[i * (kSolvePanel + 1) + tid] = z[i];
+                s_panel[i * PLD + tid] = z[i];
                 zbuf[i * d + c0 + tid] = z[i];
             }
         }
+        for (int idx = tid; idx < width * R; idx += 64) {
+            const int f = idx / R;
+            const int c = idx - f * R;
+            s_drive[f * LD + c] = drive[(c0 + f) * R + c];
+        }
         __syncthreads();
-        for (int idx = tid; idx < R * R; idx += 64) {
-            const int r = idx / R;
-            const int c = idx - r * R;
-            float sum = s_theta[r * LD + c];
-            for (int f = 0; f < width; ++f) {
-                sum += s_panel[r * (kSolvePanel + 1) + f] * drive[(c0 + f) * R + c];
+        {
+            const int bi = tid / 8;
+            const int bj = tid - 8 * bi;
+            float acc[kBlock][kBlock];
+#pragma unroll
+            for (int x = 0; x < kBlock; ++x) {
+#pragma unroll
+                for (int y = 0; y < kBlock; ++y) {
+                    acc[x][y] = s_theta[(kBlock * bi + x) * LD + kBlock * bj + y];
+                }
             }
-            s_theta[r * LD + c] = sum;
+            for (int f = 0; f < width; ++f) {
+                float zc[kBlock];
+                float wr[kBlock];
+#pragma unroll
+                for (int x = 0; x < kBlock; ++x) {
+                    zc[x] = s_panel[(kBlock * bi + x) * PLD + f];
+                    wr[x] = s_drive[f * LD + kBlock * bj + x];
+                }
+#pragma unroll
+                for (int x = 0; x < kBlock; ++x) {
+#pragma unroll
+                    for (int y = 0; y < kBlock; ++y) {
+                        acc[x][y] = fmaf(zc[x], wr[y], acc[x][y]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int x = 0; x < kBlock; ++x) {
+#pragma unroll
+                for (int y = 0; y < kBlock; ++y) {
+                    s_theta[(kBlock * bi + x) * LD + kBlock * bj + y] = acc[x][y];
+                }
+            }
         }
         __syncthreads();
     }
@@ -614,13 +699,14 @@ __global__ __launch_bounds__(64) void solve_kernel(SolveArgs a) {
                     *reinterpret_cast<uint32_t*>(record + AL::offset32(s) + 8 + i) = lo;
                 }
             }
-            if constexpr (AL::kTail16) {
+#pragma unroll
+            for (int s = 0; s < AL::kSteps16; ++s) {
 #pragma unroll
                 for (int i = 0; i < 4; i += 2) {
                     uint32_t hi, lo;
-                    split_bf16(u[AL::rank16(g, i)], u[AL::rank16(g, i + 1)], hi, lo);
-                    *reinterpret_cast<uint32_t*>(record + AL::offset16() + i) = hi;
-                    *reinterpret_cast<uint32_t*>(record + AL::offset16() + 4 + i) = lo;
+                    split_bf16(u[AL::rank16(s, g, i)], u[AL::rank16(s, g, i + 1)], hi, lo);
+                    *reinterpret_cast<uint32_t*>(record + AL::offset16(s) + i) = hi;
+                    *reinterpret_cast<uint32_t*>(record + AL::offset16(s) + 4 + i) = lo;
                 }
             }
         }
@@ -634,8 +720,8 @@ struct ApplyOperands {
     using AL = ApplyLayout<R>;
     u32x4 hi32[NFBW][AL::kSteps32 > 0 ? AL::kSteps32 : 1];
     u32x4 lo32[NFBW][AL::kSteps32 > 0 ? AL::kSteps32 : 1];
-    u32x2 hi16[NFBW];
-    u32x2 lo16[NFBW];
+    u32x2 hi16[NFBW][AL::kSteps16 > 0 ? AL::kSteps16 : 1];
+    u32x2 lo16[NFBW][AL::kSteps16 > 0 ? AL::kSteps16 : 1];
 };
 
 template <int R, int NFBW, bool VEC>
@@ -674,11 +760,12 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
             op.lo32[f][s] = live ? *reinterpret_cast<const u32x4*>(record + AL::offset32(s) + 8)
                                  : (u32x4){0u, 0u, 0u, 0u};
         }
-        if constexpr (AL::kTail16) {
-            op.hi16[f] = live ? *reinterpret_cast<const u32x2*>(record + AL::offset16())
-                              : (u32x2){0u, 0u};
-            op.lo16[f] = live ? *reinterpret_cast<const u32x2*>(record + AL::offset16() + 4)
-                              : (u32x2){0u, 0u};
+#pragma unroll
+        for (int s = 0; s < AL::kSteps16; ++s) {
+            op.hi16[f][s] = live ? *reinterpret_cast<const u32x2*>(record + AL::offset16(s))
+                                 : (u32x2){0u, 0u};
+            op.lo16[f][s] = live ? *reinterpret_cast<const u32x2*>(record + AL::offset16(s) + 4)
+                                 : (u32x2){0u, 0u};
         }
     }
 
@@ -722,10 +809,11 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
                 b_lo32[s][p] = lo;
             }
         }
-        u32x2 b_hi16 = {0u, 0u};
-        u32x2 b_lo16 = {0u, 0u};
-        if constexpr (AL::kTail16) {
-            const int first_rank = 32 * AL::kSteps32 + 4 * g;
+        u32x2 b_hi16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
+        u32x2 b_lo16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
+#pragma unroll
+        for (int s = 0; s < AL::kSteps16; ++s) {
+            const int first_rank = 16 * s + 4 * g;
             u32x2 rel;
             u32x2 ph;
             if constexpr (VEC) {
@@ -747,8 +835,8 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
             for (int p = 0; p < 2; ++p) {
                 uint32_t hi, lo;
                 split_bf16(v[2 * p], v[2 * p + 1], hi, lo);
-                b_hi16[p] = hi;
-                b_lo16[p] = lo;
+                b_hi16[s][p] = hi;
+                b_lo16[s][p] = lo;
             }
         }
 
@@ -765,10 +853,11 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
                 acc = mfma16x16x32(op.hi32[f][s], b_lo32[s], acc);
                 acc = mfma16x16x32(op.lo32[f][s], b_hi32[s], acc);
             }
-            if constexpr (AL::kTail16) {
-                acc = mfma16x16x16(op.hi16[f], b_hi16, acc);
-                acc = mfma16x16x16(op.hi16[f], b_lo16, acc);
-                acc = mfma16x16x16(op.lo16[f], b_hi16, acc);
+#pragma unroll
+            for (int s = 0; s < AL::kSteps16; ++s) {
+                acc = mfma16x16x16(op.hi16[f][s], b_hi16[s], acc);
+                acc = mfma16x16x16(op.hi16[f][s], b_lo16[s], acc);
+                acc = mfma16x16x16(op.lo16[f][s], b_hi16[s], acc);
             }
             if (!live) {
                 continue;
