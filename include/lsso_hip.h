@@ -78,7 +78,8 @@ int lsso_hip_mixer_workspace_bytes(const lsso_hip_mixer_shape* shape,
 
 /* Number of float32 values in the per-call training tape (0 if the caller
  * passes tape == NULL).  The tape holds only compact per-(sample, head)
- * state; no token-sized frame is stored.
+ * state, no token-sized frame: per system (b, h), in order, L, Theta,
+ * (I + K)^-1 and L^-1 (r x r each, row-major), then Z and U (r x d each).
  * Replaces: training_tape_layout (csrc/ball/common.cuh:84-108). */
 int lsso_hip_mixer_tape_floats(const lsso_hip_mixer_shape* shape, size_t* floats);
 

@@ -96,7 +96,7 @@ int make_plan(const lsso_hip_mixer_shape* shape, int positions_mode, MixerPlan* 
                 &p->apply_chunks, &p->apply_chunk_tokens);
 
     p->partial_stride = p->rank * p->rank + p->rank * p->head_dim;
-    p->tape_stride = 3 * p->rank * p->rank + p->rank + 2 * p->rank * p->head_dim;
+    p->tape_stride = 4 * p->rank * p->rank + 2 * p->rank * p->head_dim;
 
     const int64_t systems = p->batch * p->heads;
     size_t offset = 0;

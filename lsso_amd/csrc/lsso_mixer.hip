@@ -316,400 +316,609 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Solve: one 64-lane workgroup per (b, h) system.
+// Solve: one 256-thread workgroup per (b, h) system.
+//
+//   A = G / n + I = L L^T            Cholesky; L^-1 from the same steps
+//   Z = L^-1 S / sqrt(n)             product
+//   Theta = Theta0 + Z W / sqrt(n)   product
+//   I + K = I + F F^T + Omega        product
+//   (I + K)^-1                       Gauss-Jordan with partial (row) pivoting
+//   U = (I + K)^-1 Z, X = 2U - (1 + eta) Z, M' = L^-T X / sqrt(n)   products
+//
+// The two factorizations are sequential (one step per rank) and run in wave 0
+// with one matrix row per lane held in registers; a step's pivot column or
+// row reaches the other lanes through LDS (in-order within one wave, so no
+// barrier).  The products use all four waves.  Step loops stay rolled: the
+// instruction stream runs once per system, so code size sets the speed of
+// this kernel more than instruction count.
+extern "C" __device__ unsigned int __ockl_wfred_max_u32(unsigned int);
+
+constexpr int kSolveThreads = 256;
 constexpr int kSolvePanel = 64;
 
-__device__ __forceinline__ void wave_argmax(float& value, int& index) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        const float other_value = __shfl_xor(value, offset, 64);
-        const int other_index = __shfl_xor(index, offset, 64);
-        if (other_value > value || (other_value == value && other_index < index)) {
-            value = other_value;
-            index = other_index;
+template <int R>
+struct SolveLayout {
+    static constexpr int kLD = R + 4;              // R x R matrices (16-byte rows)
+    static constexpr int kPLD = kSolvePanel + 4;   // R x panel matrices
+    static constexpr int kChunks = R / 16;         // 16-float register chunks per row
+    static constexpr bool kSplit = R <= 32;        // Cholesky rows and L^-1 rows on separate lanes
+    static constexpr int kThetaQuads = (R * R / 4 + kSolveThreads - 1) / kSolveThreads;
+    static constexpr int kLinv = 0;                       // L^-1 rows
+    static constexpr int kLinvT = kLinv + R * kLD;        // L^-1 transposed
+    static constexpr int kTheta = kLinvT + R * kLD;       // Theta
+    static constexpr int kWork = kTheta + R * kLD;        // A; F; Gauss-Jordan rows in step order
+    static constexpr int kSys = kWork + R * kLD;          // I + K, then (I + K)^-1
+    static constexpr int kPanelA = kSys + R * kLD;        // S panel; drive panel; X panel
+    static constexpr int kPanelB = kPanelA + R * kPLD;    // Z panel; M' panel
+    static constexpr int kColumn = kPanelB + R * kPLD;    // 2 x 64 step columns
+    static constexpr int kRow = kColumn + 128;            // 2 x R step rows
+    static constexpr int kPivot = kRow + 2 * R;           // pivot row of each step
+    static constexpr int kTotal = kPivot + R;
+};
+
+// A matrix row in registers: up to four 16-float vectors that are separate
+// local values of the kernel, bound here by reference.  Kept apart (not an
+// aggregate) so that a wave-uniform element index compiles to a relative
+// register move rather than a private-memory array.
+template <int Q>
+struct RegRow {
+    f32x16 &c0, &c1, &c2, &c3;
+    template <int q>
+    __device__ __forceinline__ f32x16& at() const {
+        if constexpr (q == 0) {
+            return c0;
+        } else if constexpr (q == 1) {
+            return c1;
+        } else if constexpr (q == 2) {
+            return c2;
+        } else {
+            return c3;
         }
+    }
+};
+
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_zero(const RegRow<Q>& r) {
+    if constexpr (q < Q) {
+        r.template at<q>() = 0.0f;
+        row_zero<Q, q + 1>(r);
     }
 }
 
+// Element k of a register row for a wave-uniform k.
+template <int Q, int q = 0>
+__device__ __forceinline__ float row_get(const RegRow<Q>& r, int k, float found = 0.0f) {
+    if constexpr (q < Q) {
+        const float c = r.template at<q>()[k & 15];
+        return row_get<Q, q + 1>(r, k, (k >> 4) == q ? c : found);
+    } else {
+        return found;
+    }
+}
+
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_set(const RegRow<Q>& r, int k, float value) {
+    if constexpr (q < Q) {
+        f32x16 t = r.template at<q>();
+        const float old = t[k & 15];
+        t[k & 15] = (k >> 4) == q ? value : old;
+        r.template at<q>() = t;
+        row_set<Q, q + 1>(r, k, value);
+    }
+}
+
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_load(const RegRow<Q>& r, const float* p) {
+    if constexpr (q < Q) {
+        f32x16 t;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(p + 16 * q + 4 * m);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                t[4 * m + e] = v[e];
+            }
+        }
+        r.template at<q>() = t;
+        row_load<Q, q + 1>(r, p);
+    }
+}
+
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_store(float* p, const RegRow<Q>& r) {
+    if constexpr (q < Q) {
+        const f32x16 t = r.template at<q>();
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            *reinterpret_cast<f32x4*>(p + 16 * q + 4 * m) =
+                (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
+        }
+        row_store<Q, q + 1>(p, r);
+    }
+}
+
+// r -= f * x
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_axpy(const RegRow<Q>& r, float f, const RegRow<Q>& x) {
+    if constexpr (q < Q) {
+        f32x16 t = r.template at<q>();
+        const f32x16 xt = x.template at<q>();
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            t[e] = fmaf(-f, xt[e], t[e]);
+        }
+        r.template at<q>() = t;
+        row_axpy<Q, q + 1>(r, f, x);
+    }
+}
+
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_divide(const RegRow<Q>& r, float divisor) {
+    if constexpr (q < Q) {
+        f32x16 t = r.template at<q>();
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            t[e] = t[e] / divisor;
+        }
+        r.template at<q>() = t;
+        row_divide<Q, q + 1>(r, divisor);
+    }
+}
+
+// Row `row` of the identity (row may differ between lanes).
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_identity(const RegRow<Q>& r, int row) {
+    if constexpr (q < Q) {
+        f32x16 t;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            t[e] = 16 * q + e == row ? 1.0f : 0.0f;
+        }
+        r.template at<q>() = t;
+        row_identity<Q, q + 1>(r, row);
+    }
+}
+
+// Column `column` of an LDS matrix with row stride ld receives the row.
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_store_column(float* p, int ld, int column, const RegRow<Q>& r) {
+    if constexpr (q < Q) {
+        const f32x16 t = r.template at<q>();
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            p[(16 * q + e) * ld + column] = t[e];
+        }
+        row_store_column<Q, q + 1>(p, ld, column, r);
+    }
+}
+
+#define LSSO_REG_ROW(name)                                              \
+    f32x16 name##_0 = 0.0f, name##_1 = 0.0f, name##_2 = 0.0f, name##_3 = 0.0f; \
+    const RegRow<Q> name{name##_0, name##_1, name##_2, name##_3}
+
+// LDS ordering between lanes of one wave: its LDS instructions execute in
+// issue order, so only the compiler must be kept from reordering.
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <int R>
-__global__ __launch_bounds__(64) void solve_kernel(SolveArgs a) {
+__global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
+    using SL = SolveLayout<R>;
     using AL = ApplyLayout<R>;
-    constexpr int LD = R + 1;
-    constexpr int PLD = kSolvePanel + 1;
-    constexpr int kBlock = R / 8;  // Theta tile per lane: kBlock x kBlock
-    __shared__ float s_chol[R * LD];
-    __shared__ float s_lu[R * LD];
-    __shared__ float s_theta[R * LD];
-    __shared__ float s_panel[R * PLD];
-    __shared__ float s_drive[kSolvePanel * LD];
-    __shared__ float s_diag[R];
-    __shared__ int s_perm[R];
+    constexpr int Q = SL::kChunks;
+    constexpr int LD = SL::kLD;
+    constexpr int PLD = SL::kPLD;
+    __shared__ __attribute__((aligned(16))) float smem[SL::kTotal];
+    float* s_linv = smem + SL::kLinv;
+    float* s_linvt = smem + SL::kLinvT;
+    float* s_theta = smem + SL::kTheta;
+    float* s_work = smem + SL::kWork;
+    float* s_sys = smem + SL::kSys;
+    float* s_pa = smem + SL::kPanelA;
+    float* s_pb = smem + SL::kPanelB;
+    int* s_pivot = reinterpret_cast<int*>(smem + SL::kPivot);
 
     const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
     const int64_t system = blockIdx.x;
     const int64_t b = system / a.heads;
     const int64_t h = system - b * a.heads;
-    const int64_t d = a.head_dim;
+    const int d = static_cast<int>(a.head_dim);
+    const int chunks = static_cast<int>(a.chunks);
+    const int64_t stride = a.partial_stride;
     const float count = a.valid_counts != nullptr ? a.valid_counts[b] : static_cast<float>(a.length);
     const float root = sqrtf(count);
     const float eta = bounded_complement(a.eta_raw[h]);
-    const float* part = a.partials + system * a.chunks * a.partial_stride;
+    const float* part = a.partials + system * chunks * stride;
+    float* tape = a.tape != nullptr ? a.tape + system * a.tape_stride : nullptr;
 
-    // G / n + I, summed over token chunks in ascending order.  partial_stride
-    // is a multiple of 4 (R is a multiple of 16), so the G block is read as
-    // float4 with every chunk's loads of a group in flight together.
-    {
-        constexpr int kG4 = R * R / 4;
-        constexpr int kPer = (kG4 + 63) / 64;
-        f32x4 acc[kPer];
-#pragma unroll
-        for (int p = 0; p < kPer; ++p) {
-            acc[p] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    // ---- A = G / n + I; chunk partials summed in ascending order ----------
+    for (int q = tid; q < R * R / 4; q += kSolveThreads) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ch = 0; ch < chunks; ++ch) {
+            acc += *reinterpret_cast<const f32x4*>(part + ch * stride + 4 * q);
         }
-        int64_t ch = 0;
-        for (; ch + 4 <= a.chunks; ch += 4) {
-            f32x4 v[4][kPer];
+        const int i = (4 * q) / R;
+        const int j = 4 * q - i * R;
+        f32x4 value;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-#pragma unroll
-                for (int p = 0; p < kPer; ++p) {
-                    const int vec = tid + 64 * p;
-                    v[u][p] = vec < kG4 ? *reinterpret_cast<const f32x4*>(part + (ch + u) * a.partial_stride + 4 * vec)
-                                        : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-#pragma unroll
-                for (int p = 0; p < kPer; ++p) {
-                    acc[p] += v[u][p];
-                }
-            }
+        for (int e = 0; e < 4; ++e) {
+            value[e] = acc[e] / count + (j + e == i ? 1.0f : 0.0f);
         }
-        for (; ch < a.chunks; ++ch) {
-#pragma unroll
-            for (int p = 0; p < kPer; ++p) {
-                const int vec = tid + 64 * p;
-                if (vec < kG4) {
-                    acc[p] += *reinterpret_cast<const f32x4*>(part + ch * a.partial_stride + 4 * vec);
-                }
-            }
+        *reinterpret_cast<f32x4*>(s_work + i * LD + j) = value;
+    }
+    __syncthreads();
+
+    // ---- Cholesky in wave 0, LDL^T-update form with the unit-lower inverse
+    // carried along: step k subtracts (a_ik / a_kk) times row k from every
+    // row i > k of [A | I].  Then L = L_u D^1/2 and L^-1 = D^-1/2 L_u^-1.
+    if (wave == 0) {
+        constexpr bool kSplit = SL::kSplit;
+        const int row = kSplit ? (lane & 31) : lane;
+        const bool inverse_lane = kSplit && lane >= 32;
+        const bool live = row < R;
+        LSSO_REG_ROW(work);    // A row (L^-1 row on inverse lanes when split)
+        LSSO_REG_ROW(carry);   // L^-1 row (unsplit only)
+        if (live && !inverse_lane) {
+            row_load(work, s_work + row * LD);
         }
-#pragma unroll
-        for (int p = 0; p < kPer; ++p) {
-            const int vec = tid + 64 * p;
-            if (vec < kG4) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int idx = 4 * vec + e;
-                    const int r = idx / R;
-                    const int c = idx - r * R;
-                    s_chol[r * LD + c] = acc[p][e] / count + (r == c ? 1.0f : 0.0f);
+        if (live) {
+            if (kSplit) {
+                if (inverse_lane) {
+                    row_identity(work, row);
                 }
+            } else {
+                row_identity(carry, row);
             }
         }
-        for (int idx = tid; idx < R * LD; idx += 64) {
-            s_theta[idx] = 0.0f;
+        float own_root = 1.0f;
+#pragma unroll 1
+        for (int k = 0; k < R; ++k) {
+            float* column = smem + SL::kColumn + (k & 1) * 64;
+            float* step_row = smem + SL::kRow + (k & 1) * R;
+            const float x = row_get(work, k);
+            if (!inverse_lane) {
+                column[row] = row >= k ? x : 0.0f;
+            }
+            if (lane == (kSplit ? 32 + k : k)) {
+                if constexpr (kSplit) {
+                    row_store(step_row, work);
+                } else {
+                    row_store(step_row, carry);
+                }
+            }
+            wave_lds_order();
+            const float pivot = column[k];
+            const float own = column[row];
+            const float f = row > k ? own / pivot : 0.0f;
+            LSSO_REG_ROW(source);
+            row_load(source, kSplit && inverse_lane ? step_row : column);
+            row_axpy(work, f, source);
+            if (!kSplit) {
+                LSSO_REG_ROW(aug);
+                row_load(aug, step_row);
+                row_axpy(carry, f, aug);
+            }
+            const float root_pivot = sqrtf(pivot);
+            if (!inverse_lane) {
+                row_set(work, k, row > k ? x / root_pivot : (row == k ? root_pivot : 0.0f));
+            }
+            own_root = row == k ? root_pivot : own_root;
+        }
+        if (live) {
+            const RegRow<Q>& inverse = kSplit ? work : carry;
+            if (!kSplit || inverse_lane) {
+                row_divide(inverse, own_root);
+                row_store(s_linv + row * LD, inverse);
+                row_store_column(s_linvt, LD, row, inverse);
+                if (tape != nullptr) {
+                    row_store(tape + 3 * R * R + row * R, inverse);
+                }
+            }
+            if (!inverse_lane && tape != nullptr) {
+                row_store(tape + row * R, work);
+            }
         }
     }
     __syncthreads();
 
-    // Cholesky in LDL^T-update form: step k subtracts a_ik a_jk / a_kk from
-    // the trailing lower triangle; lane i owns row i, so no step races.
-    for (int k = 0; k < R - 1; ++k) {
-        const int i = tid;
-        if (i > k && i < R) {
-            const float f = s_chol[i * LD + k] / s_chol[k * LD + k];
-            for (int j = k + 1; j <= i; ++j) {
-                s_chol[i * LD + j] -= f * s_chol[j * LD + k];
-            }
-        }
-        __syncthreads();
-    }
-    if (tid < R) {
-        s_diag[tid] = sqrtf(s_chol[tid * LD + tid]);
-    }
-    __syncthreads();
-    for (int idx = tid; idx < R * R; idx += 64) {
-        const int r = idx / R;
-        const int c = idx - r * R;
-        float value = 0.0f;
-        if (c < r) {
-            value = s_chol[r * LD + c] / s_diag[c];
-        } else if (c == r) {
-            value = s_diag[r];
-        }
-        s_chol[r * LD + c] = value;
-    }
-    __syncthreads();
-
-    // Z = L^-1 S panel by panel (lane = column: S summed over chunks straight
-    // into registers, then forward substitution); Theta accumulates Z W_drive
-    // from LDS copies of the panel and of W_drive's rows.
+    // ---- Z panels (Z = L^-1 S / sqrt(n)) and Theta = Z W accumulation ------
     float* zbuf = a.zbuf + system * R * d;
     const float* drive = a.drive + h * d * R;
-    const float* part_s = part + R * R;
-    for (int64_t c0 = 0; c0 < d; c0 += kSolvePanel) {
-        const int64_t width = d - c0 < kSolvePanel ? d - c0 : kSolvePanel;
-        if (tid < width) {
-            float z[R];
+    f32x4 theta_acc[SL::kThetaQuads];
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                z[i] = 0.0f;
-            }
-            for (int64_t ch = 0; ch < a.chunks; ++ch) {
-                const float* column = part_s + ch * a.partial_stride + c0 + tid;
-#pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    z[i] += column[i * d];
+    for (int t = 0; t < SL::kThetaQuads; ++t) {
+        theta_acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    for (int c0 = 0; c0 < d; c0 += kSolvePanel) {
+        const int width = d - c0 < kSolvePanel ? d - c0 : kSolvePanel;
+        for (int e = tid; e < R * kSolvePanel; e += kSolveThreads) {
+            const int i = e / kSolvePanel;
+            const int c = e - i * kSolvePanel;
+            float v = 0.0f;
+            if (c < width) {
+                const float* p = part + R * R + i * d + c0 + c;
+                for (int ch = 0; ch < chunks; ++ch) {
+                    v += p[ch * stride];
                 }
             }
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                float value = z[i] / root;
-#pragma unroll
-                for (int k = 0; k < i; ++k) {
-                    value -= s_chol[i * LD + k] * z[k];
-                }
-                z[i] = value / s_chol[i * LD + i];
-            }
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                s_panel[i * PLD + tid] = z[i];
-                zbuf[i * d + c0 + tid] = z[i];
-            }
-        }
-        for (int idx = tid; idx < width * R; idx += 64) {
-            const int f = idx / R;
-            const int c = idx - f * R;
-            s_drive[f * LD + c] = drive[(c0 + f) * R + c];
+            s_pa[i * PLD + c] = v / root;
         }
         __syncthreads();
         {
-            const int bi = tid / 8;
-            const int bj = tid - 8 * bi;
-            float acc[kBlock][kBlock];
+            float scol[R];
 #pragma unroll
-            for (int x = 0; x < kBlock; ++x) {
-#pragma unroll
-                for (int y = 0; y < kBlock; ++y) {
-                    acc[x][y] = s_theta[(kBlock * bi + x) * LD + kBlock * bj + y];
-                }
+            for (int k = 0; k < R; ++k) {
+                scol[k] = s_pa[k * PLD + lane];
             }
-            for (int f = 0; f < width; ++f) {
-                float zc[kBlock];
-                float wr[kBlock];
+#pragma unroll 1
+            for (int i = wave; i < R; i += 4) {
+                const float* lrow = s_linv + i * LD;
+                float acc = 0.0f;
 #pragma unroll
-                for (int x = 0; x < kBlock; ++x) {
-                    zc[x] = s_panel[(kBlock * bi + x) * PLD + f];
-                    wr[x] = s_drive[f * LD + kBlock * bj + x];
+                for (int k = 0; k < R; k += 4) {
+                    const f32x4 l4 = *reinterpret_cast<const f32x4*>(lrow + k);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc = fmaf(l4[e], scol[k + e], acc);
+                    }
                 }
-#pragma unroll
-                for (int x = 0; x < kBlock; ++x) {
-#pragma unroll
-                    for (int y = 0; y < kBlock; ++y) {
-                        acc[x][y] = fmaf(zc[x], wr[y], acc[x][y]);
+                s_pb[i * PLD + lane] = acc;
+                if (lane < width) {
+                    zbuf[i * d + c0 + lane] = acc;
+                    if (tape != nullptr) {
+                        tape[4 * R * R + i * d + c0 + lane] = acc;
                     }
                 }
             }
+        }
+        __syncthreads();
+        for (int e = tid; e < kSolvePanel * R / 4; e += kSolveThreads) {
+            const int c = (4 * e) / R;
+            f32x4 w = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (c < width) {
+                w = *reinterpret_cast<const f32x4*>(drive + (c0 + c) * R + (4 * e - c * R));
+            }
+            *reinterpret_cast<f32x4*>(s_pa + 4 * e) = w;
+        }
+        __syncthreads();
 #pragma unroll
-            for (int x = 0; x < kBlock; ++x) {
-#pragma unroll
-                for (int y = 0; y < kBlock; ++y) {
-                    s_theta[(kBlock * bi + x) * LD + kBlock * bj + y] = acc[x][y];
+        for (int t = 0; t < SL::kThetaQuads; ++t) {
+            const int q = tid + t * kSolveThreads;
+            if (q < R * R / 4) {
+                const int i = q / (R / 4);
+                const int j = 4 * (q - i * (R / 4));
+#pragma unroll 8
+                for (int c = 0; c < width; ++c) {
+                    const float z = s_pb[i * PLD + c];
+                    const f32x4 w = *reinterpret_cast<const f32x4*>(s_pa + c * R + j);
+                    theta_acc[t] = z * w + theta_acc[t];
                 }
             }
         }
         __syncthreads();
     }
 
-    // Theta = Theta0 + Z W_drive / sqrt(n); F holds the lower factor.
-    const float* base = a.base + h * R * R;
-    for (int idx = tid; idx < R * R; idx += 64) {
-        const int r = idx / R;
-        const int c = idx - r * R;
-        const float theta = base[idx] + s_theta[r * LD + c] / root;
-        s_theta[r * LD + c] = theta;
-        float factor = 0.0f;
-        if (c < r) {
-            factor = theta;
-        } else if (c == r) {
-            factor = softplus_one(theta);
+    // ---- Theta = Theta0 + acc / sqrt(n); F = tril(Theta, -1) + diag(softplus)
+#pragma unroll
+    for (int t = 0; t < SL::kThetaQuads; ++t) {
+        const int q = tid + t * kSolveThreads;
+        if (q < R * R / 4) {
+            const int i = q / (R / 4);
+            const int j = 4 * (q - i * (R / 4));
+            const f32x4 base = *reinterpret_cast<const f32x4*>(a.base + (h * R + i) * R + j);
+            const f32x4 theta = base + theta_acc[t] / root;
+            *reinterpret_cast<f32x4*>(s_theta + i * LD + j) = theta;
+            if (tape != nullptr) {
+                *reinterpret_cast<f32x4*>(tape + R * R + i * R + j) = theta;
+            }
+            f32x4 factor;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                factor[e] = j + e < i ? theta[e] : 0.0f;
+            }
+            if (j <= i && i < j + 4) {
+                factor[i - j] = softplus_one(theta[i - j]);
+            }
+            *reinterpret_cast<f32x4*>(s_work + i * LD + j) = factor;
         }
-        s_lu[r * LD + c] = factor;
     }
     __syncthreads();
-    // I + K = I + F F^T + Omega with IEEE FP32 products (reference.py:491-497).
-    {
-        float row_values[R];
-        const bool owner = tid < R;
-        if (owner) {
+
+    // ---- I + K = I + F F^T + Omega, IEEE FP32 products (reference.py:491-497);
+    // all R products summed (F is lower triangular, the rest add exact zeros).
 #pragma unroll
-            for (int c = 0; c < R; ++c) {
-                const int limit = c < tid ? c : tid;
-                float sum = 0.0f;
-                for (int k = 0; k <= limit; ++k) {
-                    sum = fmaf(s_lu[tid * LD + k], s_lu[c * LD + k], sum);
+    for (int t = 0; t < SL::kThetaQuads; ++t) {
+        const int q = tid + t * kSolveThreads;
+        if (q < R * R / 4) {
+            const int i = q / (R / 4);
+            const int j = 4 * (q - i * (R / 4));
+            f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+            for (int k = 0; k < R; k += 4) {
+                const f32x4 fi = *reinterpret_cast<const f32x4*>(s_work + i * LD + k);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f32x4 fj = *reinterpret_cast<const f32x4*>(s_work + (j + e) * LD + k);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        sum[e] = fmaf(fi[m], fj[m], sum[e]);
+                    }
                 }
+            }
+            f32x4 value;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = j + e;
                 float skew = 0.0f;
-                if (c > tid) {
-                    skew = s_theta[tid * LD + c];
-                } else if (c < tid) {
-                    skew = -s_theta[c * LD + tid];
+                if (c > i) {
+                    skew = s_theta[i * LD + c];
+                } else if (c < i) {
+                    skew = -s_theta[c * LD + i];
                 }
-                row_values[c] = sum + skew + (c == tid ? 1.0f : 0.0f);
+                value[e] = sum[e] + skew + (c == i ? 1.0f : 0.0f);
             }
-        }
-        __syncthreads();
-        if (owner) {
-            for (int c = 0; c < R; ++c) {
-                s_lu[tid * LD + c] = row_values[c];
-            }
-        }
-        __syncthreads();
-    }
-
-    // LU with partial pivoting (first maximal |a_ik| wins, as LAPACK getrf).
-    for (int k = 0; k < R; ++k) {
-        float value = (tid >= k && tid < R) ? fabsf(s_lu[tid * LD + k]) : -1.0f;
-        int index = tid;
-        wave_argmax(value, index);
-        const int pivot = __shfl(index, 0, 64);
-        if (pivot != k && tid < R) {
-            const float upper = s_lu[k * LD + tid];
-            s_lu[k * LD + tid] = s_lu[pivot * LD + tid];
-            s_lu[pivot * LD + tid] = upper;
-        }
-        if (tid == 0) {
-            s_perm[k] = pivot;
-        }
-        __syncthreads();
-        if (tid > k && tid < R) {
-            const float f = s_lu[tid * LD + k] / s_lu[k * LD + k];
-            s_lu[tid * LD + k] = f;
-            for (int j = k + 1; j < R; ++j) {
-                s_lu[tid * LD + j] -= f * s_lu[k * LD + j];
-            }
-        }
-        __syncthreads();
-    }
-
-    if (a.tape != nullptr) {
-        float* tape = a.tape + system * a.tape_stride;
-        for (int idx = tid; idx < R * R; idx += 64) {
-            const int r = idx / R;
-            const int c = idx - r * R;
-            tape[idx] = s_chol[r * LD + c];
-            tape[R * R + idx] = s_theta[r * LD + c];
-            tape[2 * R * R + idx] = s_lu[r * LD + c];
-        }
-        if (tid < R) {
-            tape[3 * R * R + tid] = static_cast<float>(s_perm[tid]);
+            *reinterpret_cast<f32x4*>(s_sys + i * LD + j) = value;
         }
     }
+    __syncthreads();
 
-    // U = (I + K)^-1 Z, X = 2U - (1 + eta) Z, M' = L^-T X / sqrt(n); one
-    // lane per column, written straight into the apply operand layout.
-    const int64_t blocks = (d + 15) / 16;
-    for (int64_t c0 = 0; c0 < blocks * 16; c0 += kSolvePanel) {
-        const int64_t column = c0 + tid;
-        if (column >= blocks * 16) {
-            continue;
+    // ---- (I + K)^-1 by Gauss-Jordan in wave 0, in place, with implicit row
+    // pivoting: step k picks the largest |a_ik| over rows not yet used (first
+    // row on ties, as the LU partial pivoting it replaces), eliminates column
+    // k from every other row with the unscaled pivot row, and keeps column k
+    // as column p_k of the growing inverse.  Row p_k ends as pi_k times row k
+    // of the inverse with its columns in step order.
+    if (wave == 0) {
+        const bool live = lane < R;
+        LSSO_REG_ROW(rowv);
+        if (live) {
+            row_load(rowv, s_sys + lane * LD);
         }
-        // u holds U, then X = 2U - (1 + eta) Z, then M' in place.
-        float u[R];
-        if (column < d) {
-            float z[R];
+        bool open = live;
+        int own_step = 0;
+        float own_pivot = 1.0f;
+#pragma unroll 1
+        for (int k = 0; k < R; ++k) {
+            float* step_row = smem + SL::kRow + (k & 1) * R;
+            const float x = row_get(rowv, k);
+            const unsigned magnitude = __float_as_uint(fabsf(x));
+            const unsigned best = __builtin_amdgcn_readfirstlane(__ockl_wfred_max_u32(open ? magnitude : 0u));
+            const unsigned long long ties = __ballot(open && magnitude == best);
+            const int p = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(ties)));
+            const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), p));
+            if (lane == p) {
+                row_store(step_row, rowv);
+                open = false;
+                own_step = k;
+                own_pivot = pivot;
+            }
+            if (lane == 0) {
+                s_pivot[k] = p;
+            }
+            wave_lds_order();
+            LSSO_REG_ROW(pivot_row);
+            row_load(pivot_row, step_row);
+            const float f = lane == p ? 0.0f : x / pivot;
+            row_axpy(rowv, f, pivot_row);
+            row_set(rowv, k, lane == p ? 1.0f : -f);
+        }
+        if (live) {
+            row_divide(rowv, own_pivot);
+            row_store(s_work + own_step * LD, rowv);
+        }
+    }
+    __syncthreads();
+    // Column order back to row numbers: inverse[k][p_m] = work[k][m].
+    for (int e = tid; e < R * R; e += kSolveThreads) {
+        const int k = e / R;
+        const int m = e - k * R;
+        s_sys[k * LD + s_pivot[m]] = s_work[k * LD + m];
+    }
+    __syncthreads();
+    if (tape != nullptr) {
+        for (int q = tid; q < R * R / 4; q += kSolveThreads) {
+            const int i = (4 * q) / R;
+            const int j = 4 * q - i * R;
+            *reinterpret_cast<f32x4*>(tape + 2 * R * R + 4 * q) = *reinterpret_cast<const f32x4*>(s_sys + i * LD + j);
+        }
+    }
+
+    // ---- U, X, M' panels, written as apply operand records -----------------
+    const int blocks = (d + 15) / 16;
+    for (int c0 = 0; c0 < blocks * 16; c0 += kSolvePanel) {
+        const int width = d - c0 < kSolvePanel ? d - c0 : kSolvePanel;
+        if (d > kSolvePanel) {
+            for (int e = tid; e < R * kSolvePanel; e += kSolveThreads) {
+                const int i = e / kSolvePanel;
+                const int c = e - i * kSolvePanel;
+                s_pb[i * PLD + c] = c < width ? zbuf[i * d + c0 + c] : 0.0f;
+            }
+            __syncthreads();
+        }
+        {
+            float zcol[R];
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                z[i] = zbuf[i * d + column];
-                s_panel[i * (kSolvePanel + 1) + tid] = z[i];
-            }
             for (int k = 0; k < R; ++k) {
-                const int p = s_perm[k];
-                if (p != k) {
-                    const float swap = s_panel[k * (kSolvePanel + 1) + tid];
-                    s_panel[k * (kSolvePanel + 1) + tid] = s_panel[p * (kSolvePanel + 1) + tid];
-                    s_panel[p * (kSolvePanel + 1) + tid] = swap;
+                zcol[k] = s_pb[k * PLD + lane];
+            }
+#pragma unroll 1
+            for (int i = wave; i < R; i += 4) {
+                const float* irow = s_sys + i * LD;
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < R; k += 4) {
+                    const f32x4 v4 = *reinterpret_cast<const f32x4*>(irow + k);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc = fmaf(v4[e], zcol[k + e], acc);
+                    }
                 }
-            }
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                float value = s_panel[i * (kSolvePanel + 1) + tid];
-#pragma unroll
-                for (int k = 0; k < i; ++k) {
-                    value -= s_lu[i * LD + k] * u[k];
+                if (tape != nullptr && lane < width) {
+                    tape[4 * R * R + R * d + i * d + c0 + lane] = acc;
                 }
-                u[i] = value;
-            }
-#pragma unroll
-            for (int i = R - 1; i >= 0; --i) {
-                float value = u[i];
-#pragma unroll
-                for (int k = i + 1; k < R; ++k) {
-                    value -= s_lu[i * LD + k] * u[k];
-                }
-                u[i] = value / s_lu[i * LD + i];
-            }
-            if (a.tape != nullptr) {
-                float* tape = a.tape + system * a.tape_stride + 3 * R * R + R;
-#pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    tape[i * d + column] = z[i];
-                    tape[R * d + i * d + column] = u[i];
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                u[i] = 2.0f * u[i] - (1.0f + eta) * z[i];
-            }
-#pragma unroll
-            for (int i = R - 1; i >= 0; --i) {
-                float value = u[i];
-#pragma unroll
-                for (int k = i + 1; k < R; ++k) {
-                    value -= s_chol[k * LD + i] * u[k];
-                }
-                u[i] = value / s_chol[i * LD + i];
-            }
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                u[i] = u[i] / root;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                u[i] = 0.0f;
+                s_pa[i * PLD + lane] = 2.0f * acc - (1.0f + eta) * s_pb[i * PLD + lane];
             }
         }
-        // Operand record of (feature block fb, lane g*16 + column%16).
-        const int64_t fb = column / 16;
-        const int lane_low = static_cast<int>(column & 15);
-        uint16_t* record_base = a.mop + ((system * blocks + fb) * 64) * AL::kLaneHalfs;
+        __syncthreads();
+        {
+            float xcol[R];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            uint16_t* record = record_base + (g * 16 + lane_low) * AL::kLaneHalfs;
-#pragma unroll
-            for (int s = 0; s < AL::kSteps32; ++s) {
-#pragma unroll
-                for (int i = 0; i < 8; i += 2) {
-                    uint32_t hi, lo;
-                    split_bf16(u[AL::rank32(s, g, i)], u[AL::rank32(s, g, i + 1)], hi, lo);
-                    *reinterpret_cast<uint32_t*>(record + AL::offset32(s) + i) = hi;
-                    *reinterpret_cast<uint32_t*>(record + AL::offset32(s) + 8 + i) = lo;
-                }
+            for (int k = 0; k < R; ++k) {
+                xcol[k] = s_pa[k * PLD + lane];
             }
+#pragma unroll 1
+            for (int i = wave; i < R; i += 4) {
+                const float* trow = s_linvt + i * LD;
+                float acc = 0.0f;
 #pragma unroll
-            for (int s = 0; s < AL::kSteps16; ++s) {
+                for (int k = 0; k < R; k += 4) {
+                    const f32x4 v4 = *reinterpret_cast<const f32x4*>(trow + k);
 #pragma unroll
-                for (int i = 0; i < 4; i += 2) {
-                    uint32_t hi, lo;
-                    split_bf16(u[AL::rank16(s, g, i)], u[AL::rank16(s, g, i + 1)], hi, lo);
-                    *reinterpret_cast<uint32_t*>(record + AL::offset16(s) + i) = hi;
-                    *reinterpret_cast<uint32_t*>(record + AL::offset16(s) + 4 + i) = lo;
+                    for (int e = 0; e < 4; ++e) {
+                        acc = fmaf(v4[e], xcol[k + e], acc);
+                    }
+                }
+                s_pb[i * PLD + lane] = lane < width ? acc / root : 0.0f;
+            }
+        }
+        __syncthreads();
+        {
+            // Record of feature block fb, lane g4 * 16 + column % 16.
+            const int fb_local = tid >> 6;
+            const int fb = c0 / 16 + fb_local;
+            if (fb < blocks) {
+                const int g4 = lane >> 4;
+                const int column = fb_local * 16 + (lane & 15);
+                uint16_t* record = a.mop + ((system * blocks + fb) * 64 + lane) * AL::kLaneHalfs;
+#pragma unroll
+                for (int st = 0; st < AL::kSteps32; ++st) {
+#pragma unroll
+                    for (int i = 0; i < 8; i += 2) {
+                        uint32_t hi, lo;
+                        split_bf16(s_pb[AL::rank32(st, g4, i) * PLD + column],
+                                   s_pb[AL::rank32(st, g4, i + 1) * PLD + column], hi, lo);
+                        *reinterpret_cast<uint32_t*>(record + AL::offset32(st) + i) = hi;
+                        *reinterpret_cast<uint32_t*>(record + AL::offset32(st) + 8 + i) = lo;
+                    }
+                }
+#pragma unroll
+                for (int st = 0; st < AL::kSteps16; ++st) {
+#pragma unroll
+                    for (int i = 0; i < 4; i += 2) {
+                        uint32_t hi, lo;
+                        split_bf16(s_pb[AL::rank16(st, g4, i) * PLD + column],
+                                   s_pb[AL::rank16(st, g4, i + 1) * PLD + column], hi, lo);
+                        *reinterpret_cast<uint32_t*>(record + AL::offset16(st) + i) = hi;
+                        *reinterpret_cast<uint32_t*>(record + AL::offset16(st) + 4 + i) = lo;
+                    }
                 }
             }
         }
+        __syncthreads();
     }
 }
 
@@ -942,10 +1151,10 @@ hipError_t launch_reduce(int rank, const ReduceArgs& a, int cpw, bool vec, hipSt
 hipError_t launch_solve(int rank, const SolveArgs& a, int64_t systems, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(systems));
     switch (rank) {
-        case 16: solve_kernel<16><<<grid, 64, 0, stream>>>(a); break;
-        case 32: solve_kernel<32><<<grid, 64, 0, stream>>>(a); break;
-        case 48: solve_kernel<48><<<grid, 64, 0, stream>>>(a); break;
-        default: solve_kernel<64><<<grid, 64, 0, stream>>>(a); break;
+        case 16: solve_kernel<16><<<grid, kSolveThreads, 0, stream>>>(a); break;
+        case 32: solve_kernel<32><<<grid, kSolveThreads, 0, stream>>>(a); break;
+        case 48: solve_kernel<48><<<grid, kSolveThreads, 0, stream>>>(a); break;
+        default: solve_kernel<64><<<grid, kSolveThreads, 0, stream>>>(a); break;
     }
     return hipGetLastError();
 }
