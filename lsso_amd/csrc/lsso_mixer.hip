@@ -343,6 +343,7 @@ struct SolveLayout {
     static constexpr int kChunks = R / 16;         // 16-float register chunks per row
     static constexpr bool kSplit = R <= 32;        // Cholesky rows and L^-1 rows on separate lanes
     static constexpr int kThetaQuads = (R * R / 4 + kSolveThreads - 1) / kSolveThreads;
+    static constexpr int kChunkBatch = R <= 32 ? 8 : 4;    // chunk loads in flight per element
     static constexpr int kLinv = 0;                       // L^-1 rows
     static constexpr int kLinvT = kLinv + R * kLD;        // L^-1 transposed
     static constexpr int kTheta = kLinvT + R * kLD;       // Theta
@@ -453,15 +454,10 @@ __device__ __forceinline__ void row_axpy(const RegRow<Q>& r, float f, const RegR
 }
 
 template <int Q, int q = 0>
-__device__ __forceinline__ void row_divide(const RegRow<Q>& r, float divisor) {
+__device__ __forceinline__ void row_scale(const RegRow<Q>& r, float factor) {
     if constexpr (q < Q) {
-        f32x16 t = r.template at<q>();
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            t[e] = t[e] / divisor;
-        }
-        r.template at<q>() = t;
-        row_divide<Q, q + 1>(r, divisor);
+        r.template at<q>() = r.template at<q>() * factor;
+        row_scale<Q, q + 1>(r, factor);
     }
 }
 
@@ -535,20 +531,52 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
     const float* part = a.partials + system * chunks * stride;
     float* tape = a.tape != nullptr ? a.tape + system * a.tape_stride : nullptr;
 
-    // ---- A = G / n + I; chunk partials summed in ascending order ----------
-    for (int q = tid; q < R * R / 4; q += kSolveThreads) {
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int ch = 0; ch < chunks; ++ch) {
-            acc += *reinterpret_cast<const f32x4*>(part + ch * stride + 4 * q);
-        }
-        const int i = (4 * q) / R;
-        const int j = 4 * q - i * R;
-        f32x4 value;
+    // ---- A = G / n + I; chunk partials summed in ascending order, each
+    // thread keeping kChunkBatch chunks of loads in flight --------------------
+    {
+        constexpr int kQuads = (R * R / 4 + kSolveThreads - 1) / kSolveThreads;
+        f32x4 acc[kQuads];
+        const float* src[kQuads];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            value[e] = acc[e] / count + (j + e == i ? 1.0f : 0.0f);
+        for (int t = 0; t < kQuads; ++t) {
+            const int q = tid + t * kSolveThreads;
+            acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            src[t] = part + 4 * (q < R * R / 4 ? q : 0);
         }
-        *reinterpret_cast<f32x4*>(s_work + i * LD + j) = value;
+        for (int ch0 = 0; ch0 < chunks; ch0 += SL::kChunkBatch) {
+            f32x4 v[kQuads][SL::kChunkBatch];
+#pragma unroll
+            for (int t = 0; t < kQuads; ++t) {
+#pragma unroll
+                for (int u = 0; u < SL::kChunkBatch; ++u) {
+                    const int ch = ch0 + u < chunks ? ch0 + u : chunks - 1;
+                    v[t][u] = *reinterpret_cast<const f32x4*>(src[t] + ch * stride);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < kQuads; ++t) {
+#pragma unroll
+                for (int u = 0; u < SL::kChunkBatch; ++u) {
+                    if (ch0 + u < chunks) {
+                        acc[t] += v[t][u];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kQuads; ++t) {
+            const int q = tid + t * kSolveThreads;
+            if (q < R * R / 4) {
+                const int i = (4 * q) / R;
+                const int j = 4 * q - i * R;
+                f32x4 value;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    value[e] = acc[t][e] / count + (j + e == i ? 1.0f : 0.0f);
+                }
+                *reinterpret_cast<f32x4*>(s_work + i * LD + j) = value;
+            }
+        }
     }
     __syncthreads();
 
@@ -574,12 +602,14 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
                 row_identity(carry, row);
             }
         }
-        float own_root = 1.0f;
+        float own_inv_root = 1.0f;
 #pragma unroll 1
         for (int k = 0; k < R; ++k) {
             float* column = smem + SL::kColumn + (k & 1) * 64;
             float* step_row = smem + SL::kRow + (k & 1) * R;
             const float x = row_get(work, k);
+            // a_kk straight from lane k; only the column and row k go through LDS.
+            const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
             if (!inverse_lane) {
                 column[row] = row >= k ? x : 0.0f;
             }
@@ -591,9 +621,14 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
                 }
             }
             wave_lds_order();
-            const float pivot = column[k];
-            const float own = column[row];
-            const float f = row > k ? own / pivot : 0.0f;
+            // Pivots of A = G/n + I are >= 1, so the hardware reciprocal,
+            // square root and reciprocal square root (1 ulp) need no range
+            // handling.
+            const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
+            const float inv_root = __builtin_amdgcn_rsqf(pivot);
+            const float root_pivot = __builtin_amdgcn_sqrtf(pivot);
+            const float own = inverse_lane ? column[row] : x;
+            const float f = row > k ? own * inv_pivot : 0.0f;
             LSSO_REG_ROW(source);
             row_load(source, kSplit && inverse_lane ? step_row : column);
             row_axpy(work, f, source);
@@ -602,16 +637,15 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
                 row_load(aug, step_row);
                 row_axpy(carry, f, aug);
             }
-            const float root_pivot = sqrtf(pivot);
             if (!inverse_lane) {
-                row_set(work, k, row > k ? x / root_pivot : (row == k ? root_pivot : 0.0f));
+                row_set(work, k, row > k ? x * inv_root : (row == k ? root_pivot : 0.0f));
             }
-            own_root = row == k ? root_pivot : own_root;
+            own_inv_root = row == k ? inv_root : own_inv_root;
         }
         if (live) {
             const RegRow<Q>& inverse = kSplit ? work : carry;
             if (!kSplit || inverse_lane) {
-                row_divide(inverse, own_root);
+                row_scale(inverse, own_inv_root);
                 row_store(s_linv + row * LD, inverse);
                 row_store_column(s_linvt, LD, row, inverse);
                 if (tape != nullptr) {
@@ -635,17 +669,41 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
     }
     for (int c0 = 0; c0 < d; c0 += kSolvePanel) {
         const int width = d - c0 < kSolvePanel ? d - c0 : kSolvePanel;
-        for (int e = tid; e < R * kSolvePanel; e += kSolveThreads) {
-            const int i = e / kSolvePanel;
-            const int c = e - i * kSolvePanel;
-            float v = 0.0f;
-            if (c < width) {
-                const float* p = part + R * R + i * d + c0 + c;
-                for (int ch = 0; ch < chunks; ++ch) {
-                    v += p[ch * stride];
+        {
+            // S panel: thread (row wave + 4 t, column lane); columns past the
+            // panel width load a clamped column and store zero.
+            constexpr int kRows = R / 4;
+            const int c = lane < width ? lane : width - 1;
+            float acc[kRows];
+#pragma unroll
+            for (int t = 0; t < kRows; ++t) {
+                acc[t] = 0.0f;
+            }
+            const float* src = part + R * R + wave * d + c0 + c;
+            for (int ch0 = 0; ch0 < chunks; ch0 += SL::kChunkBatch) {
+                float v[kRows][SL::kChunkBatch];
+#pragma unroll
+                for (int t = 0; t < kRows; ++t) {
+#pragma unroll
+                    for (int u = 0; u < SL::kChunkBatch; ++u) {
+                        const int ch = ch0 + u < chunks ? ch0 + u : chunks - 1;
+                        v[t][u] = src[ch * stride + 4 * t * d];
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < kRows; ++t) {
+#pragma unroll
+                    for (int u = 0; u < SL::kChunkBatch; ++u) {
+                        if (ch0 + u < chunks) {
+                            acc[t] += v[t][u];
+                        }
+                    }
                 }
             }
-            s_pa[i * PLD + c] = v / root;
+#pragma unroll
+            for (int t = 0; t < kRows; ++t) {
+                s_pa[(wave + 4 * t) * PLD + lane] = lane < width ? acc[t] / root : 0.0f;
+            }
         }
         __syncthreads();
         {
@@ -790,6 +848,7 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
             const unsigned long long ties = __ballot(open && magnitude == best);
             const int p = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(ties)));
             const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), p));
+            const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
             if (lane == p) {
                 row_store(step_row, rowv);
                 open = false;
@@ -802,12 +861,12 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
             wave_lds_order();
             LSSO_REG_ROW(pivot_row);
             row_load(pivot_row, step_row);
-            const float f = lane == p ? 0.0f : x / pivot;
+            const float f = lane == p ? 0.0f : x * inv_pivot;
             row_axpy(rowv, f, pivot_row);
             row_set(rowv, k, lane == p ? 1.0f : -f);
         }
         if (live) {
-            row_divide(rowv, own_pivot);
+            row_scale(rowv, __builtin_amdgcn_rcpf(own_pivot));
             row_store(s_work + own_step * LD, rowv);
         }
     }
