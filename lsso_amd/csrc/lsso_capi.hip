@@ -343,7 +343,7 @@ int lsso_hip_linear(const void* x, int x_dtype, int64_t rows, int64_t in_feature
     args.tiles = ceil_div(rows, lsso_hip::linear_tile_rows());
     args.column_groups = ceil_div(out_features, lsso_hip::linear_columns_per_group(tier));
     args.x_vector = (in_features % 8 == 0 && x_row_stride % 8 == 0 && aligned(x, 16)) ? 1 : 0;
-    args.y_vector = (out_features % 4 == 0 && aligned(y, 8)) ? 1 : 0;
+    args.y_vector = (out_features % 8 == 0 && aligned(y, 16)) ? 1 : 0;
     int64_t groups = units / args.column_groups;
     if (groups < 1) groups = 1;
     if (groups > args.tiles) groups = args.tiles;

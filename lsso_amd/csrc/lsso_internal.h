@@ -87,7 +87,7 @@ struct LinearArgs {
     int64_t tiles;              // ceil(rows / tile_rows)
     int64_t column_groups;
     int x_vector;               // 16-byte x loads are legal
-    int y_vector;               // 8-byte y stores are legal
+    int y_vector;               // 16-byte y stores are legal
 };
 
 hipError_t launch_phase(const PhaseArgs& a, hipStream_t stream);

@@ -12,7 +12,8 @@
 // shared by the workgroup's waves.
 // The MFMA computes y^T = W x^T on v_mfma_f32_32x32x16_bf16; in that form a
 // lane's accumulators are 4 runs of 4 consecutive output features of one
-// row, stored as 8-byte writes.
+// row.  The rounded tile is staged in LDS and written back in 16-byte pieces
+// of whole row segments (scattered 8-byte writes cost half the store rate).
 
 #include "lsso_device.h"
 #include "lsso_internal.h"
@@ -21,6 +22,7 @@
 namespace lsso_hip {
 
 constexpr int kLinearTileRows = 64;
+constexpr int kXcds = 8;   // accelerator complex dies of an MI355X
 
 // Waves per workgroup: eight (two per SIMD, 256 registers each) while the
 // resident W slice fits; four once K exceeds 256.
@@ -40,32 +42,18 @@ int linear_k_tier(int64_t in_features) {
     return 0;
 }
 
-// Load 8 consecutive x elements as BF16.  Out-of-range rows and columns read
-// a clamped in-bounds address and are zeroed by select, so the tile load has
-// no divergent branches.
+// Load 8 consecutive x elements as BF16 one element at a time (rows whose
+// length or stride rules out 16-byte loads).  Out-of-range rows and columns
+// read a clamped in-bounds address and are zeroed by select.  Masked rows are
+// loaded like any other: the output rows they feed are zeroed in the epilogue.
 template <int XT>
-__device__ __forceinline__ u32x4 load_x_chunk(const LinearArgs& a, int64_t row, int64_t k0) {
+__device__ __forceinline__ u32x4 load_x_chunk_scalar(const LinearArgs& a, int64_t row, int64_t k0) {
     const int64_t safe_row = row < a.rows ? row : a.rows - 1;
-    const bool row_live = row < a.rows && (a.row_mask == nullptr || a.row_mask[safe_row] != 0);
     const uint16_t* x = static_cast<const uint16_t*>(a.x) + safe_row * a.x_stride;
-    u32x4 out;
-    if (a.x_vector) {
-        const bool live = row_live && k0 < a.in_features;
-        const u32x4 raw = *reinterpret_cast<const u32x4*>(x + (live ? k0 : 0));
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            uint32_t value = raw[p];
-            if constexpr (XT == LSSO_HIP_F16) {
-                value = pack_bf16(f16_lo(value), f16_hi(value));
-            }
-            out[p] = live ? value : 0u;
-        }
-        return out;
-    }
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const bool live = row_live && k0 + i < a.in_features;
+        const bool live = row < a.rows && k0 + i < a.in_features;
         const uint16_t bits = x[live ? k0 + i : 0];
         float value;
         if constexpr (XT == LSSO_HIP_BF16) {
@@ -75,9 +63,49 @@ __device__ __forceinline__ u32x4 load_x_chunk(const LinearArgs& a, int64_t row, 
         }
         v[i] = live ? value : 0.0f;
     }
+    u32x4 out;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         out[p] = pack_bf16(v[2 * p], v[2 * p + 1]);
+    }
+    return out;
+}
+
+// A staged x chunk: raw bits as loaded plus their liveness, so that the
+// loads of the next tile stay in flight while the current tile is multiplied
+// and only their conversion waits for them.
+struct XChunk {
+    u32x4 raw;
+    int live;
+};
+
+template <int XT, bool XVEC>
+__device__ __forceinline__ XChunk fetch_x_chunk(const LinearArgs& a, int64_t row, int64_t k0) {
+    XChunk c;
+    if constexpr (XVEC) {
+        const bool in_range = row < a.rows && k0 < a.in_features;
+        const int64_t safe_row = row < a.rows ? row : a.rows - 1;
+        const uint16_t* x = static_cast<const uint16_t*>(a.x) + safe_row * a.x_stride;
+        c.raw = *reinterpret_cast<const u32x4*>(x + (in_range ? k0 : 0));
+        c.live = in_range;
+    } else {
+        c.raw = load_x_chunk_scalar<XT>(a, row, k0);
+        c.live = 1;
+    }
+    return c;
+}
+
+// BF16 bits of a staged chunk (zero outside the matrix).
+template <int XT, bool XVEC>
+__device__ __forceinline__ u32x4 finish_x_chunk(const XChunk& c) {
+    u32x4 out;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        uint32_t value = c.raw[p];
+        if constexpr (XVEC && XT == LSSO_HIP_F16) {
+            value = pack_bf16(f16_lo(value), f16_hi(value));
+        }
+        out[p] = c.live ? value : 0u;
     }
     return out;
 }
@@ -91,7 +119,7 @@ __device__ __forceinline__ uint16_t to_output_bits(float value) {
     }
 }
 
-template <int KSTEPS, int XT, int YT>
+template <int KSTEPS, int XT, int YT, bool XVEC>
 __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(LinearArgs a) {
     constexpr int kWaves = linear_waves<KSTEPS>();
     constexpr int kGroupColumns = kWaves * 32;
@@ -102,13 +130,28 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     static_assert(kLinearTileRows * kChunksPerRow % kThreads == 0, "tile split");
     __shared__ __attribute__((aligned(16))) uint16_t s_x[2][kLinearTileRows * KP];
     __shared__ __attribute__((aligned(16))) float s_bias[kGroupColumns];
+    constexpr int YP = kGroupColumns + 8;                 // staged output row pitch
+    constexpr int kStoreChunks = kLinearTileRows * kGroupColumns / 8 / kThreads;
+    static_assert(kLinearTileRows * kGroupColumns / 8 % kThreads == 0, "store split");
+    __shared__ __attribute__((aligned(16))) uint16_t s_y[kLinearTileRows * YP];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int half = lane >> 5;
-    const int64_t cg = blockIdx.x % a.column_groups;
-    const int64_t group_index = blockIdx.x / a.column_groups;
+    // Workgroups are dealt to the eight XCDs round-robin by block index.  When
+    // the grid allows, the column groups of one row tile are given to blocks
+    // of the same XCD, so the second read of each x tile hits that XCD's L2.
+    int64_t cg, group_index;
+    if (gridDim.x % (kXcds * a.column_groups) == 0) {
+        const int64_t xcd = blockIdx.x % kXcds;
+        const int64_t slot = blockIdx.x / kXcds;
+        cg = slot % a.column_groups;
+        group_index = (slot / a.column_groups) * kXcds + xcd;
+    } else {
+        cg = blockIdx.x % a.column_groups;
+        group_index = blockIdx.x / a.column_groups;
+    }
     const int64_t group_count = gridDim.x / a.column_groups;
     const int64_t n0 = cg * kGroupColumns + wave * 32;
     const int64_t K = a.in_features;
@@ -156,14 +199,14 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         s_bias[c] = (a.bias != nullptr && n < N) ? a.bias[n] : 0.0f;
     }
 
-    u32x4 stage[kChunksPerThread];
+    XChunk stage[kChunksPerThread];
     auto load_stage = [&](int64_t tile) {
 #pragma unroll
         for (int c = 0; c < kChunksPerThread; ++c) {
             const int chunk = tid + c * kThreads;
             const int rr = chunk / kChunksPerRow;
             const int cc = chunk - rr * kChunksPerRow;
-            stage[c] = load_x_chunk<XT>(a, tile * kLinearTileRows + rr, 8 * cc);
+            stage[c] = fetch_x_chunk<XT, XVEC>(a, tile * kLinearTileRows + rr, 8 * cc);
         }
     };
     auto write_stage = [&](int buf) {
@@ -172,7 +215,7 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
             const int chunk = tid + c * kThreads;
             const int rr = chunk / kChunksPerRow;
             const int cc = chunk - rr * kChunksPerRow;
-            *reinterpret_cast<u32x4*>(&s_x[buf][rr * KP + 8 * cc]) = stage[c];
+            *reinterpret_cast<u32x4*>(&s_x[buf][rr * KP + 8 * cc]) = finish_x_chunk<XT, XVEC>(stage[c]);
         }
     };
 
@@ -185,6 +228,16 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     int buf = 0;
     for (; tile < a.tiles; tile += group_count) {
         const int64_t next = tile + group_count;
+        // Memory operations complete in issue order as far as the wait
+        // counter is concerned, so the order below matters: the row mask
+        // bytes (needed first) are requested before the next tile's x, and the
+        // next tile's x is consumed before this tile's y stores are issued.
+        bool keep[2];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int64_t m = tile * kLinearTileRows + mb * 32 + (lane & 31);
+            keep[mb] = m < a.rows && (a.row_mask == nullptr || a.row_mask[m < a.rows ? m : 0] != 0);
+        }
         if (next < a.tiles) {
             load_stage(next);
         }
@@ -227,70 +280,90 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
             __builtin_amdgcn_sched_barrier(0);
         }
         // y^T block: lane holds row m = lane%32 of the 32-row block and
-        // features n0 + 8 q + 4 half + r for q, r in 0..3.
+        // features n0 + 8 q + 4 half + r for q, r in 0..3.  The tile is
+        // rounded and staged in LDS, then written back row by row so that
+        // each store instruction covers whole contiguous row segments.
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
-            const int64_t m = tile * kLinearTileRows + mb * 32 + (lane & 31);
-            if (m < a.rows) {
-                const bool keep = a.row_mask == nullptr || a.row_mask[m] != 0;
-                uint16_t* yrow = static_cast<uint16_t*>(a.y) + m * N;
+            const int mr = mb * 32 + (lane & 31);
 #pragma unroll
-                for (int qd = 0; qd < 4; ++qd) {
-                    const int64_t n = n0 + 8 * qd + 4 * half;
-                    const f32x4 bias = *reinterpret_cast<const f32x4*>(
-                        &s_bias[wave * 32 + 8 * qd + 4 * half]);
-                    const float v0 = keep ? acc[mb][4 * qd + 0] + bias[0] : 0.0f;
-                    const float v1 = keep ? acc[mb][4 * qd + 1] + bias[1] : 0.0f;
-                    const float v2 = keep ? acc[mb][4 * qd + 2] + bias[2] : 0.0f;
-                    const float v3 = keep ? acc[mb][4 * qd + 3] + bias[3] : 0.0f;
-                    if (a.y_vector && n + 3 < N) {
-                        u32x2 packed;
-                        if constexpr (YT == LSSO_HIP_BF16) {
-                            packed.x = pack_bf16(v0, v1);
-                            packed.y = pack_bf16(v2, v3);
-                        } else {
-                            packed.x = pack_f16(v0, v1);
-                            packed.y = pack_f16(v2, v3);
-                        }
-                        *reinterpret_cast<u32x2*>(yrow + n) = packed;
+            for (int qd = 0; qd < 4; ++qd) {
+                const int c = wave * 32 + 8 * qd + 4 * half;
+                const f32x4 bias = *reinterpret_cast<const f32x4*>(&s_bias[c]);
+                const float v0 = keep[mb] ? acc[mb][4 * qd + 0] + bias[0] : 0.0f;
+                const float v1 = keep[mb] ? acc[mb][4 * qd + 1] + bias[1] : 0.0f;
+                const float v2 = keep[mb] ? acc[mb][4 * qd + 2] + bias[2] : 0.0f;
+                const float v3 = keep[mb] ? acc[mb][4 * qd + 3] + bias[3] : 0.0f;
+                u32x2 packed;
+                if constexpr (YT == LSSO_HIP_BF16) {
+                    packed.x = pack_bf16(v0, v1);
+                    packed.y = pack_bf16(v2, v3);
+                } else {
+                    packed.x = pack_f16(v0, v1);
+                    packed.y = pack_f16(v2, v3);
+                }
+                *reinterpret_cast<u32x2*>(&s_y[mr * YP + c]) = packed;
+            }
+        }
+        __syncthreads();
+        if (next < a.tiles) {
+            write_stage(buf ^ 1);
+        }
+        {
+            const int64_t col0 = cg * kGroupColumns;
+#pragma unroll
+            for (int i = 0; i < kStoreChunks; ++i) {
+                const int chunk = tid + i * kThreads;
+                const int mr = chunk / (kGroupColumns / 8);
+                const int c8 = 8 * (chunk - mr * (kGroupColumns / 8));
+                const int64_t m = tile * kLinearTileRows + mr;
+                const int64_t n = col0 + c8;
+                if (m < a.rows && n < N) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(&s_y[mr * YP + c8]);
+                    uint16_t* dst = static_cast<uint16_t*>(a.y) + m * N + n;
+                    if (a.y_vector) {
+                        *reinterpret_cast<u32x4*>(dst) = v;
                     } else {
-                        const float v[4] = {v0, v1, v2, v3};
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
+                        for (int r = 0; r < 8; ++r) {
                             if (n + r < N) {
-                                yrow[n + r] = to_output_bits<YT>(v[r]);
+                                dst[r] = static_cast<uint16_t>(v[r >> 1] >> (16 * (r & 1)));
                             }
                         }
                     }
                 }
             }
         }
-        if (next < a.tiles) {
-            write_stage(buf ^ 1);
-        }
         __syncthreads();
         buf ^= 1;
     }
 }
 
-template <int KSTEPS>
-static hipError_t launch_linear_k(const LinearArgs& a, int x_dtype, int y_dtype, dim3 grid,
-                                  hipStream_t stream) {
+template <int KSTEPS, bool XVEC>
+static hipError_t launch_linear_kv(const LinearArgs& a, int x_dtype, int y_dtype, dim3 grid,
+                                   hipStream_t stream) {
     const dim3 block(linear_waves<KSTEPS>() * 64);
     if (x_dtype == LSSO_HIP_F16) {
         if (y_dtype == LSSO_HIP_F16) {
-            linear_kernel<KSTEPS, LSSO_HIP_F16, LSSO_HIP_F16><<<grid, block, 0, stream>>>(a);
+            linear_kernel<KSTEPS, LSSO_HIP_F16, LSSO_HIP_F16, XVEC><<<grid, block, 0, stream>>>(a);
         } else {
-            linear_kernel<KSTEPS, LSSO_HIP_F16, LSSO_HIP_BF16><<<grid, block, 0, stream>>>(a);
+            linear_kernel<KSTEPS, LSSO_HIP_F16, LSSO_HIP_BF16, XVEC><<<grid, block, 0, stream>>>(a);
         }
     } else {
         if (y_dtype == LSSO_HIP_F16) {
-            linear_kernel<KSTEPS, LSSO_HIP_BF16, LSSO_HIP_F16><<<grid, block, 0, stream>>>(a);
+            linear_kernel<KSTEPS, LSSO_HIP_BF16, LSSO_HIP_F16, XVEC><<<grid, block, 0, stream>>>(a);
         } else {
-            linear_kernel<KSTEPS, LSSO_HIP_BF16, LSSO_HIP_BF16><<<grid, block, 0, stream>>>(a);
+            linear_kernel<KSTEPS, LSSO_HIP_BF16, LSSO_HIP_BF16, XVEC><<<grid, block, 0, stream>>>(a);
         }
     }
     return hipGetLastError();
+}
+
+template <int KSTEPS>
+static hipError_t launch_linear_k(const LinearArgs& a, int x_dtype, int y_dtype, dim3 grid,
+                                  hipStream_t stream) {
+    return a.x_vector ? launch_linear_kv<KSTEPS, true>(a, x_dtype, y_dtype, grid, stream)
+                      : launch_linear_kv<KSTEPS, false>(a, x_dtype, y_dtype, grid, stream);
 }
 
 hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,
