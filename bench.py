@@ -1,9 +1,9 @@
 """Benchmark the complete LSSO mixer forward on one MI355X.
 
-Workload (BASELINE.json metric "mixer fwd tokens/s @B64 D256 H8 r32 L4096
-fp16"): LSSO(LSSOConfig(256, 8, 32, bias=True)) with seeded random
-compact-core parameters, x ~ N(0, 1) FP16 [64, 4096, 256], shared default
-positions, no mask.  One step is one forward x -> y including both
+Workload (metric "mixer fwd tokens/s @B64 D256 H8 r32 L4096 fp16"):
+LSSO(LSSOConfig(256, 8, 32, bias=True)) with seeded random compact-core
+parameters, x ~ N(0, 1) FP16 [64, 4096, 256], shared default positions, no
+mask.  One step is one forward x -> y including both
 projections (reference protocol: benchmarks/benchmark_ball.py:156-208).
 
 Prints one JSON line with the driver's fields plus
@@ -25,6 +25,9 @@ import time
 import torch
 
 HBM_PEAK_GBPS = 8000.0
+# Reference native CUDA forward at this exact shell: 10.135 ms per batch of
+# 64 x 4096 tokens on one RTX 5070 Ti (results/cuda/wall_clock.csv:4).
+REFERENCE_TOKENS_PER_S = 64 * 4096 / 10.135e-3
 
 
 def parse_args() -> argparse.Namespace:
@@ -34,10 +37,34 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--batch", type=int, default=64)
     parser.add_argument("--length", type=int, default=4096)
-    parser.add_argument("--cpu-samples", type=int, default=8,
+    parser.add_argument("--cpu-samples", type=int, default=64,
                         help="sequences of the workload timed on the CPU oracle (0 skips)")
-    parser.add_argument("--cpu-repeats", type=int, default=3)
+    parser.add_argument("--cpu-repeats", type=int, default=7)
+    parser.add_argument("--copy-mib", type=int, default=0,
+                        help="after the timed region, run one device copy of this many MiB "
+                             "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return parser.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "mixer_forward_c3_l4096_hbm_traffic.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` at the headline workload, from the
+    calibrated rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under
+    profiles/ (None when the summary has no line for it)."""
+
+    try:
+        with open(TRAFFIC_FILE) as handle:
+            for line in handle:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    name, _, value = line.split(":", 1)[1].rpartition("=")
+                    if name.strip() == kernel:
+                        return float(value)
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> dict:
@@ -145,6 +172,14 @@ def main() -> int:
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
 
+    if args.copy_mib > 0:
+        source = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=device).fill_(1)
+        target = torch.empty_like(source)
+        torch.cuda.synchronize()
+        target.copy_(source)
+        torch.cuda.synchronize()
+        del source, target
+
     ms_per_step = 1e3 * elapsed / args.steps
     tokens = batch * length
     value = tokens * args.steps / elapsed
@@ -155,6 +190,10 @@ def main() -> int:
     projection_bytes = tokens * (dim * 2 + width * 2) + width * dim * 4 + width * 4
     achieved = projection_bytes / (projection_ms * 1e-3) / 1e9
     chain_bytes = tokens * 5120
+    k_tier = next(t for t in (4, 8, 12, 16, 24, 32) if dim <= 16 * t)
+    projection_kernel = f"lsso_hip::linear_kernel<{k_tier}, 1, 2, true>"
+    headline = (batch, length) == (64, 4096)
+    traffic = measured_traffic(projection_kernel) if headline else None
     result = {
         "metric": "mixer fwd tokens/s @B64 D256 H8 r32 L4096 fp16; % HBM roofline",
         "value": value,
@@ -165,7 +204,7 @@ def main() -> int:
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": value / REFERENCE_TOKENS_PER_S if headline else None,
         "dtype": "bf16",
         "data": "synthetic: x ~ N(0,1) fp16, seeded random-init weights",
         "config": {
@@ -183,12 +222,14 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "linear_kernel (input projection x -> packed)",
+            "kernel": projection_kernel + " (input projection x -> packed)",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": ("profiles/mixer_forward_c3_l4096_hbm_traffic.md (rocprofv3 FETCH_SIZE + "
+                               "WRITE_SIZE, copy-calibrated)") if traffic is not None else None,
             "avg_ms": projection_ms,
         },
     }

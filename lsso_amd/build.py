@@ -24,9 +24,10 @@ OFFLOAD_ARCH = "gfx950"
 LIBRARY_NAME = f"liblsso_hip_{OFFLOAD_ARCH}.so"
 SOURCES = ("lsso_capi.hip", "lsso_mixer.hip", "lsso_linear.hip")
 
-# Packed FP32 VALU forms are disabled for all device code (see DESIGN.md's
-# build section for the reason); hipcc's host pass warns that it does not
-# know the feature, which is harmless.
+# Packed FP32 VALU forms (v_pk_add/mul/fma_f32) are disabled for all device
+# code: some of their forms have returned wrong results on the MI355X boxes
+# this library is tested on, without any error.  hipcc's host pass warns that
+# it does not know the feature, which is harmless.
 DEVICE_FLAGS = (
     f"--offload-arch={OFFLOAD_ARCH}",
     "-O3",

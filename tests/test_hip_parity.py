@@ -348,7 +348,7 @@ def test_module_c1_config_matches_reference_golden(native) -> None:
 
 @pytest.mark.parametrize("length", (1024, 4096))
 def test_headline_shell_slice_matches_oracle(native, length: int) -> None:
-    """B=64, D=256, H=8, r=32, FP16 (BASELINE configs C2/C3): the full batch
+    """B=64, D=256, H=8, r=32, FP16 (the L=1024 and L=4096 benchmark shells): the full batch
     runs on the GPU; samples 0, 17 and 63 are checked against the FP64
     oracle, and the full batch is checked for determinism."""
 
