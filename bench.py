@@ -141,9 +141,10 @@ def main() -> int:
     w_o, b_o = layer.w_o.weight, layer.w_o.bias
     base, drive, eta_raw = layer.core_base_raw, layer.core_drive_weight, layer.eta_raw
 
-    # The step is exactly the module's native forward for an unmasked input
-    # with default positions (lsso_amd/ball/model.py, _forward_native),
-    # unrolled so that events bracket the input projection.
+    # The step is exactly the module's native inference forward for an
+    # unmasked input with default positions (lsso_amd/ball/model.py,
+    # _forward_native): input projection, then the mixer fused with the output
+    # projection; unrolled so that events bracket the input projection.
     events = []
 
     def step(record: bool) -> torch.Tensor:
@@ -154,8 +155,7 @@ def main() -> int:
         if record:
             stop.record()
             events.append((start, stop))
-        mixed = hip.fast_mix(projected, base, drive, eta_raw)
-        return hip.linear(mixed, w_o, b_o, x.dtype)
+        return hip.mix_project(projected, base, drive, eta_raw, None, None, w_o, b_o, x.dtype)
 
     with torch.inference_mode():
         reference_out = layer(x, implementation="hip")

@@ -109,6 +109,44 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape,
                            size_t workspace_bytes,
                            void* stream);
 
+/* 1 if lsso_hip_mixer_forward_projected handles this shape, 0 if not (use
+ * lsso_hip_mixer_forward followed by lsso_hip_linear), or a negative code for
+ * an invalid shape.  The fused path covers heads <= 8, head_dim a multiple of
+ * 16 up to 64, heads*head_dim <= 256 and heads*(rank+head_dim) <= 512.
+ * Replaces: the choice between the native mixer and its output projection
+ * in LSSO._forward_cuda (lsso/ball/model.py:389-405). */
+int lsso_hip_mixer_projected_supported(const lsso_hip_mixer_shape* shape);
+
+/* Mixer forward fused with the biased output projection (inference):
+ *   y = cast(bf16(mixed) bf16(out_weight)^T + out_bias),  row_mask rows -> 0,
+ * with mixed as in lsso_hip_mixer_forward, computed per token tile in LDS and
+ * never written to memory.  The result is bitwise that of
+ * lsso_hip_mixer_forward followed by lsso_hip_linear(mixed, out_weight,
+ * out_bias, row_mask).  out_weight: float32 [H*d, H*d]; out_bias: float32
+ * [H*d] or NULL; row_mask: uint8 [batch*length] or NULL; y: [batch, length,
+ * H*d] of y_dtype (LSSO_HIP_F16 or LSSO_HIP_BF16), 16-byte aligned.  The
+ * workspace is that of lsso_hip_mixer_forward.
+ * Replaces: fast_mix followed by tensor_core_linear in LSSO._forward_cuda
+ * (lsso/ball/model.py:389-405; lsso/ball/cuda.py:283-323,
+ *  lsso/ball/reference.py:347-408). */
+int lsso_hip_mixer_forward_projected(const lsso_hip_mixer_shape* shape,
+                                     const void* projected,
+                                     const float* core_base_raw,
+                                     const float* core_drive_weight,
+                                     const float* eta_raw,
+                                     const float* inverse_frequency,
+                                     const float* centered_positions,
+                                     int positions_mode,
+                                     const float* valid_counts,
+                                     const float* out_weight,
+                                     const float* out_bias,
+                                     const uint8_t* row_mask,
+                                     void* y,
+                                     int y_dtype,
+                                     void* workspace,
+                                     size_t workspace_bytes,
+                                     void* stream);
+
 /* Device scratch bytes needed by lsso_hip_linear. */
 int lsso_hip_linear_workspace_bytes(int64_t rows, int64_t in_features,
                                     int64_t out_features, size_t* bytes);

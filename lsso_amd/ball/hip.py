@@ -42,6 +42,8 @@ _SYMBOLS = (
     "lsso_hip_mixer_workspace_bytes",
     "lsso_hip_mixer_tape_floats",
     "lsso_hip_mixer_forward",
+    "lsso_hip_mixer_projected_supported",
+    "lsso_hip_mixer_forward_projected",
     "lsso_hip_linear_workspace_bytes",
     "lsso_hip_linear",
 )
@@ -80,6 +82,14 @@ def _declare(library: ctypes.CDLL) -> None:
     library.lsso_hip_mixer_forward.argtypes = [
         shape_p, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp, ctypes.c_size_t, vp,
     ]
+    library.lsso_hip_mixer_projected_supported.restype = ctypes.c_int
+    library.lsso_hip_mixer_projected_supported.argtypes = [shape_p]
+    library.lsso_hip_mixer_forward_projected.restype = ctypes.c_int
+    library.lsso_hip_mixer_forward_projected.argtypes = [
+        shape_p, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int, vp,
+        ctypes.c_size_t, vp,
+    ]  # shape, projected, base, drive, eta, inv_freq, positions, mode, counts,
+    #    out_weight, out_bias, row_mask, y, y_dtype, workspace, workspace_bytes, stream
     library.lsso_hip_linear_workspace_bytes.restype = ctypes.c_int
     library.lsso_hip_linear_workspace_bytes.argtypes = [i64, i64, i64, size_p]
     library.lsso_hip_linear.restype = ctypes.c_int
@@ -460,6 +470,101 @@ def fast_mix(
     return _FastMix.apply(
         projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
     )
+
+
+def mix_project_supported(
+    projected: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+) -> bool:
+    """Whether the fused mixer + output projection covers this geometry."""
+
+    library = _library()
+    shape, _mode = _validate_mixer(projected, core_base_raw, core_drive_weight, eta_raw, None, None)
+    status = library.lsso_hip_mixer_projected_supported(ctypes.byref(shape))
+    if status < 0:
+        _check(status, library)
+    return status == 1
+
+
+def mix_project(
+    projected: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None,
+    valid_counts: torch.Tensor | None,
+    out_weight: torch.Tensor,
+    out_bias: torch.Tensor | None,
+    output_dtype: torch.dtype,
+    row_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Inference-only native mixer fused with the biased output projection.
+
+    Bitwise ``linear(forward_inference(...), out_weight, out_bias,
+    output_dtype, row_mask)``: the mixed tensor stays on chip (the
+    orchestration of reference model.py:389-405 in one pass).
+    """
+
+    if torch.is_grad_enabled() and _any_requires_grad(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts,
+        out_weight, out_bias,
+    ):
+        raise RuntimeError(
+            "lsso_hip mix_project is an inference-only entry point and cannot participate in "
+            "autograd; use fast_mix() followed by linear()"
+        )
+    library = _library()
+    shape, mode = _validate_mixer(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+    )
+    device = projected.device
+    dim = shape.heads * shape.head_dim
+    dtype_codes = {torch.float16: _F16, torch.bfloat16: _BF16}
+    if output_dtype not in dtype_codes:
+        raise TypeError("the fused projection supports float16/bfloat16 outputs")
+    if out_weight.dtype != torch.float32 or tuple(out_weight.shape) != (dim, dim):
+        raise TypeError(f"out_weight must be float32 [{dim}, {dim}]")
+    if out_bias is not None and (out_bias.dtype != torch.float32 or tuple(out_bias.shape) != (dim,)):
+        raise TypeError(f"out_bias must be float32 [{dim}]")
+    for name, value in (("out_weight", out_weight), ("out_bias", out_bias)):
+        if value is not None:
+            _require_device_tensor(value, name, device)
+    out_weight = out_weight.contiguous()
+    out_bias = None if out_bias is None else out_bias.contiguous()
+    mask_ptr = None
+    if row_mask is not None:
+        if row_mask.dtype != torch.bool or tuple(row_mask.shape) != (shape.batch, shape.length):
+            raise ValueError("row_mask must be a bool [B, N] tensor")
+        row_mask = row_mask.contiguous()
+        mask_ptr = row_mask.data_ptr()
+    workspace_bytes = ctypes.c_size_t()
+    _check(library.lsso_hip_mixer_workspace_bytes(ctypes.byref(shape), mode, ctypes.byref(workspace_bytes)), library)
+    workspace = torch.empty(workspace_bytes.value, dtype=torch.uint8, device=device)
+    output = torch.empty((shape.batch, shape.length, dim), dtype=output_dtype, device=device)
+    with torch.cuda.device(device):
+        status = library.lsso_hip_mixer_forward_projected(
+            ctypes.byref(shape),
+            projected.data_ptr(),
+            core_base_raw.data_ptr(),
+            core_drive_weight.data_ptr(),
+            eta_raw.data_ptr(),
+            ctypes.cast(_inverse_frequency(shape.rank), ctypes.c_void_p),
+            None if centered_positions is None else centered_positions.data_ptr(),
+            mode,
+            None if valid_counts is None else valid_counts.data_ptr(),
+            out_weight.data_ptr(),
+            None if out_bias is None else out_bias.data_ptr(),
+            mask_ptr,
+            output.data_ptr(),
+            dtype_codes[output_dtype],
+            workspace.data_ptr(),
+            workspace_bytes.value,
+            _stream(device),
+        )
+    _check(status, library)
+    return output
 
 
 def linear(

@@ -308,6 +308,26 @@ class LSSO(nn.Module):
         # Masked rows are neither read nor biased: the projection writes zeros
         # there (reference model.py:371-383, 402-404).
         projected = hip.linear(x, self.w_bc.weight, self.w_bc.bias, torch.bfloat16, row_mask=mask)
+        needs_grad = torch.is_grad_enabled() and any(
+            parameter.requires_grad for parameter in (x, *self.parameters())
+        )
+        if not needs_grad and hip.mix_project_supported(
+            projected, self.core_base_raw, self.core_drive_weight, self.eta_raw
+        ):
+            # Inference: the mixer and the output projection in one pass,
+            # bitwise equal to the two-step path below.
+            return hip.mix_project(
+                projected,
+                self.core_base_raw,
+                self.core_drive_weight,
+                self.eta_raw,
+                centered_positions,
+                valid_counts,
+                self.w_o.weight,
+                self.w_o.bias,
+                x.dtype,
+                row_mask=mask,
+            )
         mixed = hip.fast_mix(
             projected,
             self.core_base_raw,

@@ -158,17 +158,22 @@ int lsso_hip_mixer_tape_floats(const lsso_hip_mixer_shape* shape, size_t* floats
     return LSSO_HIP_OK;
 }
 
-int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projected,
-                           const float* core_base_raw, const float* core_drive_weight,
-                           const float* eta_raw, const float* inverse_frequency,
-                           const float* centered_positions, int positions_mode,
-                           const float* valid_counts, void* output, float* tape,
-                           void* workspace, size_t workspace_bytes, void* stream_handle) {
-    MixerPlan plan;
-    int status = make_plan(shape, positions_mode, &plan);
-    if (status != LSSO_HIP_OK) {
-        return status;
-    }
+}  // extern "C"
+
+namespace {
+
+// Device pointers of the mixer workspace.
+struct MixerBuffers {
+    uint32_t* phases;
+    float* partials;
+    float* zbuf;
+    uint16_t* mop;
+};
+
+int check_mixer_call(const MixerPlan& plan, const void* projected, const float* core_base_raw,
+                     const float* core_drive_weight, const float* eta_raw, const void* output,
+                     const float* centered_positions, int positions_mode, void* workspace,
+                     size_t workspace_bytes, MixerBuffers* buffers) {
     if (projected == nullptr || core_base_raw == nullptr || core_drive_weight == nullptr ||
         eta_raw == nullptr || output == nullptr) {
         return fail(LSSO_HIP_EINVAL, "projected, parameters and output must not be NULL");
@@ -183,18 +188,35 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projec
         return fail(LSSO_HIP_EINVAL, "workspace must be 256-byte aligned");
     }
     if (!aligned(projected, 2) || !aligned(output, 2)) {
-        return fail(LSSO_HIP_EINVAL, "projected and output must be 2-byte aligned bfloat16 buffers");
+        return fail(LSSO_HIP_EINVAL, "projected and output must be 2-byte aligned 16-bit buffers");
     }
-    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
     char* ws = static_cast<char*>(workspace);
-    uint32_t* phases = reinterpret_cast<uint32_t*>(ws + plan.off_phases);
-    float* partials = reinterpret_cast<float*>(ws + plan.off_partials);
-    float* zbuf = reinterpret_cast<float*>(ws + plan.off_zbuf);
-    uint16_t* mop = reinterpret_cast<uint16_t*>(ws + plan.off_mop);
+    buffers->phases = reinterpret_cast<uint32_t*>(ws + plan.off_phases);
+    buffers->partials = reinterpret_cast<float*>(ws + plan.off_partials);
+    buffers->zbuf = reinterpret_cast<float*>(ws + plan.off_zbuf);
+    buffers->mop = reinterpret_cast<uint16_t*>(ws + plan.off_mop);
+    return LSSO_HIP_OK;
+}
 
+int64_t phase_batch_stride(const MixerPlan& plan, int positions_mode) {
+    return positions_mode == LSSO_HIP_POSITIONS_BATCHED ? plan.length * plan.pairs : 0;
+}
+
+bool vector_rows(const MixerPlan& plan, const void* projected, const void* output) {
+    return plan.width % 8 == 0 && plan.head_dim % 4 == 0 && aligned(projected, 16) &&
+           aligned(output, 16);
+}
+
+// Phase table, L-reductions and the compact solve: everything up to the
+// apply operand records.
+int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
+                const float* core_base_raw, const float* core_drive_weight, const float* eta_raw,
+                const float* inverse_frequency, const float* centered_positions,
+                int positions_mode, const float* valid_counts, float* tape, bool vec,
+                hipStream_t stream) {
     lsso_hip::PhaseArgs phase{};
     phase.positions = positions_mode == LSSO_HIP_POSITIONS_DEFAULT ? nullptr : centered_positions;
-    phase.phases = phases;
+    phase.phases = buf.phases;
     phase.count = plan.phase_batches * plan.length * plan.pairs;
     phase.length = plan.length;
     phase.pairs = static_cast<int>(plan.pairs);
@@ -208,21 +230,16 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projec
         return hip_failure(error, "phase_kernel launch");
     }
 
-    const bool vec = plan.width % 8 == 0 && plan.head_dim % 4 == 0 && aligned(projected, 16) &&
-                     aligned(output, 16);
-    const int64_t phase_stride =
-        positions_mode == LSSO_HIP_POSITIONS_BATCHED ? plan.length * plan.pairs : 0;
-
     lsso_hip::ReduceArgs reduce{};
     reduce.projected = static_cast<const uint16_t*>(projected);
-    reduce.phases = phases;
-    reduce.partials = partials;
+    reduce.phases = buf.phases;
+    reduce.partials = buf.partials;
     reduce.batch = plan.batch;
     reduce.length = plan.length;
     reduce.heads = plan.heads;
     reduce.head_dim = plan.head_dim;
     reduce.width = plan.width;
-    reduce.phase_batch_stride = phase_stride;
+    reduce.phase_batch_stride = phase_batch_stride(plan, positions_mode);
     reduce.chunks = plan.reduce_chunks;
     reduce.chunk_tokens = plan.reduce_chunk_tokens;
     reduce.column_groups = plan.column_groups;
@@ -234,7 +251,7 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projec
     }
 
     lsso_hip::SolveArgs solve{};
-    solve.partials = partials;
+    solve.partials = buf.partials;
     solve.chunks = plan.reduce_chunks;
     solve.partial_stride = plan.partial_stride;
     solve.batch = plan.batch;
@@ -245,8 +262,8 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projec
     solve.drive = core_drive_weight;
     solve.eta_raw = eta_raw;
     solve.valid_counts = valid_counts;
-    solve.zbuf = zbuf;
-    solve.mop = mop;
+    solve.zbuf = buf.zbuf;
+    solve.mop = buf.mop;
     solve.tape = tape;
     solve.tape_stride = plan.tape_stride;
     error = lsso_hip::launch_solve(static_cast<int>(plan.rank), solve, plan.batch * plan.heads,
@@ -254,11 +271,47 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projec
     if (error != hipSuccess) {
         return hip_failure(error, "solve_kernel launch");
     }
+    return LSSO_HIP_OK;
+}
+
+bool projected_shape_supported(const MixerPlan& plan) {
+    return lsso_hip::mix_project_supported(plan.rank, plan.heads, plan.head_dim, plan.width);
+}
+
+}  // namespace
+
+extern "C" {
+
+int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projected,
+                           const float* core_base_raw, const float* core_drive_weight,
+                           const float* eta_raw, const float* inverse_frequency,
+                           const float* centered_positions, int positions_mode,
+                           const float* valid_counts, void* output, float* tape,
+                           void* workspace, size_t workspace_bytes, void* stream_handle) {
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    MixerBuffers buf{};
+    status = check_mixer_call(plan, projected, core_base_raw, core_drive_weight, eta_raw, output,
+                              centered_positions, positions_mode, workspace, workspace_bytes, &buf);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    const bool vec = vector_rows(plan, projected, output);
+    status = run_compact(plan, buf, projected, core_base_raw, core_drive_weight, eta_raw,
+                         inverse_frequency, centered_positions, positions_mode, valid_counts, tape,
+                         vec, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
 
     lsso_hip::ApplyArgs apply{};
     apply.projected = static_cast<const uint16_t*>(projected);
-    apply.phases = phases;
-    apply.mop = mop;
+    apply.phases = buf.phases;
+    apply.mop = buf.mop;
     apply.eta_raw = eta_raw;
     apply.output = static_cast<uint16_t*>(output);
     apply.batch = plan.batch;
@@ -267,15 +320,112 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projec
     apply.head_dim = plan.head_dim;
     apply.width = plan.width;
     apply.out_width = plan.out_width;
-    apply.phase_batch_stride = phase_stride;
+    apply.phase_batch_stride = phase_batch_stride(plan, positions_mode);
     apply.chunks = plan.apply_chunks;
     apply.chunk_tokens = plan.apply_chunk_tokens;
     apply.feature_blocks = plan.feature_blocks;
     apply.block_groups = plan.block_groups;
     apply.total_waves = plan.batch * plan.heads * plan.apply_chunks * plan.block_groups;
-    error = lsso_hip::launch_apply(static_cast<int>(plan.rank), apply, plan.nfbw, vec, stream);
+    const hipError_t error =
+        lsso_hip::launch_apply(static_cast<int>(plan.rank), apply, plan.nfbw, vec, stream);
     if (error != hipSuccess) {
         return hip_failure(error, "apply_kernel launch");
+    }
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_mixer_projected_supported(const lsso_hip_mixer_shape* shape) {
+    MixerPlan plan;
+    const int status = make_plan(shape, LSSO_HIP_POSITIONS_DEFAULT, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    return projected_shape_supported(plan) ? 1 : 0;
+}
+
+int lsso_hip_mixer_forward_projected(const lsso_hip_mixer_shape* shape, const void* projected,
+                                     const float* core_base_raw, const float* core_drive_weight,
+                                     const float* eta_raw, const float* inverse_frequency,
+                                     const float* centered_positions, int positions_mode,
+                                     const float* valid_counts, const float* out_weight,
+                                     const float* out_bias, const uint8_t* row_mask, void* y,
+                                     int y_dtype, void* workspace, size_t workspace_bytes,
+                                     void* stream_handle) {
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    if (!projected_shape_supported(plan)) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "the fused mixer + output projection supports heads <= 8, head_dim a multiple "
+                    "of 16 up to 64, H*head_dim <= 256 and H*(rank+head_dim) <= 512; use "
+                    "lsso_hip_mixer_forward followed by lsso_hip_linear");
+    }
+    if (y_dtype != LSSO_HIP_F16 && y_dtype != LSSO_HIP_BF16) {
+        return fail(LSSO_HIP_EINVAL, "y_dtype must be LSSO_HIP_F16 or LSSO_HIP_BF16");
+    }
+    if (out_weight == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "out_weight must not be NULL");
+    }
+    MixerBuffers buf{};
+    status = check_mixer_call(plan, projected, core_base_raw, core_drive_weight, eta_raw, y,
+                              centered_positions, positions_mode, workspace, workspace_bytes, &buf);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    if (!aligned(projected, 16) || !aligned(y, 16)) {
+        return fail(LSSO_HIP_EINVAL, "the fused path needs 16-byte aligned projected and y buffers");
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    status = run_compact(plan, buf, projected, core_base_raw, core_drive_weight, eta_raw,
+                         inverse_frequency, centered_positions, positions_mode, valid_counts,
+                         nullptr, true, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+
+    int device = 0;
+    hipError_t error = hipGetDevice(&device);
+    if (error != hipSuccess) {
+        return hip_failure(error, "hipGetDevice");
+    }
+    int units = 0;
+    error = hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device);
+    if (error != hipSuccess) {
+        return hip_failure(error, "hipDeviceGetAttribute");
+    }
+    // One persistent workgroup per compute unit, each on a contiguous token
+    // range of one sample (ranges are whole tiles).
+    const int64_t tile = lsso_hip::mix_project_tile_rows();
+    int64_t ranges = ceil_div(units, plan.batch);
+    const int64_t max_ranges = ceil_div(plan.length, tile);
+    if (ranges > max_ranges) ranges = max_ranges;
+    const int64_t range_tokens = ceil_div(ceil_div(plan.length, ranges), tile) * tile;
+    ranges = ceil_div(plan.length, range_tokens);
+
+    lsso_hip::MixProjectArgs mix{};
+    mix.projected = static_cast<const uint16_t*>(projected);
+    mix.phases = buf.phases;
+    mix.mop = buf.mop;
+    mix.eta_raw = eta_raw;
+    mix.weight = out_weight;
+    mix.bias = out_bias;
+    mix.row_mask = row_mask;
+    mix.y = y;
+    mix.batch = plan.batch;
+    mix.length = plan.length;
+    mix.heads = plan.heads;
+    mix.head_dim = plan.head_dim;
+    mix.width = plan.width;
+    mix.out_features = plan.out_width;
+    mix.feature_blocks = plan.feature_blocks;
+    mix.phase_batch_stride = phase_batch_stride(plan, positions_mode);
+    mix.ranges = ranges;
+    mix.range_tokens = range_tokens;
+    error = lsso_hip::launch_mix_project(static_cast<int>(plan.rank), mix, y_dtype, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "mix_project_kernel launch");
     }
     return LSSO_HIP_OK;
 }

@@ -110,4 +110,67 @@ __device__ __forceinline__ void rotate_pair(uint32_t relation_pair, uint32_t pha
     odd_out = even * sine + odd * cosine;
 }
 
+// Apply operand layout: the rank dimension is the MFMA K index.  Ranks that
+// are multiples of 32 use K32 steps (16x16x32; lane group g holds ranks
+// base + 8g .. +7), the others K16 steps (16x16x16; ranks base + 4g .. +3).
+// One accumulation chain never mixes the two MFMA shapes: a 16x16x32 result
+// consumed as SrcC of a 16x16x16 produced wrong accumulators on gfx950 with
+// this toolchain.  Per lane the M' operand holds, per step, the hi values
+// followed by the lo values.
+template <int R>
+struct ApplyLayout {
+    static constexpr bool kWide = (R % 32) == 0;
+    static constexpr int kSteps32 = kWide ? R / 32 : 0;
+    static constexpr int kSteps16 = kWide ? 0 : R / 16;
+    static constexpr int kLaneValues = R / 4;          // per hi or lo part
+    static constexpr int kLaneHalfs = 2 * kLaneValues;  // bf16 per lane per block
+    __device__ static constexpr int rank32(int s, int g, int i) { return 32 * s + 8 * g + i; }
+    __device__ static constexpr int rank16(int s, int g, int i) { return 16 * s + 4 * g + i; }
+    // offsets (in bf16) of the hi part of a step inside a lane record
+    __device__ static constexpr int offset32(int s) { return 16 * s; }
+    __device__ static constexpr int offset16(int s) { return 8 * s; }
+};
+
+// Resident BF16 slice of an FP32 weight [N, K] for y^T = W x^T on
+// v_mfma_f32_32x32x16_bf16: lane holds row n0 + lane % 32 and columns
+// 16 ks + 8 (lane / 32) + 0..7 (RNE-rounded, zero outside the matrix).  Rows
+// are read as float4 pairs when K is a multiple of 4.
+template <int KSTEPS>
+__device__ __forceinline__ void load_weight_slice(u32x4 (&wreg)[KSTEPS], const float* weight,
+                                                  int64_t N, int64_t K, int64_t n0, int lane) {
+    const int half = lane >> 5;
+    const int64_t n = n0 + (lane & 31);
+    const bool nv = n < N;
+    const float* wrow = weight + (nv ? n : 0) * K;
+    const bool vector_rows = (K % 4) == 0;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int64_t k0 = 16 * ks + 8 * half;
+        float v[8];
+        if (vector_rows && nv && k0 + 8 <= K) {
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(wrow + k0);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(wrow + k0 + 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = lo[i];
+                v[4 + i] = hi[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const bool live = nv && k0 + i < K;
+                const float value = wrow[live ? k0 + i : 0];
+                v[i] = live ? value : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            wreg[ks][p] = pack_bf16(v[2 * p], v[2 * p + 1]);
+        }
+        // Convert one K step at a time: keeps the FP32 staging of W from
+        // being hoisted next to the whole BF16 slice.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 }  // namespace lsso_hip

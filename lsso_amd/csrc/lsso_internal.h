@@ -74,6 +74,29 @@ struct ApplyArgs {
     int64_t total_waves;
 };
 
+// Apply fused with the output projection: y = cast(bf16(mixed) bf16(W_o)^T
+// + b_o) with mixed = eta C + rot(R) M' computed per 64-token tile in LDS.
+struct MixProjectArgs {
+    const uint16_t* projected;  // BF16 [B, N, width]
+    const uint32_t* phases;
+    const uint16_t* mop;        // apply operand records
+    const float* eta_raw;       // [H]
+    const float* weight;        // FP32 [D, D] (D = H * head_dim)
+    const float* bias;          // FP32 [D] or nullptr
+    const uint8_t* row_mask;    // [B * N] or nullptr
+    void* y;                    // FP16/BF16 [B, N, D]
+    int64_t batch;
+    int64_t length;
+    int64_t heads;
+    int64_t head_dim;
+    int64_t width;
+    int64_t out_features;       // D
+    int64_t feature_blocks;     // head_dim / 16
+    int64_t phase_batch_stride;
+    int64_t ranges;             // token ranges per sample (one workgroup each)
+    int64_t range_tokens;       // multiple of the 64-token tile
+};
+
 struct LinearArgs {
     const void* x;
     int64_t rows;
@@ -97,6 +120,12 @@ hipError_t launch_apply(int rank, const ApplyArgs& a, int nfbw, bool vec, hipStr
 
 // Projection launcher; k_steps = ceil(in_features / 16) rounded to a
 // compiled tier.  Returns hipErrorInvalidValue for an unsupported tier.
+// Shapes the fused apply + output projection handles: heads <= 8, head_dim a
+// multiple of 16 up to 64, D = heads * head_dim <= 256, width <= 512.
+bool mix_project_supported(int64_t rank, int64_t heads, int64_t head_dim, int64_t width);
+int mix_project_tile_rows();
+hipError_t launch_mix_project(int rank, const MixProjectArgs& a, int y_dtype, hipStream_t stream);
+
 hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,
                          int grid_groups, hipStream_t stream);
 int linear_tile_rows();

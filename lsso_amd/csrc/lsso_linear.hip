@@ -157,43 +157,8 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     const int64_t K = a.in_features;
     const int64_t N = a.out_features;
 
-    // W slice: lane holds row n0 + lane%32, k = 16 ks + 8 half + 0..7.  Rows
-    // are read as float4 pairs when K is a multiple of 4 (16-byte rows).
     u32x4 wreg[KSTEPS];
-    {
-        const int64_t n = n0 + (lane & 31);
-        const bool nv = n < N;
-        const float* wrow = a.weight + (nv ? n : 0) * K;
-        const bool vector_rows = (K % 4) == 0;
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            const int64_t k0 = 16 * ks + 8 * half;
-            float v[8];
-            if (vector_rows && nv && k0 + 8 <= K) {
-                const f32x4 lo = *reinterpret_cast<const f32x4*>(wrow + k0);
-                const f32x4 hi = *reinterpret_cast<const f32x4*>(wrow + k0 + 4);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[i] = lo[i];
-                    v[4 + i] = hi[i];
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const bool live = nv && k0 + i < K;
-                    const float value = wrow[live ? k0 + i : 0];
-                    v[i] = live ? value : 0.0f;
-                }
-            }
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                wreg[ks][p] = pack_bf16(v[2 * p], v[2 * p + 1]);
-            }
-            // Convert one K step at a time: keeps the FP32 staging of W from
-            // being hoisted next to the whole BF16 slice.
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
+    load_weight_slice<KSTEPS>(wreg, a.weight, N, K, n0, lane);
     for (int c = tid; c < kGroupColumns; c += kThreads) {
         const int64_t n = cg * kGroupColumns + c;
         s_bias[c] = (a.bias != nullptr && n < N) ? a.bias[n] : 0.0f;

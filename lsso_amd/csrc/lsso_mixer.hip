@@ -48,27 +48,6 @@ struct ReduceLayout {
     }
 };
 
-// Apply: the rank dimension is the MFMA K index.  Ranks that are multiples
-// of 32 use K32 steps (16x16x32; lane group g holds ranks base + 8g .. +7),
-// the others K16 steps (16x16x16; ranks base + 4g .. +3).  One accumulation
-// chain never mixes the two MFMA shapes: a 16x16x32 result consumed as SrcC
-// of a 16x16x16 produced wrong accumulators on gfx950 with this toolchain.
-// Per lane the M' operand holds, per step, the hi values followed by the lo
-// values.
-template <int R>
-struct ApplyLayout {
-    static constexpr bool kWide = (R % 32) == 0;
-    static constexpr int kSteps32 = kWide ? R / 32 : 0;
-    static constexpr int kSteps16 = kWide ? 0 : R / 16;
-    static constexpr int kLaneValues = R / 4;          // per hi or lo part
-    static constexpr int kLaneHalfs = 2 * kLaneValues;  // bf16 per lane per block
-    __device__ static constexpr int rank32(int s, int g, int i) { return 32 * s + 8 * g + i; }
-    __device__ static constexpr int rank16(int s, int g, int i) { return 16 * s + 4 * g + i; }
-    // offsets (in bf16) of the hi part of a step inside a lane record
-    __device__ static constexpr int offset32(int s) { return 16 * s; }
-    __device__ static constexpr int offset16(int s) { return 8 * s; }
-};
-
 // ---------------------------------------------------------------------------
 // Phase table.
 __global__ __launch_bounds__(256) void phase_kernel(PhaseArgs a) {

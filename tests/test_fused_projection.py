@@ -1,0 +1,108 @@
+"""The fused mixer + output projection against the two-step native path (GPU).
+
+``lsso_hip_mixer_forward_projected`` keeps the mixed tensor on chip; it must
+reproduce ``lsso_hip_mixer_forward`` followed by ``lsso_hip_linear`` bit for
+bit (same apply MFMA order and BF16 rounding of mixed, same projection K
+order, FP32 bias, masked rows zeroed), so the comparison is exact.  Module-
+level parity against the FP64 oracle runs through this path in
+tests/test_hip_parity.py wherever the geometry is supported.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(batch, rank, heads, head_dim, length, seed, scale=0.05):
+    generator = torch.Generator().manual_seed(seed)
+    dim = heads * head_dim
+    projected = torch.randn(batch, length, heads * rank + dim, generator=generator).bfloat16()
+    base = scale * torch.randn(heads, rank, rank, generator=generator)
+    drive = scale * torch.randn(heads, head_dim, rank, generator=generator)
+    eta_raw = scale * torch.randn(heads, generator=generator)
+    weight = torch.randn(dim, dim, generator=generator) / dim**0.5
+    bias = 0.1 * torch.randn(dim, generator=generator)
+    return [t.cuda() for t in (projected, base, drive, eta_raw, weight, bias)]
+
+
+def _two_step(native, projected, base, drive, eta_raw, positions, counts, weight, bias, dtype, mask):
+    mixed = native.forward_inference(projected, base, drive, eta_raw, positions, counts)
+    return native.linear(mixed, weight, bias, dtype, row_mask=mask)
+
+
+@pytest.mark.parametrize(
+    ("batch", "rank", "heads", "head_dim", "length"),
+    [
+        (2, 32, 8, 32, 1000),   # headline geometry, ragged tail tile
+        (3, 16, 3, 64, 65),     # C1 geometry
+        (2, 48, 4, 32, 333),    # rank 48 (K16 MFMA steps)
+        (1, 64, 4, 64, 257),    # rank 64, widest operands
+        (2, 16, 8, 16, 31),     # shorter than one tile
+        (1, 32, 1, 48, 100),    # one head, three feature blocks
+    ],
+)
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_fused_projection_is_bitwise_the_two_step_path(native, batch, rank, heads, head_dim, length, dtype):
+    projected, base, drive, eta_raw, weight, bias = _inputs(
+        batch, rank, heads, head_dim, length, seed=1000 + rank + head_dim + length
+    )
+    with torch.no_grad():
+        assert native.mix_project_supported(projected, base, drive, eta_raw)
+        fused = native.mix_project(projected, base, drive, eta_raw, None, None, weight, bias, dtype)
+        expected = _two_step(native, projected, base, drive, eta_raw, None, None, weight, bias, dtype, None)
+    torch.cuda.synchronize()
+    assert fused.dtype == dtype
+    assert torch.isfinite(fused).all()
+    assert torch.equal(fused, expected)
+
+
+def test_fused_projection_masked_per_sample_positions_and_no_bias(native):
+    batch, rank, heads, head_dim, length = 3, 32, 8, 32, 300
+    projected, base, drive, eta_raw, weight, _bias = _inputs(batch, rank, heads, head_dim, length, seed=77)
+    lengths = torch.tensor([300, 123, 1])
+    mask = (torch.arange(length)[None, :] < lengths[:, None]).cuda()
+    projected = torch.where(mask[:, :, None], projected, torch.zeros_like(projected))
+    positions = (torch.arange(length)[None, :] * torch.tensor([[1.0], [3.0], [7.0]])).cuda()
+    positions = positions - positions.mean(dim=1, keepdim=True)
+    counts = lengths.float().cuda()
+    with torch.no_grad():
+        fused = native.mix_project(projected, base, drive, eta_raw, positions, counts, weight, None,
+                                   torch.float16, row_mask=mask)
+        expected = _two_step(native, projected, base, drive, eta_raw, positions, counts, weight, None,
+                             torch.float16, mask)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, expected)
+    assert not fused[~mask].any()
+
+
+def test_fused_projection_rejects_unsupported_geometry_and_autograd(native):
+    projected, base, drive, eta_raw, weight, bias = _inputs(1, 32, 2, 96, 40, seed=5)
+    with torch.no_grad():
+        assert not native.mix_project_supported(projected, base, drive, eta_raw)
+        with pytest.raises(ValueError, match="fused mixer"):
+            native.mix_project(projected, base, drive, eta_raw, None, None, weight, bias, torch.float16)
+    projected, base, drive, eta_raw, weight, bias = _inputs(1, 32, 2, 32, 40, seed=6)
+    weight.requires_grad_(True)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        native.mix_project(projected, base, drive, eta_raw, None, None, weight, bias, torch.float16)
+
+
+def test_module_uses_fused_path_and_matches_two_step(native):
+    from lsso_amd import LSSO, LSSOConfig
+
+    torch.manual_seed(3)
+    layer = LSSO(LSSOConfig(dim=256, num_heads=8, rank=32, bias=True)).cuda().eval()
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.05)
+        layer.core_drive_weight.normal_(std=0.05)
+    x = torch.randn(2, 200, 256, generator=torch.Generator().manual_seed(4)).half().cuda()
+    with torch.no_grad():
+        y = layer(x, implementation="hip")
+        projected = native.linear(x, layer.w_bc.weight, layer.w_bc.bias, torch.bfloat16)
+        mixed = native.forward_inference(projected, layer.core_base_raw, layer.core_drive_weight, layer.eta_raw)
+        expected = native.linear(mixed, layer.w_o.weight, layer.w_o.bias, torch.float16)
+    torch.cuda.synchronize()
+    assert torch.equal(y, expected)
