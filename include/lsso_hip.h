@@ -109,6 +109,39 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape,
                            size_t workspace_bytes,
                            void* stream);
 
+/* Device scratch bytes needed by lsso_hip_mixer_backward.
+ * Replaces: the at::empty allocations of backward_cuda
+ * (csrc/ball/backward.cu:1386-1400). */
+int lsso_hip_mixer_backward_workspace_bytes(const lsso_hip_mixer_shape* shape,
+                                            int positions_mode, size_t* bytes);
+
+/* First-order backward of lsso_hip_mixer_forward, given the tape that a call
+ * with a tape pointer recorded.  grad_output: bfloat16 [batch, length,
+ * heads*head_dim] (masked rows zero); outputs grad_projected bfloat16 like
+ * projected, and float32 grad_base [H, r, r], grad_drive [H, d, r] and
+ * grad_eta [H] (sums over the batch in a fixed order: deterministic).
+ * head_dim <= 64.  Positions, counts and inverse_frequency as in the forward.
+ * Replaces: torch.ops.lsso_equilibrium.backward (csrc/ball/binding.cpp:92-95,
+ * csrc/ball/backward.cu:1386-1667, lsso/ball/cuda.py:256-280). */
+int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape,
+                            const void* grad_output,
+                            const void* projected,
+                            const float* core_base_raw,
+                            const float* core_drive_weight,
+                            const float* eta_raw,
+                            const float* inverse_frequency,
+                            const float* centered_positions,
+                            int positions_mode,
+                            const float* valid_counts,
+                            const float* tape,
+                            void* grad_projected,
+                            float* grad_base,
+                            float* grad_drive,
+                            float* grad_eta,
+                            void* workspace,
+                            size_t workspace_bytes,
+                            void* stream);
+
 /* 1 if lsso_hip_mixer_forward_projected handles this shape, 0 if not (use
  * lsso_hip_mixer_forward followed by lsso_hip_linear), or a negative code for
  * an invalid shape.  The fused path covers heads <= 8, head_dim a multiple of

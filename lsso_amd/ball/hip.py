@@ -44,6 +44,8 @@ _SYMBOLS = (
     "lsso_hip_mixer_forward",
     "lsso_hip_mixer_projected_supported",
     "lsso_hip_mixer_forward_projected",
+    "lsso_hip_mixer_backward_workspace_bytes",
+    "lsso_hip_mixer_backward",
     "lsso_hip_linear_workspace_bytes",
     "lsso_hip_linear",
 )
@@ -90,6 +92,14 @@ def _declare(library: ctypes.CDLL) -> None:
         ctypes.c_size_t, vp,
     ]  # shape, projected, base, drive, eta, inv_freq, positions, mode, counts,
     #    out_weight, out_bias, row_mask, y, y_dtype, workspace, workspace_bytes, stream
+    library.lsso_hip_mixer_backward_workspace_bytes.restype = ctypes.c_int
+    library.lsso_hip_mixer_backward_workspace_bytes.argtypes = [shape_p, ctypes.c_int, size_p]
+    library.lsso_hip_mixer_backward.restype = ctypes.c_int
+    library.lsso_hip_mixer_backward.argtypes = [
+        shape_p, vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp,
+        ctypes.c_size_t, vp,
+    ]  # shape, grad_output, projected, base, drive, eta, inv_freq, positions, mode, counts,
+    #    tape, grad_projected, grad_base, grad_drive, grad_eta, workspace, workspace_bytes, stream
     library.lsso_hip_linear_workspace_bytes.restype = ctypes.c_int
     library.lsso_hip_linear_workspace_bytes.argtypes = [i64, i64, i64, size_p]
     library.lsso_hip_linear.restype = ctypes.c_int
@@ -422,6 +432,72 @@ def forward_train(
     return output, tape
 
 
+def backward(
+    grad_output: torch.Tensor,
+    projected: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    tape: torch.Tensor,
+    centered_positions: torch.Tensor | None = None,
+    valid_counts: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Native first-order VJP of the mixer (csrc/ball/binding.cpp:92-95):
+    returns (grad_projected, grad_core_base_raw, grad_core_drive_weight,
+    grad_eta_raw)."""
+
+    library = _library()
+    shape, mode = _validate_mixer(
+        projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+    )
+    device = projected.device
+    expected = (shape.batch, shape.length, shape.heads * shape.head_dim)
+    if tuple(grad_output.shape) != expected:
+        raise RuntimeError(f"grad_output must have shape {expected}, got {tuple(grad_output.shape)}")
+    if grad_output.dtype != torch.bfloat16:
+        raise RuntimeError("grad_output must use bfloat16 under the mixed precision HIP contract")
+    _require_device_tensor(grad_output, "grad_output", device)
+    _require_device_tensor(tape, "tape", device)
+    grad_output = grad_output.contiguous()
+    floats = ctypes.c_size_t()
+    _check(library.lsso_hip_mixer_tape_floats(ctypes.byref(shape), ctypes.byref(floats)), library)
+    if tape.dtype != torch.float32 or tape.numel() != floats.value or not tape.is_contiguous():
+        raise RuntimeError("tape does not match this geometry's lsso_hip_mixer_tape_floats()")
+    workspace_bytes = ctypes.c_size_t()
+    _check(
+        library.lsso_hip_mixer_backward_workspace_bytes(ctypes.byref(shape), mode, ctypes.byref(workspace_bytes)),
+        library,
+    )
+    workspace = torch.empty(workspace_bytes.value, dtype=torch.uint8, device=device)
+    grad_projected = torch.empty_like(projected)
+    grad_base = torch.empty_like(core_base_raw)
+    grad_drive = torch.empty_like(core_drive_weight)
+    grad_eta = torch.empty_like(eta_raw)
+    with torch.cuda.device(device):
+        status = library.lsso_hip_mixer_backward(
+            ctypes.byref(shape),
+            grad_output.data_ptr(),
+            projected.data_ptr(),
+            core_base_raw.data_ptr(),
+            core_drive_weight.data_ptr(),
+            eta_raw.data_ptr(),
+            ctypes.cast(_inverse_frequency(shape.rank), ctypes.c_void_p),
+            None if centered_positions is None else centered_positions.data_ptr(),
+            mode,
+            None if valid_counts is None else valid_counts.data_ptr(),
+            tape.data_ptr(),
+            grad_projected.data_ptr(),
+            grad_base.data_ptr(),
+            grad_drive.data_ptr(),
+            grad_eta.data_ptr(),
+            workspace.data_ptr(),
+            workspace_bytes.value,
+            _stream(device),
+        )
+    _check(status, library)
+    return grad_projected, grad_base, grad_drive, grad_eta
+
+
 class _FastMix(torch.autograd.Function):
     """First-order autograd boundary of the native mixer (cuda.py:220-280)."""
 
@@ -432,14 +508,32 @@ class _FastMix(torch.autograd.Function):
                 projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
             )
         ctx.save_for_backward(projected, core_base_raw, core_drive_weight, eta_raw, tape)
+        ctx.centered_positions = centered_positions
+        ctx.valid_counts = valid_counts
         return output
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad_output):
-        raise NotImplementedError(
-            "the native LSSO HIP mixer backward is not built yet; train with "
-            "implementation='reference'"
+        projected, core_base_raw, core_drive_weight, eta_raw, tape = ctx.saved_tensors
+        grads = backward(
+            grad_output.to(dtype=torch.bfloat16),
+            projected,
+            core_base_raw,
+            core_drive_weight,
+            eta_raw,
+            tape,
+            ctx.centered_positions,
+            ctx.valid_counts,
+        )
+        needs = ctx.needs_input_grad
+        return (
+            grads[0] if needs[0] else None,
+            grads[1] if needs[1] else None,
+            grads[2] if needs[2] else None,
+            grads[3] if needs[3] else None,
+            None,
+            None,
         )
 
 
@@ -567,19 +661,14 @@ def mix_project(
     return output
 
 
-def linear(
+def _linear_forward(
     value: torch.Tensor,
     weight: torch.Tensor,
     bias: torch.Tensor | None,
     output_dtype: torch.dtype,
     row_mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Native biased projection cast(bf16(x) bf16(W)^T + b) (reference.py:20-75, 347-408).
-
-    value: [..., K] float16/bfloat16 with unit feature stride; weight: float32
-    [N, K]; bias: float32 [N] or None; output: contiguous [..., N].
-    ``row_mask`` (bool, value.shape[:-1]) zeroes the output rows it excludes.
-    """
+    """The native projection kernel (no autograd)."""
 
     library = _library()
     if value.device.type != "cuda":
@@ -631,12 +720,75 @@ def linear(
     return output
 
 
+
+
+class _Linear(torch.autograd.Function):
+    """Autograd of the native projection with the reference's VJP
+    (lsso/ball/reference.py:205-247): BF16 operands with FP32 accumulation
+    for the value and weight gradients, an FP32 sum of the upstream gradient
+    for the bias.  These are plain library GEMMs (hipBLASLt through torch);
+    rows excluded by ``row_mask`` carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, value, weight, bias, output_dtype, row_mask):
+        output = _linear_forward(value, weight, bias, output_dtype, row_mask)
+        ctx.save_for_backward(value, weight, row_mask)
+        ctx.has_bias = bias is not None
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return output
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_output):
+        value, weight, row_mask = ctx.saved_tensors
+        if row_mask is not None:
+            grad_output = torch.where(row_mask[..., None], grad_output, torch.zeros_like(grad_output))
+        flat_gradient = grad_output.to(dtype=torch.bfloat16).reshape(-1, weight.shape[0]).float()
+        weight_bf16 = weight.to(dtype=torch.bfloat16).float()
+        grad_value = grad_weight = grad_bias = None
+        if ctx.needs_input_grad[0]:
+            grad_value = flat_gradient @ weight_bf16
+            if value.dtype == torch.bfloat16:
+                grad_value = grad_value.to(dtype=torch.bfloat16)
+            grad_value = grad_value.to(dtype=value.dtype).reshape(value.shape)
+        if ctx.needs_input_grad[1]:
+            flat_value = value.to(dtype=torch.bfloat16).reshape(-1, value.shape[-1]).float()
+            grad_weight = (flat_gradient.mT @ flat_value).to(dtype=weight.dtype)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            dimensions = tuple(range(grad_output.ndim - 1))
+            grad_bias = grad_output.sum(dim=dimensions, dtype=torch.float32).to(dtype=ctx.bias_dtype)
+        return grad_value, grad_weight, grad_bias, None, None
+
+
+def linear(
+    value: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    output_dtype: torch.dtype,
+    row_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Native biased projection cast(bf16(x) bf16(W)^T + b) (reference.py:20-75, 347-408).
+
+    value: [..., K] float16/bfloat16 with unit feature stride; weight: float32
+    [N, K]; bias: float32 [N] or None; output: contiguous [..., N].
+    ``row_mask`` (bool, value.shape[:-1]) zeroes the output rows it excludes.
+    Differentiable (first order) when autograd needs it.
+    """
+
+    if torch.is_grad_enabled() and _any_requires_grad(value, weight, bias):
+        return _Linear.apply(value, weight, bias, output_dtype, row_mask)
+    return _linear_forward(value, weight, bias, output_dtype, row_mask)
+
+
 __all__ = [
+    "backward",
     "fast_mix",
     "forward_inference",
     "forward_train",
     "is_available",
     "linear",
     "load",
+    "mix_project",
+    "mix_project_supported",
     "require_available",
 ]

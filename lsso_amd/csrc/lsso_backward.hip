@@ -1,0 +1,604 @@
+// gfx950 first-order backward of the LSSO mixer (reference: lsso/ball/cuda.py:256-280,
+// csrc/ball/backward.cu:326-1667), restated for the Gram-Cholesky forward.
+//
+// Per system (b, h) with a = rot(R) / sqrt(n), P = a L^-T, L L^T = a^T a + I:
+//   forward:  s = a^T C, z = L^-1 s, Theta = Theta0 + z W / sqrt(n),
+//             u = (I + K)^-1 z, x = 2u - (1 + eta) z, m = L^-T x,
+//             Y = eta C + a m.
+//   backward (dY given):
+//     dm = a^T dY                                     (token reduction)
+//     dx = L^-1 dm,  v = (I + K)^-T (2 dx),  dK = -v u^T
+//     dF = (dK + dK^T) F
+//     dTheta = tril(dF, -1) + diag(dF_ii sigmoid(Theta_ii + log(e - 1)))
+//              + triu(dK - dK^T, 1)
+//     dz = -(1 + eta) dx + v + dTheta W^T / sqrt(n),   ds = L^-T dz
+//     Lbar = tril(-m dx^T - ds z^T),  Mbar = L^-T Phi(L^T Lbar) L^-1
+//            (Phi: lower triangle, halved diagonal),   Gamma = Mbar + Mbar^T
+//     dW = z^T dTheta / sqrt(n),  deta = <dY, C> - <dx, z>
+//   per token (token map):
+//     dA = dY M'^T + C (ds / sqrt(n))^T + A Gamma / n      (A = rot(R), M' = m / sqrt(n))
+//     dC = eta dY + A ds / sqrt(n),   dR = rot^T(dA).
+// Kernels: the token reduction reuses reduce_kernel with dY as its content;
+// bwd_solve_kernel runs the compact algebra of one system in LDS and writes
+// the token-map operands as MFMA records; bwd_apply_kernel is the token map;
+// param_reduce_kernel sums parameter gradients over the batch in fixed order.
+
+#include <type_traits>
+
+#include "lsso_device.h"
+#include "lsso_internal.h"
+#include "lsso_hip.h"
+
+namespace lsso_hip {
+
+constexpr int kBwdThreads = 256;
+constexpr int kBwdMaxHeadDim = 64;
+
+bool backward_supported(int64_t rank, int64_t head_dim) {
+    return (rank == 16 || rank == 32 || rank == 48 || rank == 64) && head_dim >= 1 &&
+           head_dim <= kBwdMaxHeadDim;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA operand records of an M x K FP32 matrix split into BF16 hi + lo.
+// K32 steps (16x16x32): lane (g, q) of row block rb and step s holds row
+// 16 rb + q, columns 32 s + 8 g .. +7 (hi then lo, 16 bf16).  K16 steps
+// (16x16x16): columns 16 s + 4 g .. +3 (8 bf16).  Rows and columns past the
+// matrix are zero.
+template <bool K32>
+struct RecordShape {
+    static constexpr int kWidth = K32 ? 32 : 16;     // K per step
+    static constexpr int kPerLane = K32 ? 8 : 4;     // values per lane per part
+    static constexpr int kLaneHalfs = 2 * kPerLane;  // hi + lo
+};
+
+template <bool K32>
+__host__ __device__ constexpr int64_t record_halfs(int64_t rows, int64_t cols) {
+    using RS = RecordShape<K32>;
+    return ((rows + 15) / 16) * ((cols + RS::kWidth - 1) / RS::kWidth) * 64 * RS::kLaneHalfs;
+}
+
+// Writes the records of `value(i, k)` (i < rows, k < cols) with all threads
+// of the workgroup.
+template <bool K32, typename Value>
+__device__ __forceinline__ void write_records(uint16_t* out, int rows, int cols, Value value) {
+    using RS = RecordShape<K32>;
+    const int row_blocks = (rows + 15) / 16;
+    const int steps = (cols + RS::kWidth - 1) / RS::kWidth;
+    const int lanes = row_blocks * steps * 64;
+    for (int idx = threadIdx.x; idx < lanes; idx += blockDim.x) {
+        const int lane = idx & 63;
+        const int step = (idx >> 6) % steps;
+        const int rb = (idx >> 6) / steps;
+        const int row = 16 * rb + (lane & 15);
+        const int k0 = RS::kWidth * step + RS::kPerLane * (lane >> 4);
+        uint16_t* rec = out + static_cast<int64_t>(idx) * RS::kLaneHalfs;
+#pragma unroll
+        for (int i = 0; i < RS::kPerLane; i += 2) {
+            const float v0 = (row < rows && k0 + i < cols) ? value(row, k0 + i) : 0.0f;
+            const float v1 = (row < rows && k0 + i + 1 < cols) ? value(row, k0 + i + 1) : 0.0f;
+            uint32_t hi, lo;
+            split_bf16(v0, v1, hi, lo);
+            *reinterpret_cast<uint32_t*>(rec + i) = hi;
+            *reinterpret_cast<uint32_t*>(rec + RS::kPerLane + i) = lo;
+        }
+    }
+}
+
+// C[i][j] = sum_k A(i, k) B(k, j) over an M x N output, all threads.
+template <typename FA, typename FB, typename Store>
+__device__ __forceinline__ void block_product(int M, int N, int K, FA a, FB b, Store store) {
+    for (int idx = threadIdx.x; idx < M * N; idx += blockDim.x) {
+        const int i = idx / N;
+        const int j = idx - i * N;
+        float acc = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            acc = fmaf(a(i, k), b(k, j), acc);
+        }
+        store(i, j, acc);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Compact backward of one system.
+template <int R>
+__global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) {
+    constexpr int PR = R + 1;                         // r x r pitch
+    constexpr int PD = kBwdMaxHeadDim + 1;            // r x d pitch
+    __shared__ float s_linv[R * PR];
+    __shared__ float s_k[R * PR];    // (I+K)^-1 -> dK -> L -> Mbar
+    __shared__ float s_f[R * PR];    // Theta -> F -> Lbar -> P Linv
+    __shared__ float s_d[R * PR];    // dF -> dTheta -> P
+    __shared__ float s_z[R * PD];
+    __shared__ float s_u[R * PD];    // u -> ds
+    __shared__ float s_x[R * PD];    // x -> dx
+    __shared__ float s_m[R * PD];
+    __shared__ float s_v[R * PD];    // dm -> v -> dz
+    __shared__ float s_diag[R];
+    __shared__ float s_red[kBwdThreads / 64];
+
+    const int tid = threadIdx.x;
+    const int64_t system = blockIdx.x;
+    const int64_t b = system / a.heads;
+    const int64_t h = system - b * a.heads;
+    const int d = static_cast<int>(a.head_dim);
+    const float count = a.valid_counts != nullptr ? a.valid_counts[b] : static_cast<float>(a.length);
+    const float root = sqrtf(count);
+    const float eta = bounded_complement(a.eta_raw[h]);
+    const float* tape = a.tape + system * a.tape_stride;
+    const float* part = a.partials + system * a.chunks * a.partial_stride + R * R;
+    const float* drive = a.drive + h * d * R;
+
+    // ---- loads ------------------------------------------------------------
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        s_linv[i * PR + j] = tape[3 * R * R + idx];
+        s_k[i * PR + j] = tape[2 * R * R + idx];
+        s_f[i * PR + j] = tape[R * R + idx];
+    }
+    for (int idx = tid; idx < R * d; idx += kBwdThreads) {
+        const int i = idx / d;
+        const int f = idx - i * d;
+        const float z = tape[4 * R * R + idx];
+        const float u = tape[4 * R * R + R * d + idx];
+        s_z[i * PD + f] = z;
+        s_u[i * PD + f] = u;
+        s_x[i * PD + f] = 2.0f * u - (1.0f + eta) * z;
+        float dm = 0.0f;
+        for (int ch = 0; ch < a.chunks; ++ch) {
+            dm += part[ch * a.partial_stride + idx];
+        }
+        s_v[i * PD + f] = dm / root;
+    }
+    __syncthreads();
+
+    // ---- m = L^-T x;  dx = L^-1 dm ------------------------------------------
+    block_product(R, d, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+                  [&](int k, int j) { return s_x[k * PD + j]; },
+                  [&](int i, int j, float v) { s_m[i * PD + j] = v; });
+    __syncthreads();
+    block_product(R, d, R, [&](int i, int k) { return s_linv[i * PR + k]; },
+                  [&](int k, int j) { return s_v[k * PD + j]; },
+                  [&](int i, int j, float v) { s_x[i * PD + j] = v; });
+    __syncthreads();
+    // ---- v = (I + K)^-T (2 dx) ----------------------------------------------
+    block_product(R, d, R, [&](int i, int k) { return s_k[k * PR + i]; },
+                  [&](int k, int j) { return 2.0f * s_x[k * PD + j]; },
+                  [&](int i, int j, float v) { s_v[i * PD + j] = v; });
+    __syncthreads();
+    // ---- dK = -v u^T;  F and diag(Theta) -------------------------------------
+    block_product(R, R, d, [&](int i, int k) { return s_v[i * PD + k]; },
+                  [&](int k, int j) { return s_u[j * PD + k]; },
+                  [&](int i, int j, float v) { s_k[i * PR + j] = -v; });
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        const float theta = s_f[i * PR + j];
+        if (i == j) {
+            s_diag[i] = theta;
+        }
+        s_f[i * PR + j] = j < i ? theta : (j == i ? softplus_one(theta) : 0.0f);
+    }
+    __syncthreads();
+    // ---- dF = (dK + dK^T) F;  dTheta -----------------------------------------
+    block_product(R, R, R, [&](int i, int k) { return s_k[i * PR + k] + s_k[k * PR + i]; },
+                  [&](int k, int j) { return s_f[k * PR + j]; },
+                  [&](int i, int j, float v) { s_d[i * PR + j] = v; });
+    __syncthreads();
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        float g;
+        if (j < i) {
+            g = s_d[i * PR + j];
+        } else if (j == i) {
+            const float shifted = s_diag[i] + kSoftplusOneOffset;
+            g = s_d[i * PR + j] / (1.0f + expf(-shifted));
+        } else {
+            g = s_k[i * PR + j] - s_k[j * PR + i];
+        }
+        s_d[i * PR + j] = g;
+    }
+    __syncthreads();
+    // ---- parameter partials: dTheta, z^T dTheta / sqrt(n) ------------------
+    {
+        float* dtheta = a.dtheta_part + system * R * R;
+        for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+            const int i = idx / R;
+            const int j = idx - i * R;
+            dtheta[idx] = s_d[i * PR + j];
+        }
+        float* ddrive = a.ddrive_part + system * d * R;
+        block_product(d, R, R, [&](int f, int k) { return s_z[k * PD + f]; },
+                      [&](int k, int j) { return s_d[k * PR + j]; },
+                      [&](int f, int j, float v) { ddrive[f * R + j] = v / root; });
+    }
+    // ---- dz = -(1 + eta) dx + v + dTheta W^T / sqrt(n) (in place in s_v) ---
+    for (int idx = tid; idx < R * d; idx += kBwdThreads) {
+        const int i = idx / d;
+        const int f = idx - i * d;
+        float acc = 0.0f;
+        for (int k = 0; k < R; ++k) {
+            acc = fmaf(s_d[i * PR + k], drive[f * R + k], acc);
+        }
+        s_v[i * PD + f] = -(1.0f + eta) * s_x[i * PD + f] + s_v[i * PD + f] + acc / root;
+    }
+    __syncthreads();
+    // ---- ds = L^-T dz -> s_u;  -<dx, z> --------------------------------------
+    block_product(R, d, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+                  [&](int k, int j) { return s_v[k * PD + j]; },
+                  [&](int i, int j, float v) { s_u[i * PD + j] = v; });
+    {
+        float partial = 0.0f;
+        for (int idx = tid; idx < R * d; idx += kBwdThreads) {
+            const int i = idx / d;
+            const int f = idx - i * d;
+            partial = fmaf(s_x[i * PD + f], s_z[i * PD + f], partial);
+        }
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            partial += __shfl_xor(partial, offset);
+        }
+        if ((tid & 63) == 0) {
+            s_red[tid >> 6] = partial;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float total = 0.0f;
+        for (int w = 0; w < kBwdThreads / 64; ++w) {
+            total += s_red[w];
+        }
+        a.deta_part[system] = -total;
+    }
+    // ---- Lbar = tril(-m dx^T - ds z^T) -> s_f;  L -> s_k ---------------------
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        float acc = 0.0f;
+        if (j <= i) {
+            for (int f = 0; f < d; ++f) {
+                acc = fmaf(s_m[i * PD + f], s_x[j * PD + f], acc);
+                acc = fmaf(s_u[i * PD + f], s_z[j * PD + f], acc);
+            }
+        }
+        s_f[i * PR + j] = -acc;
+    }
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        s_k[i * PR + j] = tape[idx];
+    }
+    __syncthreads();
+    // ---- P = Phi(L^T Lbar) -> s_d --------------------------------------------
+    block_product(R, R, R, [&](int i, int k) { return s_k[k * PR + i]; },
+                  [&](int k, int j) { return s_f[k * PR + j]; },
+                  [&](int i, int j, float v) {
+                      s_d[i * PR + j] = j < i ? v : (j == i ? 0.5f * v : 0.0f);
+                  });
+    __syncthreads();
+    // ---- Mbar = L^-T P L^-1 --------------------------------------------------
+    block_product(R, R, R, [&](int i, int k) { return s_d[i * PR + k]; },
+                  [&](int k, int j) { return s_linv[k * PR + j]; },
+                  [&](int i, int j, float v) { s_f[i * PR + j] = v; });
+    __syncthreads();
+    block_product(R, R, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+                  [&](int k, int j) { return s_f[k * PR + j]; },
+                  [&](int i, int j, float v) { s_k[i * PR + j] = v; });
+    __syncthreads();
+
+    // ---- token-map operand records -------------------------------------------
+    const float inv_root = 1.0f / root;
+    const float inv_count = 1.0f / count;
+    uint16_t* rec = a.records + system * a.record_stride;
+    constexpr bool kRank32 = (R % 32) == 0;
+    if (a.feature_k32) {
+        write_records<true>(rec + a.off_m, R, d, [&](int i, int f) { return s_m[i * PD + f] * inv_root; });
+        write_records<true>(rec + a.off_e, R, d, [&](int i, int f) { return s_u[i * PD + f] * inv_root; });
+    } else {
+        write_records<false>(rec + a.off_m, R, d, [&](int i, int f) { return s_m[i * PD + f] * inv_root; });
+        write_records<false>(rec + a.off_e, R, d, [&](int i, int f) { return s_u[i * PD + f] * inv_root; });
+    }
+    write_records<kRank32>(rec + a.off_g, R, R, [&](int i, int k) {
+        return (s_k[i * PR + k] + s_k[k * PR + i]) * inv_count;
+    });
+    write_records<kRank32>(rec + a.off_f, d, R, [&](int f, int k) { return s_u[k * PD + f] * inv_root; });
+}
+
+// ---------------------------------------------------------------------------
+// Token map: one wave per (b, chunk, h), 16 tokens per step.
+template <int R, bool DK32>
+__global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
+    constexpr bool RK32 = (R % 32) == 0;
+    using RR = RecordShape<RK32>;
+    using RD = RecordShape<DK32>;
+    constexpr int RBLK = R / 16;                        // rank row blocks
+    constexpr int RSTEPS = R / RR::kWidth;              // rank K steps
+    constexpr int PAIRS = R / 2;
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wave >= a.total_waves) {
+        return;
+    }
+    int64_t rest = wave;
+    const int64_t h = rest % a.heads;
+    rest /= a.heads;
+    const int64_t chunk = rest % a.chunks;
+    const int64_t b = rest / a.chunks;
+    const int q = lane & 15;
+    const int g = lane >> 4;
+    const int64_t d = a.head_dim;
+    const int64_t system = b * a.heads + h;
+    const int dsteps = static_cast<int>((d + RD::kWidth - 1) / RD::kWidth);
+    const int fblocks = static_cast<int>((d + 15) / 16);
+    const float eta = bounded_complement(a.eta_raw[h]);
+    const uint16_t* rec = a.records + system * a.record_stride;
+    const uint16_t* rec_m = rec + a.off_m;
+    const uint16_t* rec_e = rec + a.off_e;
+    const uint16_t* rec_g = rec + a.off_g;
+    const uint16_t* rec_f = rec + a.off_f;
+
+    const int64_t begin = chunk * a.chunk_tokens;
+    const int64_t end = begin + a.chunk_tokens < a.length ? begin + a.chunk_tokens : a.length;
+    float dot = 0.0f;
+    for (int64_t t0 = begin; t0 < end; t0 += 16) {
+        const int64_t token = t0 + q;
+        const bool live = token < end;
+        const int64_t safe = live ? token : begin;
+        const uint16_t* prow = a.projected + (b * a.length + safe) * a.width;
+        const uint16_t* grow = a.grad_output + (b * a.length + safe) * a.grad_stride + h * d;
+        const uint16_t* crow = prow + a.heads * R + h * d;
+        const uint32_t* phrow = a.phases + b * a.phase_batch_stride + safe * PAIRS;
+        uint16_t* out_row = a.grad_projected + (b * a.length + safe) * a.width;
+
+        // Rotated relation as the B operand (rank K), split hi/lo.
+        typedef typename std::conditional<RK32, u32x4, u32x2>::type RankOp;
+        RankOp a_hi[RSTEPS];
+        RankOp a_lo[RSTEPS];
+#pragma unroll
+        for (int s = 0; s < RSTEPS; ++s) {
+            const int first = RR::kWidth * s + RR::kPerLane * g;
+#pragma unroll
+            for (int p = 0; p < RR::kPerLane / 2; ++p) {
+                const uint32_t rel = live ? *reinterpret_cast<const uint32_t*>(prow + h * R + first + 2 * p) : 0u;
+                const uint32_t ph = live ? phrow[first / 2 + p] : 0u;
+                float e, o;
+                rotate_pair(rel, ph, e, o);
+                uint32_t hi, lo;
+                split_bf16(e, o, hi, lo);
+                a_hi[s][p] = hi;
+                a_lo[s][p] = lo;
+            }
+        }
+        // dY and C as B operands (feature K; exact in BF16), plus <dY, C>.
+        typedef typename std::conditional<DK32, u32x4, u32x2>::type FeatOp;
+        FeatOp y_op[kBwdMaxHeadDim / 16];
+        FeatOp c_op[kBwdMaxHeadDim / 16];
+#pragma unroll
+        for (int s = 0; s < kBwdMaxHeadDim / RD::kWidth; ++s) {
+            if (s < dsteps) {
+                const int first = RD::kWidth * s + RD::kPerLane * g;
+#pragma unroll
+                for (int p = 0; p < RD::kPerLane / 2; ++p) {
+                    const int f = first + 2 * p;
+                    uint32_t yv = 0u, cv = 0u;
+                    if (live && f < d) {
+                        const uint32_t y_lo = grow[f];
+                        const uint32_t c_lo = crow[f];
+                        const uint32_t y_hi = f + 1 < d ? grow[f + 1] : 0u;
+                        const uint32_t c_hi = f + 1 < d ? crow[f + 1] : 0u;
+                        yv = y_lo | (y_hi << 16);
+                        cv = c_lo | (c_hi << 16);
+                    }
+                    y_op[s][p] = yv;
+                    c_op[s][p] = cv;
+                    dot = fmaf(bf16_lo(yv), bf16_lo(cv), dot);
+                    dot = fmaf(bf16_hi(yv), bf16_hi(cv), dot);
+                }
+            }
+        }
+
+        // dA^T blocks: feature-K chain (dY, C) and rank-K chain (A) kept apart.
+#pragma unroll
+        for (int rb = 0; rb < RBLK; ++rb) {
+            f32x4 acc_d = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 acc_r = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < kBwdMaxHeadDim / RD::kWidth; ++s) {
+                if (s < dsteps) {
+                    const int64_t o = ((static_cast<int64_t>(rb) * dsteps + s) * 64 + lane) * RD::kLaneHalfs;
+                    if constexpr (DK32) {
+                        const u32x4 mh = *reinterpret_cast<const u32x4*>(rec_m + o);
+                        const u32x4 ml = *reinterpret_cast<const u32x4*>(rec_m + o + 8);
+                        const u32x4 eh = *reinterpret_cast<const u32x4*>(rec_e + o);
+                        const u32x4 el = *reinterpret_cast<const u32x4*>(rec_e + o + 8);
+                        acc_d = mfma16x16x32(mh, y_op[s], acc_d);
+                        acc_d = mfma16x16x32(ml, y_op[s], acc_d);
+                        acc_d = mfma16x16x32(eh, c_op[s], acc_d);
+                        acc_d = mfma16x16x32(el, c_op[s], acc_d);
+                    } else {
+                        const u32x2 mh = *reinterpret_cast<const u32x2*>(rec_m + o);
+                        const u32x2 ml = *reinterpret_cast<const u32x2*>(rec_m + o + 4);
+                        const u32x2 eh = *reinterpret_cast<const u32x2*>(rec_e + o);
+                        const u32x2 el = *reinterpret_cast<const u32x2*>(rec_e + o + 4);
+                        acc_d = mfma16x16x16(mh, y_op[s], acc_d);
+                        acc_d = mfma16x16x16(ml, y_op[s], acc_d);
+                        acc_d = mfma16x16x16(eh, c_op[s], acc_d);
+                        acc_d = mfma16x16x16(el, c_op[s], acc_d);
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < RSTEPS; ++s) {
+                const int64_t o = ((static_cast<int64_t>(rb) * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
+                if constexpr (RK32) {
+                    const u32x4 gh = *reinterpret_cast<const u32x4*>(rec_g + o);
+                    const u32x4 gl = *reinterpret_cast<const u32x4*>(rec_g + o + 8);
+                    acc_r = mfma16x16x32(gh, a_hi[s], acc_r);
+                    acc_r = mfma16x16x32(gh, a_lo[s], acc_r);
+                    acc_r = mfma16x16x32(gl, a_hi[s], acc_r);
+                } else {
+                    const u32x2 gh = *reinterpret_cast<const u32x2*>(rec_g + o);
+                    const u32x2 gl = *reinterpret_cast<const u32x2*>(rec_g + o + 4);
+                    acc_r = mfma16x16x16(gh, a_hi[s], acc_r);
+                    acc_r = mfma16x16x16(gh, a_lo[s], acc_r);
+                    acc_r = mfma16x16x16(gl, a_hi[s], acc_r);
+                }
+            }
+            // Lane holds dA[token q][ranks 16 rb + 4 g .. +3]: rotate back.
+            if (live) {
+                const int rank0 = 16 * rb + 4 * g;
+                const u32x2 ph = *reinterpret_cast<const u32x2*>(phrow + rank0 / 2);
+                float grad[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    grad[i] = acc_d[i] + acc_r[i];
+                }
+                u32x2 packed;
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const float cosine = f16_lo(ph[p]);
+                    const float sine = f16_hi(ph[p]);
+                    const float even = grad[2 * p] * cosine + grad[2 * p + 1] * sine;
+                    const float odd = grad[2 * p + 1] * cosine - grad[2 * p] * sine;
+                    packed[p] = pack_bf16(even, odd);
+                }
+                *reinterpret_cast<u32x2*>(out_row + h * R + rank0) = packed;
+            }
+        }
+        // dC^T blocks: eta dY + (ds / sqrt(n))^T A^T.
+#pragma unroll
+        for (int fb = 0; fb < kBwdMaxHeadDim / 16; ++fb) {
+            if (fb < fblocks) {
+                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int s = 0; s < RSTEPS; ++s) {
+                    const int64_t o = ((static_cast<int64_t>(fb) * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
+                    if constexpr (RK32) {
+                        const u32x4 fh = *reinterpret_cast<const u32x4*>(rec_f + o);
+                        const u32x4 fl = *reinterpret_cast<const u32x4*>(rec_f + o + 8);
+                        acc = mfma16x16x32(fh, a_hi[s], acc);
+                        acc = mfma16x16x32(fh, a_lo[s], acc);
+                        acc = mfma16x16x32(fl, a_hi[s], acc);
+                    } else {
+                        const u32x2 fh = *reinterpret_cast<const u32x2*>(rec_f + o);
+                        const u32x2 fl = *reinterpret_cast<const u32x2*>(rec_f + o + 4);
+                        acc = mfma16x16x16(fh, a_hi[s], acc);
+                        acc = mfma16x16x16(fh, a_lo[s], acc);
+                        acc = mfma16x16x16(fl, a_hi[s], acc);
+                    }
+                }
+                if (live) {
+                    const int f0 = 16 * fb + 4 * g;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (f0 + i < d) {
+                            const float dy = bf16_bits_to_float(grow[f0 + i]);
+                            out_row[a.heads * R + h * d + f0 + i] = to_bf16_bits(fmaf(eta, dy, acc[i]));
+                        }
+                    }
+                }
+            }
+        }
+    }
+    // <dY, C> of this wave's tokens.
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        dot += __shfl_xor(dot, offset);
+    }
+    if (lane == 0) {
+        a.dot_part[system * a.chunks + chunk] = dot;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Parameter gradients: sums over the batch in ascending order.
+__global__ __launch_bounds__(256) void param_reduce_kernel(ParamReduceArgs a) {
+    const int64_t per_head = a.rank * a.rank + a.head_dim * a.rank + 1;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= a.heads * per_head) {
+        return;
+    }
+    const int64_t h = idx / per_head;
+    const int64_t e = idx - h * per_head;
+    const int64_t rr = a.rank * a.rank;
+    const int64_t dr = a.head_dim * a.rank;
+    float acc = 0.0f;
+    for (int64_t b = 0; b < a.batch; ++b) {
+        const int64_t system = b * a.heads + h;
+        if (e < rr) {
+            acc += a.dtheta_part[system * rr + e];
+        } else if (e < rr + dr) {
+            acc += a.ddrive_part[system * dr + (e - rr)];
+        } else {
+            float value = a.deta_part[system];
+            for (int64_t ch = 0; ch < a.chunks; ++ch) {
+                value += a.dot_part[system * a.chunks + ch];
+            }
+            acc += value;
+        }
+    }
+    if (e < rr) {
+        a.grad_base[h * rr + e] = acc;
+    } else if (e < rr + dr) {
+        a.grad_drive[h * dr + (e - rr)] = acc;
+    } else {
+        a.grad_eta[h] = acc * bounded_complement_derivative(a.eta_raw[h]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers.
+int64_t bwd_record_layout(int64_t rank, int64_t head_dim, int64_t* off_m, int64_t* off_e,
+                          int64_t* off_g, int64_t* off_f, int* feature_k32) {
+    const bool dk32 = head_dim % 32 == 0;
+    const bool rk32 = rank % 32 == 0;
+    const int64_t feature = dk32 ? record_halfs<true>(rank, head_dim) : record_halfs<false>(rank, head_dim);
+    const int64_t gram = rk32 ? record_halfs<true>(rank, rank) : record_halfs<false>(rank, rank);
+    const int64_t content = rk32 ? record_halfs<true>(head_dim, rank) : record_halfs<false>(head_dim, rank);
+    *off_m = 0;
+    *off_e = feature;
+    *off_g = 2 * feature;
+    *off_f = 2 * feature + gram;
+    *feature_k32 = dk32 ? 1 : 0;
+    return 2 * feature + gram + content;
+}
+
+hipError_t launch_bwd_solve(int rank, const BwdSolveArgs& a, int64_t systems, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(systems));
+    switch (rank) {
+        case 16: bwd_solve_kernel<16><<<grid, kBwdThreads, 0, stream>>>(a); break;
+        case 32: bwd_solve_kernel<32><<<grid, kBwdThreads, 0, stream>>>(a); break;
+        case 48: bwd_solve_kernel<48><<<grid, kBwdThreads, 0, stream>>>(a); break;
+        default: bwd_solve_kernel<64><<<grid, kBwdThreads, 0, stream>>>(a); break;
+    }
+    return hipGetLastError();
+}
+
+template <int R>
+static hipError_t launch_bwd_apply_r(const BwdApplyArgs& a, bool dk32, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((a.total_waves + 3) / 4));
+    if (dk32) {
+        bwd_apply_kernel<R, true><<<grid, 256, 0, stream>>>(a);
+    } else {
+        bwd_apply_kernel<R, false><<<grid, 256, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, hipStream_t stream) {
+    switch (rank) {
+        case 16: return launch_bwd_apply_r<16>(a, dk32, stream);
+        case 32: return launch_bwd_apply_r<32>(a, dk32, stream);
+        case 48: return launch_bwd_apply_r<48>(a, dk32, stream);
+        default: return launch_bwd_apply_r<64>(a, dk32, stream);
+    }
+}
+
+hipError_t launch_param_reduce(const ParamReduceArgs& a, hipStream_t stream) {
+    const int64_t total = a.heads * (a.rank * a.rank + a.head_dim * a.rank + 1);
+    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+    param_reduce_kernel<<<grid, 256, 0, stream>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace lsso_hip

@@ -232,6 +232,9 @@ int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* proj
 
     lsso_hip::ReduceArgs reduce{};
     reduce.projected = static_cast<const uint16_t*>(projected);
+    reduce.content = static_cast<const uint16_t*>(projected) + plan.heads * plan.rank;
+    reduce.content_stride = plan.width;
+    reduce.gram = 1;
     reduce.phases = buf.phases;
     reduce.partials = buf.partials;
     reduce.batch = plan.batch;
@@ -426,6 +429,231 @@ int lsso_hip_mixer_forward_projected(const lsso_hip_mixer_shape* shape, const vo
     error = lsso_hip::launch_mix_project(static_cast<int>(plan.rank), mix, y_dtype, stream);
     if (error != hipSuccess) {
         return hip_failure(error, "mix_project_kernel launch");
+    }
+    return LSSO_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+struct BackwardPlan {
+    int64_t record_stride, off_m, off_e, off_g, off_f;
+    int feature_k32;
+    size_t off_phases, off_partials, off_records, off_dtheta, off_ddrive, off_deta, off_dot, total;
+};
+
+int make_backward_plan(const MixerPlan& plan, BackwardPlan* bp) {
+    if (!lsso_hip::backward_supported(plan.rank, plan.head_dim)) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "the HIP mixer backward supports head_dim <= 64, got " +
+                        std::to_string(plan.head_dim));
+    }
+    bp->record_stride = lsso_hip::bwd_record_layout(plan.rank, plan.head_dim, &bp->off_m, &bp->off_e,
+                                                    &bp->off_g, &bp->off_f, &bp->feature_k32);
+    const int64_t systems = plan.batch * plan.heads;
+    size_t offset = 0;
+    bp->off_phases = offset;
+    offset = align_up(offset + sizeof(uint32_t) * plan.phase_batches * plan.length * plan.pairs);
+    bp->off_partials = offset;
+    offset = align_up(offset + sizeof(float) * systems * plan.reduce_chunks * plan.partial_stride);
+    bp->off_records = offset;
+    offset = align_up(offset + sizeof(uint16_t) * systems * bp->record_stride);
+    bp->off_dtheta = offset;
+    offset = align_up(offset + sizeof(float) * systems * plan.rank * plan.rank);
+    bp->off_ddrive = offset;
+    offset = align_up(offset + sizeof(float) * systems * plan.head_dim * plan.rank);
+    bp->off_deta = offset;
+    offset = align_up(offset + sizeof(float) * systems);
+    bp->off_dot = offset;
+    offset = align_up(offset + sizeof(float) * systems * plan.apply_chunks);
+    bp->total = offset;
+    return LSSO_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lsso_hip_mixer_backward_workspace_bytes(const lsso_hip_mixer_shape* shape, int positions_mode,
+                                            size_t* bytes) {
+    if (bytes == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "bytes must not be NULL");
+    }
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    BackwardPlan bp;
+    status = make_backward_plan(plan, &bp);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    *bytes = bp.total;
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape, const void* grad_output,
+                            const void* projected, const float* core_base_raw,
+                            const float* core_drive_weight, const float* eta_raw,
+                            const float* inverse_frequency, const float* centered_positions,
+                            int positions_mode, const float* valid_counts, const float* tape,
+                            void* grad_projected, float* grad_base, float* grad_drive,
+                            float* grad_eta, void* workspace, size_t workspace_bytes,
+                            void* stream_handle) {
+    (void)core_base_raw;  // Theta is read from the tape
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    BackwardPlan bp;
+    status = make_backward_plan(plan, &bp);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    if (grad_output == nullptr || projected == nullptr || core_drive_weight == nullptr ||
+        eta_raw == nullptr || tape == nullptr || grad_projected == nullptr || grad_base == nullptr ||
+        grad_drive == nullptr || grad_eta == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "backward tensors must not be NULL");
+    }
+    if (positions_mode != LSSO_HIP_POSITIONS_DEFAULT && centered_positions == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "centered_positions must not be NULL for this positions_mode");
+    }
+    if (workspace == nullptr || workspace_bytes < bp.total || !aligned(workspace, 256)) {
+        return fail(LSSO_HIP_EINVAL,
+                    "workspace must be 256-byte aligned and hold lsso_hip_mixer_backward_workspace_bytes()");
+    }
+    if (!aligned(grad_output, 4) || !aligned(projected, 4) || !aligned(grad_projected, 8)) {
+        return fail(LSSO_HIP_EINVAL, "grad_output, projected and grad_projected must be aligned bfloat16 buffers");
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    char* ws = static_cast<char*>(workspace);
+    uint32_t* phases = reinterpret_cast<uint32_t*>(ws + bp.off_phases);
+    float* partials = reinterpret_cast<float*>(ws + bp.off_partials);
+    uint16_t* records = reinterpret_cast<uint16_t*>(ws + bp.off_records);
+    float* dtheta = reinterpret_cast<float*>(ws + bp.off_dtheta);
+    float* ddrive = reinterpret_cast<float*>(ws + bp.off_ddrive);
+    float* deta = reinterpret_cast<float*>(ws + bp.off_deta);
+    float* dot = reinterpret_cast<float*>(ws + bp.off_dot);
+
+    lsso_hip::PhaseArgs phase{};
+    phase.positions = positions_mode == LSSO_HIP_POSITIONS_DEFAULT ? nullptr : centered_positions;
+    phase.phases = phases;
+    phase.count = plan.phase_batches * plan.length * plan.pairs;
+    phase.length = plan.length;
+    phase.pairs = static_cast<int>(plan.pairs);
+    for (int j = 0; j < plan.pairs; ++j) {
+        phase.inverse_frequency[j] = inverse_frequency != nullptr
+            ? inverse_frequency[j]
+            : std::pow(10000.0f, -static_cast<float>(j) / static_cast<float>(plan.pairs));
+    }
+    hipError_t error = lsso_hip::launch_phase(phase, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "phase_kernel launch");
+    }
+
+    // dm partials: A^T dY per chunk through the forward's reduction.
+    const bool vec = plan.width % 8 == 0 && plan.head_dim % 4 == 0 && aligned(projected, 16) &&
+                     aligned(grad_output, 16);
+    lsso_hip::ReduceArgs reduce{};
+    reduce.projected = static_cast<const uint16_t*>(projected);
+    reduce.content = static_cast<const uint16_t*>(grad_output);
+    reduce.content_stride = plan.out_width;
+    reduce.gram = 0;
+    reduce.phases = phases;
+    reduce.partials = partials;
+    reduce.batch = plan.batch;
+    reduce.length = plan.length;
+    reduce.heads = plan.heads;
+    reduce.head_dim = plan.head_dim;
+    reduce.width = plan.width;
+    reduce.phase_batch_stride = phase_batch_stride(plan, positions_mode);
+    reduce.chunks = plan.reduce_chunks;
+    reduce.chunk_tokens = plan.reduce_chunk_tokens;
+    reduce.column_groups = plan.column_groups;
+    reduce.partial_stride = plan.partial_stride;
+    reduce.total_waves = plan.batch * plan.heads * plan.reduce_chunks * plan.column_groups;
+    error = lsso_hip::launch_reduce(static_cast<int>(plan.rank), reduce, plan.cpw, vec, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "reduce_kernel launch (backward)");
+    }
+
+    lsso_hip::BwdSolveArgs solve{};
+    solve.partials = partials;
+    solve.chunks = plan.reduce_chunks;
+    solve.partial_stride = plan.partial_stride;
+    solve.tape = tape;
+    solve.tape_stride = plan.tape_stride;
+    solve.drive = core_drive_weight;
+    solve.eta_raw = eta_raw;
+    solve.valid_counts = valid_counts;
+    solve.batch = plan.batch;
+    solve.length = plan.length;
+    solve.heads = plan.heads;
+    solve.head_dim = plan.head_dim;
+    solve.records = records;
+    solve.record_stride = bp.record_stride;
+    solve.off_m = bp.off_m;
+    solve.off_e = bp.off_e;
+    solve.off_g = bp.off_g;
+    solve.off_f = bp.off_f;
+    solve.feature_k32 = bp.feature_k32;
+    solve.dtheta_part = dtheta;
+    solve.ddrive_part = ddrive;
+    solve.deta_part = deta;
+    error = lsso_hip::launch_bwd_solve(static_cast<int>(plan.rank), solve, plan.batch * plan.heads,
+                                       stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "bwd_solve_kernel launch");
+    }
+
+    lsso_hip::BwdApplyArgs apply{};
+    apply.projected = static_cast<const uint16_t*>(projected);
+    apply.grad_output = static_cast<const uint16_t*>(grad_output);
+    apply.grad_stride = plan.out_width;
+    apply.phases = phases;
+    apply.phase_batch_stride = phase_batch_stride(plan, positions_mode);
+    apply.records = records;
+    apply.record_stride = bp.record_stride;
+    apply.off_m = bp.off_m;
+    apply.off_e = bp.off_e;
+    apply.off_g = bp.off_g;
+    apply.off_f = bp.off_f;
+    apply.eta_raw = eta_raw;
+    apply.grad_projected = static_cast<uint16_t*>(grad_projected);
+    apply.dot_part = dot;
+    apply.batch = plan.batch;
+    apply.length = plan.length;
+    apply.heads = plan.heads;
+    apply.head_dim = plan.head_dim;
+    apply.width = plan.width;
+    apply.chunks = plan.apply_chunks;
+    apply.chunk_tokens = plan.apply_chunk_tokens;
+    apply.total_waves = plan.batch * plan.heads * plan.apply_chunks;
+    error = lsso_hip::launch_bwd_apply(static_cast<int>(plan.rank), apply, bp.feature_k32 != 0, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "bwd_apply_kernel launch");
+    }
+
+    lsso_hip::ParamReduceArgs params{};
+    params.dtheta_part = dtheta;
+    params.ddrive_part = ddrive;
+    params.deta_part = deta;
+    params.dot_part = dot;
+    params.eta_raw = eta_raw;
+    params.grad_base = grad_base;
+    params.grad_drive = grad_drive;
+    params.grad_eta = grad_eta;
+    params.batch = plan.batch;
+    params.heads = plan.heads;
+    params.rank = plan.rank;
+    params.head_dim = plan.head_dim;
+    params.chunks = plan.apply_chunks;
+    error = lsso_hip::launch_param_reduce(params, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "param_reduce_kernel launch");
     }
     return LSSO_HIP_OK;
 }

@@ -91,6 +91,13 @@ __device__ __forceinline__ float bounded_complement(float raw) {
     return kInteriorScale * (numerator / (1.0f + exponent));
 }
 
+// d eta / d raw of bounded_complement (reference csrc/ball/common.cuh:30-34).
+__device__ __forceinline__ float bounded_complement_derivative(float raw) {
+    const float exponent = raw >= 0.0f ? expf(-2.0f * raw) : expf(2.0f * raw);
+    const float denominator = 1.0f + exponent;
+    return kInteriorScale * 4.0f * exponent / (denominator * denominator);
+}
+
 // torch.nn.functional.softplus with beta=1, threshold=20.
 __device__ __forceinline__ float softplus_one(float raw) {
     const float shifted = raw + kSoftplusOneOffset;

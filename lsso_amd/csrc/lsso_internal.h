@@ -20,7 +20,10 @@ struct PhaseArgs {
 };
 
 struct ReduceArgs {
-    const uint16_t* projected;  // BF16 [B, N, width]
+    const uint16_t* projected;  // BF16 [B, N, width] (relation columns)
+    const uint16_t* content;    // BF16 rows whose head-h columns are contracted with A
+    int64_t content_stride;     // elements between consecutive tokens of `content`
+    int gram;                   // also accumulate G = A^T A
     const uint32_t* phases;
     float* partials;            // [B, H, chunks, partial_stride]
     int64_t batch;
@@ -97,6 +100,67 @@ struct MixProjectArgs {
     int64_t range_tokens;       // multiple of the 64-token tile
 };
 
+// Backward of the mixer (one compact system per workgroup).
+struct BwdSolveArgs {
+    const float* partials;      // S-part holds A^T dY per chunk
+    int64_t chunks;
+    int64_t partial_stride;
+    const float* tape;          // [L | Theta | (I+K)^-1 | L^-1 | Z | U] per system
+    int64_t tape_stride;
+    const float* drive;         // [H, d, R]
+    const float* eta_raw;       // [H]
+    const float* valid_counts;  // [B] or nullptr
+    int64_t batch;
+    int64_t length;
+    int64_t heads;
+    int64_t head_dim;
+    uint16_t* records;          // token-map operand records per system
+    int64_t record_stride;      // in bf16
+    int64_t off_m, off_e, off_g, off_f;
+    int feature_k32;
+    float* dtheta_part;         // [B*H, R, R]
+    float* ddrive_part;         // [B*H, d, R]
+    float* deta_part;           // [B*H]
+};
+
+struct BwdApplyArgs {
+    const uint16_t* projected;  // BF16 [B, N, width]
+    const uint16_t* grad_output;// BF16 [B, N, H*d]
+    int64_t grad_stride;        // H*d
+    const uint32_t* phases;
+    int64_t phase_batch_stride;
+    const uint16_t* records;
+    int64_t record_stride;
+    int64_t off_m, off_e, off_g, off_f;
+    const float* eta_raw;
+    uint16_t* grad_projected;   // BF16 [B, N, width]
+    float* dot_part;            // [B*H, chunks]: <dY, C> per chunk
+    int64_t batch;
+    int64_t length;
+    int64_t heads;
+    int64_t head_dim;
+    int64_t width;
+    int64_t chunks;
+    int64_t chunk_tokens;       // multiple of 16
+    int64_t total_waves;
+};
+
+struct ParamReduceArgs {
+    const float* dtheta_part;
+    const float* ddrive_part;
+    const float* deta_part;
+    const float* dot_part;
+    const float* eta_raw;
+    float* grad_base;           // [H, R, R]
+    float* grad_drive;          // [H, d, R]
+    float* grad_eta;            // [H]
+    int64_t batch;
+    int64_t heads;
+    int64_t rank;
+    int64_t head_dim;
+    int64_t chunks;
+};
+
 struct LinearArgs {
     const void* x;
     int64_t rows;
@@ -125,6 +189,15 @@ hipError_t launch_apply(int rank, const ApplyArgs& a, int nfbw, bool vec, hipStr
 bool mix_project_supported(int64_t rank, int64_t heads, int64_t head_dim, int64_t width);
 int mix_project_tile_rows();
 hipError_t launch_mix_project(int rank, const MixProjectArgs& a, int y_dtype, hipStream_t stream);
+
+bool backward_supported(int64_t rank, int64_t head_dim);
+// Record offsets (bf16 elements) of the token-map operands of one system;
+// returns the per-system record size.
+int64_t bwd_record_layout(int64_t rank, int64_t head_dim, int64_t* off_m, int64_t* off_e,
+                          int64_t* off_g, int64_t* off_f, int* feature_k32);
+hipError_t launch_bwd_solve(int rank, const BwdSolveArgs& a, int64_t systems, hipStream_t stream);
+hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, hipStream_t stream);
+hipError_t launch_param_reduce(const ParamReduceArgs& a, hipStream_t stream);
 
 hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,
                          int grid_groups, hipStream_t stream);

@@ -126,7 +126,8 @@ __device__ __forceinline__ void reduce_load(ReduceTile<R, CPW>& t, const ReduceA
         for (int c = 0; c < CPW; ++c) {
             const int64_t feature = 2 * (static_cast<int64_t>(cg) * 16 * CPW + 16 * c + q);
             const bool fv = live && feature < a.head_dim;
-            t.con[j][c] = fv ? load_pair<VEC>(row + a.heads * R + h * a.head_dim + feature,
+            const uint16_t* content_row = a.content + (b * a.length + (live ? token : 0)) * a.content_stride;
+            t.con[j][c] = fv ? load_pair<VEC>(content_row + h * a.head_dim + feature,
                                               feature + 1 < a.head_dim)
                              : 0u;
         }
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
     const int64_t b = rest / a.chunks;
     const int q = lane & 15;
     const int g = lane >> 4;
-    const bool do_gram = cg == 0;
+    const bool do_gram = a.gram != 0 && cg == 0;
 
     f32x4 acc_g[NGB];
     f32x4 acc_s[NRB][2 * CPW];
