@@ -278,36 +278,9 @@ class LSSO(nn.Module):
 
         from . import hip
 
-        batch, length, _dim = x.shape
-        all_valid = valid_mask is None
-        mask = (
-            None
-            if all_valid
-            else self._validate_mask(valid_mask, batch=batch, length=length, device=x.device)
+        projected, centered_positions, valid_counts, mask = self._native_inputs(
+            x, valid_mask, position_ids
         )
-        centered_positions = None
-        if valid_mask is not None or position_ids is not None:
-            centered = self._center_positions(
-                position_ids,
-                mask,
-                dtype=torch.float32,
-                all_valid=all_valid,
-                batch=batch,
-                length=length,
-                device=x.device,
-            )
-            if position_ids is None or position_ids.ndim == 1:
-                centered_positions = centered[0].contiguous() if all_valid else centered.contiguous()
-            else:
-                centered_positions = centered.contiguous()
-        valid_counts = (
-            None
-            if all_valid
-            else mask.sum(dim=-1).to(dtype=torch.float32).clamp_min(1.0).contiguous()
-        )
-        # Masked rows are neither read nor biased: the projection writes zeros
-        # there (reference model.py:371-383, 402-404).
-        projected = hip.linear(x, self.w_bc.weight, self.w_bc.bias, torch.bfloat16, row_mask=mask)
         needs_grad = torch.is_grad_enabled() and any(
             parameter.requires_grad for parameter in (x, *self.parameters())
         )
@@ -339,6 +312,116 @@ class LSSO(nn.Module):
         return hip.linear(mixed, self.w_o.weight, self.w_o.bias, x.dtype, row_mask=mask)
 
     # -- reference path (reference model.py:407-496, 562-585) ---------------
+    def _native_inputs(
+        self,
+        x: torch.Tensor,
+        valid_mask: torch.Tensor | None,
+        position_ids: torch.Tensor | None,
+    ):
+        """Packed projection (native K1) and the mixer's positions / counts."""
+
+        from . import hip
+
+        batch, length, _dim = x.shape
+        all_valid = valid_mask is None
+        mask = (
+            None
+            if all_valid
+            else self._validate_mask(valid_mask, batch=batch, length=length, device=x.device)
+        )
+        centered_positions = None
+        if valid_mask is not None or position_ids is not None:
+            centered = self._center_positions(
+                position_ids,
+                mask,
+                dtype=torch.float32,
+                all_valid=all_valid,
+                batch=batch,
+                length=length,
+                device=x.device,
+            )
+            if position_ids is None or position_ids.ndim == 1:
+                centered_positions = centered[0].contiguous() if all_valid else centered.contiguous()
+            else:
+                centered_positions = centered.contiguous()
+        valid_counts = (
+            None
+            if all_valid
+            else mask.sum(dim=-1).to(dtype=torch.float32).clamp_min(1.0).contiguous()
+        )
+        # Masked rows are neither read nor biased: the projection writes zeros
+        # there (reference model.py:371-383, 402-404).
+        projected = hip.linear(x, self.w_bc.weight, self.w_bc.bias, torch.bfloat16, row_mask=mask)
+        return projected, centered_positions, valid_counts, mask
+
+    @torch.no_grad()
+    def diagnostics(
+        self,
+        x: torch.Tensor,
+        valid_mask: torch.Tensor | None = None,
+        position_ids: torch.Tensor | None = None,
+        *,
+        adjoint_rhs: torch.Tensor,
+        implementation: str = "reference",
+    ) -> dict[str, torch.Tensor]:
+        """Per-sample, per-head FP64 certificates of the realized operator
+        (reference model.py:498-522): token gain q, mu, solve/adjoint ratios.
+
+        ``implementation="reference"`` realizes the compact problem with the
+        canonical torch path, as the reference does.  ``"hip"`` (or
+        ``"cuda"``) certifies the operator that the native kernels realize,
+        from their compact tape: P^T P = I - L^-1 L^-T, I + K from Theta, Z.
+        """
+
+        self._validate_input(x)
+        if self.config.core_mode is CoreMode.ZERO:
+            raise ValueError("compact diagnostics require a nonzero compact core")
+        if implementation == "reference":
+            _projected, frame, compact_state, _content, generator, eta, _mask = (
+                self._reference_compact_problem(x, valid_mask, position_ids)
+            )
+            assert generator is not None
+            return canonical.compact_equilibrium_diagnostics(
+                frame, generator, compact_state, eta,
+                adjoint_rhs.to(device=x.device, dtype=compact_state.dtype),
+            )
+        if implementation not in ("hip", "cuda"):
+            raise ValueError(
+                "implementation must be 'reference', 'hip' or 'cuda', got " f"{implementation!r}"
+            )
+        if self.config.core_mode is not CoreMode.DYNAMIC or not self.config.rank_rotary:
+            raise ValueError(
+                f"implementation={implementation!r} diagnostics require the dynamic rank-rotary core"
+            )
+        from . import hip
+
+        config = self.config
+        batch, length, _dim = x.shape
+        rank, heads, head_dim = config.rank, config.num_heads, config.head_dim
+        if length < rank:
+            raise ValueError(
+                f"compact diagnostics require sequence length N >= rank R, got N={length}, R={rank}"
+            )
+        projected, positions, counts, _mask = self._native_inputs(x, valid_mask, position_ids)
+        _mixed, tape = hip.forward_train(
+            projected, self.core_base_raw, self.core_drive_weight, self.eta_raw, positions, counts
+        )
+        rr, rd = rank * rank, rank * head_dim
+        tape = tape.view(batch, heads, 4 * rr + 2 * rd).double()
+        linv = tape[..., 3 * rr:4 * rr].reshape(batch, heads, rank, rank)
+        theta = tape[..., rr:2 * rr].reshape(batch, heads, rank, rank)
+        compact_state = tape[..., 4 * rr:4 * rr + rd].reshape(batch, heads, rank, head_dim)
+        identity = torch.eye(rank, dtype=torch.float64, device=x.device)
+        frame_gram = identity - linv @ linv.mT
+        system = identity + canonical.accretive_generator(theta)
+        rhs = adjoint_rhs.to(device=x.device, dtype=torch.float64)
+        if tuple(rhs.shape) != tuple(compact_state.shape):
+            raise ValueError(
+                f"adjoint_rhs must have shape {tuple(compact_state.shape)}, got {tuple(rhs.shape)}"
+            )
+        eta = self.complement().to(device=x.device, dtype=torch.float64)
+        return canonical._equilibrium_certificates(frame_gram, system, compact_state, eta, rhs, length)
+
     def _reference_compact_problem(
         self,
         x: torch.Tensor,

@@ -156,10 +156,120 @@ def accretive_equilibrium_mix(
     return eta_batch * content + frame @ compact
 
 
+def _equilibrium_certificates(
+    frame_gram: torch.Tensor,
+    system: torch.Tensor,
+    compact_state: torch.Tensor,
+    eta: torch.Tensor,
+    adjoint_rhs: torch.Tensor,
+    length: int,
+) -> dict[str, torch.Tensor]:
+    """FP64 certificates of T = eta I_N + P (2 (I + K)^-1 - I - eta I_r) P^T
+    given only compact quantities: P^T P, I + K, Z and the adjoint RHS."""
+
+    rank = system.shape[-1]
+    heads = system.shape[1]
+    identity = torch.eye(rank, dtype=torch.float64, device=system.device)
+    eta = eta.view(1, heads)
+    # Restricted to range(P), T acts as eta I + S^1/2 V^T (Refl - eta I) V S^1/2
+    # in the eigenbasis P^T P = V S V^T; on range(P)'s complement it is eta I.
+    values, vectors = torch.linalg.eigh(frame_gram)
+    root_values = values.clamp_min(0.0).sqrt()
+    reflection = 2.0 * torch.linalg.solve(system, identity.expand_as(system)) - identity
+    eta_identity = eta[..., None, None] * identity
+    block = eta_identity + root_values[..., :, None] * (
+        vectors.mT @ (reflection - eta_identity) @ vectors
+    ) * root_values[..., None, :]
+    gain = torch.linalg.svdvals(block)[..., 0]
+    if length > rank:
+        gain = torch.maximum(gain, eta.abs())
+    mu = torch.linalg.eigvalsh(0.5 * (system + system.mT))[..., 0]
+    tiny = torch.finfo(torch.float64).tiny
+    state = torch.linalg.solve(system, compact_state)
+    adjoint = torch.linalg.solve(system.mT, adjoint_rhs)
+    state_ratio = torch.linalg.vector_norm(state, dim=(-2, -1)) / torch.linalg.vector_norm(
+        compact_state, dim=(-2, -1)
+    ).clamp_min(tiny)
+    adjoint_ratio = torch.linalg.vector_norm(adjoint, dim=(-2, -1)) / torch.linalg.vector_norm(
+        adjoint_rhs, dim=(-2, -1)
+    ).clamp_min(tiny)
+    return {
+        "q": gain,
+        "contraction_slack": 1.0 - gain,
+        "mu": mu,
+        "state_ratio": state_ratio,
+        "adjoint_ratio": adjoint_ratio,
+        "state_bound_usage": mu * state_ratio,
+        "adjoint_bound_usage": mu * adjoint_ratio,
+    }
+
+
+def compact_equilibrium_diagnostics(
+    frame: torch.Tensor,
+    generator: torch.Tensor,
+    compact_state: torch.Tensor,
+    eta: torch.Tensor,
+    adjoint_rhs: torch.Tensor,
+) -> dict[str, torch.Tensor]:
+    """Realized token gain q = ||T||_2, the accretivity floor mu =
+    lambda_min(sym(I + K)) and the solve / adjoint ratios, all [B, H] and in
+    FP64 (reference.py:575-688).  The N x N operator is never formed: its
+    norm follows from the R x R certificate block (requires N >= R)."""
+
+    if frame.ndim != 4:
+        raise ValueError("frame must have shape [B, H, N, R]")
+    if generator.ndim not in (3, 4):
+        raise ValueError("generator must have shape [H, R, R] or [B, H, R, R]")
+    if compact_state.ndim != 4 or adjoint_rhs.ndim != 4:
+        raise ValueError("compact_state and adjoint_rhs must have shape [B, H, R, D]")
+    batch, heads, length, rank = frame.shape
+    if length < rank:
+        raise ValueError(
+            f"compact diagnostics require sequence length N >= rank R, got N={length}, R={rank}"
+        )
+    state_shape = (batch, heads, rank, compact_state.shape[-1])
+    if tuple(compact_state.shape) != state_shape:
+        raise ValueError(f"compact_state must have shape {state_shape}, got {tuple(compact_state.shape)}")
+    if adjoint_rhs.shape != compact_state.shape:
+        raise ValueError(
+            f"adjoint_rhs must match compact_state, got {tuple(adjoint_rhs.shape)} and "
+            f"{tuple(compact_state.shape)}"
+        )
+    if tuple(eta.shape) != (heads,):
+        raise ValueError(f"eta must have shape [{heads}], got {tuple(eta.shape)}")
+    if generator.ndim == 3:
+        if tuple(generator.shape) != (heads, rank, rank):
+            raise ValueError(
+                f"static generator must have shape {(heads, rank, rank)}, got {tuple(generator.shape)}"
+            )
+        generator = generator.unsqueeze(0).expand(batch, -1, -1, -1)
+    elif tuple(generator.shape) != (batch, heads, rank, rank):
+        raise ValueError(
+            f"dynamic generator must have shape {(batch, heads, rank, rank)}, got {tuple(generator.shape)}"
+        )
+    others = (generator, compact_state, eta, adjoint_rhs)
+    if any(value.device != frame.device for value in others):
+        raise ValueError("all diagnostic inputs must share a device")
+    if any(not value.is_floating_point() for value in (frame, *others)):
+        raise TypeError("all diagnostic inputs must be floating-point tensors")
+    with torch.autocast(device_type=frame.device.type, enabled=False):
+        frame64 = frame.to(dtype=torch.float64)
+        identity = torch.eye(rank, dtype=torch.float64, device=frame.device)
+        return _equilibrium_certificates(
+            frame64.mT @ frame64,
+            generator.to(dtype=torch.float64) + identity,
+            compact_state.to(dtype=torch.float64),
+            eta.to(dtype=torch.float64),
+            adjoint_rhs.to(dtype=torch.float64),
+            length,
+        )
+
+
 __all__ = [
     "accretive_equilibrium_mix",
     "accretive_generator",
     "bounded_complement",
+    "compact_equilibrium_diagnostics",
     "linear",
     "qr_soft_frame",
     "rank_rotary",
