@@ -722,12 +722,46 @@ def _linear_forward(
 
 
 
+def _mm_fp32(left: torch.Tensor, right: torch.Tensor) -> torch.Tensor:
+    """FP32 result of BF16 operands with FP32 accumulation (hipBLASLt)."""
+
+    try:
+        return torch.mm(left, right, out_dtype=torch.float32)
+    except (NotImplementedError, RuntimeError, TypeError):
+        return left.float() @ right.float()
+
+
+def _weight_gradient(gradient: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+    """FP32 [out, in] = bf16(gradient)^T bf16(value), FP32 accumulation.
+
+    The contraction runs over every row, so it is split over row chunks
+    (batched GEMMs, one output tile set per chunk) and the chunk partials are
+    summed in FP32 in chunk order; a single GEMM would leave most of the
+    device idle on its few output tiles."""
+
+    rows = gradient.shape[0]
+    chunks = 1
+    while chunks < 64 and rows % (2 * chunks) == 0 and rows // (2 * chunks) >= 1024:
+        chunks *= 2
+    if chunks == 1:
+        return _mm_fp32(gradient.mT, value)
+    grad_chunks = gradient.reshape(chunks, rows // chunks, gradient.shape[1])
+    value_chunks = value.reshape(chunks, rows // chunks, value.shape[1])
+    try:
+        partial = torch.bmm(grad_chunks.mT, value_chunks, out_dtype=torch.float32)
+    except (NotImplementedError, RuntimeError, TypeError):
+        partial = torch.bmm(grad_chunks.mT.float(), value_chunks.float())
+    return partial.sum(dim=0)
+
+
 class _Linear(torch.autograd.Function):
     """Autograd of the native projection with the reference's VJP
     (lsso/ball/reference.py:205-247): BF16 operands with FP32 accumulation
     for the value and weight gradients, an FP32 sum of the upstream gradient
-    for the bias.  These are plain library GEMMs (hipBLASLt through torch);
-    rows excluded by ``row_mask`` carry no gradient."""
+    for the bias.  The value gradient runs on the native projection kernel
+    (dX = bf16(dY) bf16(W), stored once in the value's dtype); the weight
+    gradient, a reduction over all rows, is a library GEMM.  Rows excluded
+    by ``row_mask`` carry no gradient."""
 
     @staticmethod
     def forward(ctx, value, weight, bias, output_dtype, row_mask):
@@ -743,17 +777,19 @@ class _Linear(torch.autograd.Function):
         value, weight, row_mask = ctx.saved_tensors
         if row_mask is not None:
             grad_output = torch.where(row_mask[..., None], grad_output, torch.zeros_like(grad_output))
-        flat_gradient = grad_output.to(dtype=torch.bfloat16).reshape(-1, weight.shape[0]).float()
-        weight_bf16 = weight.to(dtype=torch.bfloat16).float()
         grad_value = grad_weight = grad_bias = None
+        flat_gradient = grad_output.to(dtype=torch.bfloat16).reshape(-1, weight.shape[0])
         if ctx.needs_input_grad[0]:
-            grad_value = flat_gradient @ weight_bf16
-            if value.dtype == torch.bfloat16:
-                grad_value = grad_value.to(dtype=torch.bfloat16)
-            grad_value = grad_value.to(dtype=value.dtype).reshape(value.shape)
+            if value.dtype in (torch.float16, torch.bfloat16) and weight.shape[0] <= 512:
+                grad_value = _linear_forward(
+                    flat_gradient, weight.mT.contiguous(), None, value.dtype
+                ).reshape(value.shape)
+            else:
+                grad_value = _mm_fp32(flat_gradient, weight.to(dtype=torch.bfloat16))
+                grad_value = grad_value.to(dtype=value.dtype).reshape(value.shape)
         if ctx.needs_input_grad[1]:
-            flat_value = value.to(dtype=torch.bfloat16).reshape(-1, value.shape[-1]).float()
-            grad_weight = (flat_gradient.mT @ flat_value).to(dtype=weight.dtype)
+            flat_value = value.to(dtype=torch.bfloat16).reshape(-1, value.shape[-1])
+            grad_weight = _weight_gradient(flat_gradient, flat_value).to(dtype=weight.dtype)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             dimensions = tuple(range(grad_output.ndim - 1))
             grad_bias = grad_output.sum(dim=dimensions, dtype=torch.float32).to(dtype=ctx.bias_dtype)

@@ -307,7 +307,7 @@ __global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) 
 
 // ---------------------------------------------------------------------------
 // Token map: one wave per (b, chunk, h), 16 tokens per step.
-template <int R, bool DK32>
+template <int R, bool DK32, bool VEC>
 __global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
     constexpr bool RK32 = (R % 32) == 0;
     using RR = RecordShape<RK32>;
@@ -378,22 +378,36 @@ __global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
         for (int s = 0; s < kBwdMaxHeadDim / RD::kWidth; ++s) {
             if (s < dsteps) {
                 const int first = RD::kWidth * s + RD::kPerLane * g;
+                if constexpr (VEC) {
+                    // d is a multiple of the per-lane run: whole runs or none.
+                    const bool run = live && first < d;
+                    y_op[s] = run ? *reinterpret_cast<const FeatOp*>(grow + (run ? first : 0))
+                                  : FeatOp{};
+                    c_op[s] = run ? *reinterpret_cast<const FeatOp*>(crow + (run ? first : 0))
+                                  : FeatOp{};
 #pragma unroll
-                for (int p = 0; p < RD::kPerLane / 2; ++p) {
-                    const int f = first + 2 * p;
-                    uint32_t yv = 0u, cv = 0u;
-                    if (live && f < d) {
-                        const uint32_t y_lo = grow[f];
-                        const uint32_t c_lo = crow[f];
-                        const uint32_t y_hi = f + 1 < d ? grow[f + 1] : 0u;
-                        const uint32_t c_hi = f + 1 < d ? crow[f + 1] : 0u;
-                        yv = y_lo | (y_hi << 16);
-                        cv = c_lo | (c_hi << 16);
+                    for (int p = 0; p < RD::kPerLane / 2; ++p) {
+                        dot = fmaf(bf16_lo(y_op[s][p]), bf16_lo(c_op[s][p]), dot);
+                        dot = fmaf(bf16_hi(y_op[s][p]), bf16_hi(c_op[s][p]), dot);
                     }
-                    y_op[s][p] = yv;
-                    c_op[s][p] = cv;
-                    dot = fmaf(bf16_lo(yv), bf16_lo(cv), dot);
-                    dot = fmaf(bf16_hi(yv), bf16_hi(cv), dot);
+                } else {
+#pragma unroll
+                    for (int p = 0; p < RD::kPerLane / 2; ++p) {
+                        const int f = first + 2 * p;
+                        uint32_t yv = 0u, cv = 0u;
+                        if (live && f < d) {
+                            const uint32_t y_lo = grow[f];
+                            const uint32_t c_lo = crow[f];
+                            const uint32_t y_hi = f + 1 < d ? grow[f + 1] : 0u;
+                            const uint32_t c_hi = f + 1 < d ? crow[f + 1] : 0u;
+                            yv = y_lo | (y_hi << 16);
+                            cv = c_lo | (c_hi << 16);
+                        }
+                        y_op[s][p] = yv;
+                        c_op[s][p] = cv;
+                        dot = fmaf(bf16_lo(yv), bf16_lo(cv), dot);
+                        dot = fmaf(bf16_hi(yv), bf16_hi(cv), dot);
+                    }
                 }
             }
         }
@@ -490,11 +504,19 @@ __global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
                 }
                 if (live) {
                     const int f0 = 16 * fb + 4 * g;
+                    if (VEC && f0 + 4 <= d) {
+                        const u32x2 dy = *reinterpret_cast<const u32x2*>(grow + f0);
+                        u32x2 packed;
+                        packed.x = pack_bf16(fmaf(eta, bf16_lo(dy.x), acc[0]), fmaf(eta, bf16_hi(dy.x), acc[1]));
+                        packed.y = pack_bf16(fmaf(eta, bf16_lo(dy.y), acc[2]), fmaf(eta, bf16_hi(dy.y), acc[3]));
+                        *reinterpret_cast<u32x2*>(out_row + a.heads * R + h * d + f0) = packed;
+                    } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if (f0 + i < d) {
-                            const float dy = bf16_bits_to_float(grow[f0 + i]);
-                            out_row[a.heads * R + h * d + f0 + i] = to_bf16_bits(fmaf(eta, dy, acc[i]));
+                        for (int i = 0; i < 4; ++i) {
+                            if (f0 + i < d) {
+                                const float dy = bf16_bits_to_float(grow[f0 + i]);
+                                out_row[a.heads * R + h * d + f0 + i] = to_bf16_bits(fmaf(eta, dy, acc[i]));
+                            }
                         }
                     }
                 }
@@ -522,19 +544,41 @@ __global__ __launch_bounds__(256) void param_reduce_kernel(ParamReduceArgs a) {
     const int64_t e = idx - h * per_head;
     const int64_t rr = a.rank * a.rank;
     const int64_t dr = a.head_dim * a.rank;
+    // Eight samples' loads are issued together, then summed in order.
+    const float* source;
+    int64_t stride;
+    if (e < rr) {
+        source = a.dtheta_part + h * rr + e;
+        stride = a.heads * rr;
+    } else if (e < rr + dr) {
+        source = a.ddrive_part + h * dr + (e - rr);
+        stride = a.heads * dr;
+    } else {
+        source = a.deta_part + h;
+        stride = a.heads;
+    }
     float acc = 0.0f;
-    for (int64_t b = 0; b < a.batch; ++b) {
-        const int64_t system = b * a.heads + h;
-        if (e < rr) {
-            acc += a.dtheta_part[system * rr + e];
-        } else if (e < rr + dr) {
-            acc += a.ddrive_part[system * dr + (e - rr)];
-        } else {
-            float value = a.deta_part[system];
-            for (int64_t ch = 0; ch < a.chunks; ++ch) {
-                value += a.dot_part[system * a.chunks + ch];
+    for (int64_t b0 = 0; b0 < a.batch; b0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t b = b0 + u < a.batch ? b0 + u : a.batch - 1;
+            v[u] = source[b * stride];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (b0 + u < a.batch) {
+                acc += v[u];
             }
-            acc += value;
+        }
+    }
+    if (e == rr + dr) {
+        // <dY, C> partials of every sample and chunk, in sample order.
+        for (int64_t b = 0; b < a.batch; ++b) {
+            const float* dots = a.dot_part + (b * a.heads + h) * a.chunks;
+            for (int64_t ch = 0; ch < a.chunks; ++ch) {
+                acc += dots[ch];
+            }
         }
     }
     if (e < rr) {
@@ -575,22 +619,30 @@ hipError_t launch_bwd_solve(int rank, const BwdSolveArgs& a, int64_t systems, hi
 }
 
 template <int R>
-static hipError_t launch_bwd_apply_r(const BwdApplyArgs& a, bool dk32, hipStream_t stream) {
+static hipError_t launch_bwd_apply_r(const BwdApplyArgs& a, bool dk32, bool vec, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((a.total_waves + 3) / 4));
     if (dk32) {
-        bwd_apply_kernel<R, true><<<grid, 256, 0, stream>>>(a);
+        if (vec) {
+            bwd_apply_kernel<R, true, true><<<grid, 256, 0, stream>>>(a);
+        } else {
+            bwd_apply_kernel<R, true, false><<<grid, 256, 0, stream>>>(a);
+        }
     } else {
-        bwd_apply_kernel<R, false><<<grid, 256, 0, stream>>>(a);
+        if (vec) {
+            bwd_apply_kernel<R, false, true><<<grid, 256, 0, stream>>>(a);
+        } else {
+            bwd_apply_kernel<R, false, false><<<grid, 256, 0, stream>>>(a);
+        }
     }
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, hipStream_t stream) {
+hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, bool vec, hipStream_t stream) {
     switch (rank) {
-        case 16: return launch_bwd_apply_r<16>(a, dk32, stream);
-        case 32: return launch_bwd_apply_r<32>(a, dk32, stream);
-        case 48: return launch_bwd_apply_r<48>(a, dk32, stream);
-        default: return launch_bwd_apply_r<64>(a, dk32, stream);
+        case 16: return launch_bwd_apply_r<16>(a, dk32, vec, stream);
+        case 32: return launch_bwd_apply_r<32>(a, dk32, vec, stream);
+        case 48: return launch_bwd_apply_r<48>(a, dk32, vec, stream);
+        default: return launch_bwd_apply_r<64>(a, dk32, vec, stream);
     }
 }
 

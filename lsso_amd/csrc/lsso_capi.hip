@@ -632,7 +632,11 @@ int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape, const void* grad_
     apply.chunks = plan.apply_chunks;
     apply.chunk_tokens = plan.apply_chunk_tokens;
     apply.total_waves = plan.batch * plan.heads * plan.apply_chunks;
-    error = lsso_hip::launch_bwd_apply(static_cast<int>(plan.rank), apply, bp.feature_k32 != 0, stream);
+    // Whole 16-byte (K32) or 8-byte (K16) feature runs per lane.
+    const bool bwd_vec = plan.head_dim % 8 == 0 && plan.width % 8 == 0 && aligned(projected, 16) &&
+                         aligned(grad_output, 16) && aligned(grad_projected, 16);
+    error = lsso_hip::launch_bwd_apply(static_cast<int>(plan.rank), apply, bp.feature_k32 != 0,
+                                       bwd_vec, stream);
     if (error != hipSuccess) {
         return hip_failure(error, "bwd_apply_kernel launch");
     }

@@ -196,7 +196,7 @@ bool backward_supported(int64_t rank, int64_t head_dim);
 int64_t bwd_record_layout(int64_t rank, int64_t head_dim, int64_t* off_m, int64_t* off_e,
                           int64_t* off_g, int64_t* off_f, int* feature_k32);
 hipError_t launch_bwd_solve(int rank, const BwdSolveArgs& a, int64_t systems, hipStream_t stream);
-hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, hipStream_t stream);
+hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, bool vec, hipStream_t stream);
 hipError_t launch_param_reduce(const ParamReduceArgs& a, hipStream_t stream);
 
 hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,
