@@ -189,8 +189,8 @@ int lsso_hip_linear_workspace_bytes(int64_t rows, int64_t in_features,
  * x: [rows, in_features] with row stride x_row_stride elements (unit column
  * stride), dtype x_dtype.  weight: float32 [out_features, in_features]
  * contiguous.  bias: float32 [out_features] or NULL.  row_mask: optional
- * device uint8 [rows]; rows whose byte is 0 are not read and are written as
- * zeros (the masked-token contract of the reference's native forward,
+ * device uint8 [rows]; rows whose byte is 0 are written as zeros whatever
+ * their x holds, NaN included (the masked-token contract of the reference's native forward,
  * lsso/ball/model.py:371-383, 402-404).  y: contiguous [rows, out_features]
  * of dtype y_dtype.
  * Replaces: tensor_core_linear / _biased_gemm (lsso/ball/reference.py:20-75,
