@@ -7,8 +7,9 @@ mask.  One step is one forward x -> y including both
 projections (reference protocol: benchmarks/benchmark_ball.py:156-208).
 
 Prints one JSON line with the driver's fields plus
-  roofline      the dominant kernel (the input projection) from HIP events
-                recorded around its launches inside the timed region;
+  roofline      the dominant kernel (the longer of the two fused streaming
+                kernels) from HIP events that the library records around each
+                stage of every timed step;
   cpu_baseline  the CPU oracle (FP32 restatement of the reference CPU path)
                 timed on this host on a bounded sample of the same workload.
 """
@@ -202,6 +203,7 @@ def main() -> int:
     layer = layer.to(device).eval()
     x_cpu = torch.randn(batch, length, dim, generator=torch.Generator().manual_seed(1)).half()
     x = x_cpu.to(device)
+    tokens = batch * length
 
     w_bc, b_bc = layer.w_bc.weight, layer.w_bc.bias
     w_o, b_o = layer.w_o.weight, layer.w_o.bias
@@ -209,32 +211,41 @@ def main() -> int:
 
     # The step is exactly the module's native inference forward for an
     # unmasked input with default positions (lsso_amd/ball/model.py,
-    # _forward_native): input projection, then the mixer fused with the output
-    # projection; unrolled so that events bracket the input projection.
-    events = []
+    # _forward_native): one lsso_hip_layer_forward call (input projection
+    # fused with the token reductions, compact solve, apply fused with the
+    # output projection).  On timed steps the library records HIP events
+    # around each stage on the launch stream.
+    stage_names = ("phase_table", "project_reduce", "solve", "mix_project")
+    # Events are created (torch creates a HIP event on its first record)
+    # before the timed region, 8 per timed step.
+    stage_events = [[torch.cuda.Event(enable_timing=True) for _ in range(8)] for _ in range(args.steps)]
+    for events in stage_events:
+        for event in events:
+            event.record()
+    torch.cuda.synchronize()
 
-    def step(record: bool) -> torch.Tensor:
-        if record:
-            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-        projected = hip.linear(x, w_bc, b_bc, torch.bfloat16)
-        if record:
-            stop.record()
-            events.append((start, stop))
-        return hip.mix_project(projected, base, drive, eta_raw, None, None, w_o, b_o, x.dtype)
+    def step(events) -> torch.Tensor:
+        return hip.layer_forward(x, w_bc, b_bc, base, drive, eta_raw, None, None, w_o, b_o,
+                                 stage_events=events)
 
     with torch.inference_mode():
         reference_out = layer(x, implementation="hip")
-        check = step(False)
-        if not torch.equal(check, reference_out):
-            print("unrolled step differs from LSSO.forward(implementation='hip')", file=sys.stderr)
+        check = step(None)
+        projected = hip.linear(x, w_bc, b_bc, torch.bfloat16)
+        mixed = hip.forward_inference(projected, base, drive, eta_raw)
+        three_calls = hip.linear(mixed, w_o, b_o, x.dtype)
+        del projected, mixed
+        if not (torch.equal(check, reference_out) and torch.equal(check, three_calls)):
+            print("the layer step differs from LSSO.forward(implementation='hip') or from "
+                  "linear -> forward_inference -> linear", file=sys.stderr)
             return 1
+        del three_calls
         for _ in range(args.warmup):
-            step(False)
+            step(None)
         torch.cuda.synchronize()
         start = time.perf_counter()
-        for _ in range(args.steps):
-            step(True)
+        for index in range(args.steps):
+            step(stage_events[index])
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
 
@@ -247,19 +258,31 @@ def main() -> int:
         del source, target
 
     ms_per_step = 1e3 * elapsed / args.steps
-    tokens = batch * length
     value = tokens * args.steps / elapsed
-    projection_ms = statistics.mean(s.elapsed_time(e) for s, e in events)
+    stage_ms = {
+        name: statistics.mean(ev[2 * k].elapsed_time(ev[2 * k + 1]) for ev in stage_events)
+        for k, name in enumerate(stage_names)
+    }
     width = heads * rank + dim
-    # Algorithmic bytes of the input projection per launch: x read (FP16) +
-    # packed write (BF16) + weights (FP32) + bias.
-    projection_bytes = tokens * (dim * 2 + width * 2) + width * dim * 4 + width * 4
-    achieved = projection_bytes / (projection_ms * 1e-3) / 1e9
+    k_tier = next(t for t in (8, 12, 16, 24) if dim <= 16 * t)
+    # Algorithmic bytes per launch, counting the ABI tensors once (the FP32
+    # partials and apply records in the workspace are left out):
+    #   project_reduce: x read (FP16) + packed write (BF16) + W_in, b_in (FP32)
+    #   mix_project:    packed read (BF16) + y write (FP16) + W_o, b_o (FP32)
+    stage_kernels = {
+        "project_reduce": (f"lsso_hip::project_reduce_kernel<{k_tier}, {rank}, 1, 1>",
+                           tokens * (dim * 2 + width * 2) + width * dim * 4 + width * 4,
+                           "fused input projection + token reductions (x -> packed, G, S)"),
+        "mix_project": (f"lsso_hip::mix_project_kernel<{rank}, 2, 1, 2>",
+                        tokens * (width * 2 + dim * 2) + dim * dim * 4 + dim * 4,
+                        "fused apply + output projection (packed -> y)"),
+    }
+    dominant = max(stage_kernels, key=lambda name: stage_ms[name])
+    kernel_name, kernel_bytes, kernel_role = stage_kernels[dominant]
+    achieved = kernel_bytes / (stage_ms[dominant] * 1e-3) / 1e9
     chain_bytes = tokens * 5120
-    k_tier = next(t for t in (4, 8, 12, 16, 24, 32) if dim <= 16 * t)
-    projection_kernel = f"lsso_hip::linear_kernel<{k_tier}, 1, 2, true>"
     headline = (batch, length) == (64, 4096)
-    traffic = measured_traffic(projection_kernel) if headline else None
+    traffic = measured_traffic(kernel_name) if headline else None
     result = {
         "metric": "mixer fwd tokens/s @B64 D256 H8 r32 L4096 fp16; % HBM roofline",
         "value": value,
@@ -288,7 +311,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": projection_kernel + " (input projection x -> packed)",
+            "kernel": f"{kernel_name} ({kernel_role})",
             "achieved": achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
@@ -296,7 +319,8 @@ def main() -> int:
             "traffic": traffic,
             "traffic_source": ("profiles/mixer_forward_c3_l4096_hbm_traffic.md (rocprofv3 FETCH_SIZE + "
                                "WRITE_SIZE, copy-calibrated)") if traffic is not None else None,
-            "avg_ms": projection_ms,
+            "avg_ms": stage_ms[dominant],
+            "stage_ms": stage_ms,
         },
     }
     if args.cpu_samples > 0:

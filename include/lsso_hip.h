@@ -180,6 +180,88 @@ int lsso_hip_mixer_forward_projected(const lsso_hip_mixer_shape* shape,
                                      size_t workspace_bytes,
                                      void* stream);
 
+/* 1 if lsso_hip_layer_forward handles this shape, 0 if not (use
+ * lsso_hip_linear and lsso_hip_mixer_forward), or a negative code for an
+ * invalid shape.  The fused layer covers head_dim a multiple of 16 up to 64
+ * and a model width H*head_dim up to 384.
+ * Replaces: the choice of the native path in LSSO._forward_cuda
+ * (lsso/ball/model.py:270-405). */
+int lsso_hip_layer_supported(const lsso_hip_mixer_shape* shape);
+
+/* Device scratch bytes needed by lsso_hip_layer_forward (the mixer workspace
+ * plus the packed projection, and the mixed block when the output projection
+ * cannot be fused). */
+int lsso_hip_layer_workspace_bytes(const lsso_hip_mixer_shape* shape, int positions_mode,
+                                   size_t* bytes);
+
+/* The whole LSSO layer forward (inference), x [batch, length, H*d] -> y:
+ *   packed = bf16(x in_weight^T + in_bias)   (row_mask rows -> 0)
+ *   mixed  = the mixer of lsso_hip_mixer_forward on packed
+ *   y      = cast(bf16(mixed) out_weight^T + out_bias)  (row_mask rows -> 0)
+ * The input projection runs fused with the mixer's token reductions (one pass
+ * over x per head group) and the output projection fused with the apply when
+ * lsso_hip_mixer_projected_supported() allows, so packed is read back once
+ * and mixed never reaches HBM.  The result is bitwise that of lsso_hip_linear,
+ * lsso_hip_mixer_forward and lsso_hip_linear in sequence.  in_weight: float32
+ * [H*(rank+d), H*d]; in_bias: float32 [H*(rank+d)] or NULL; out_weight:
+ * float32 [H*d, H*d]; out_bias: float32 [H*d] or NULL; row_mask: uint8
+ * [batch*length] or NULL; x and y 16-byte aligned, of dtypes x_dtype and
+ * y_dtype (LSSO_HIP_F16 or LSSO_HIP_BF16).  Positions, counts and
+ * inverse_frequency as in lsso_hip_mixer_forward.
+ * Replaces: tensor_core_linear -> fast_mix -> tensor_core_linear in
+ * LSSO._forward_cuda (lsso/ball/model.py:270-405; lsso/ball/reference.py:347-408,
+ * lsso/ball/cuda.py:283-323). */
+int lsso_hip_layer_forward(const lsso_hip_mixer_shape* shape,
+                           const void* x,
+                           int x_dtype,
+                           const float* in_weight,
+                           const float* in_bias,
+                           const uint8_t* row_mask,
+                           const float* core_base_raw,
+                           const float* core_drive_weight,
+                           const float* eta_raw,
+                           const float* inverse_frequency,
+                           const float* centered_positions,
+                           int positions_mode,
+                           const float* valid_counts,
+                           const float* out_weight,
+                           const float* out_bias,
+                           void* y,
+                           int y_dtype,
+                           void* workspace,
+                           size_t workspace_bytes,
+                           void* stream);
+
+/* lsso_hip_layer_forward with timing marks for profiling callers: events
+ * points to 8 hipEvent_t handles (entries may be NULL); events[2k] and
+ * events[2k+1] are recorded on the stream around stage k: 0 the phase table,
+ * 1 the fused input projection + reductions, 2 the compact solve, 3 the apply
+ * + output projection.  Results are those of lsso_hip_layer_forward.
+ * Replaces: the CUDA events around the timed region of the reference's
+ * benchmark (benchmarks/benchmark_ball.py:189-206), moved inside the call so
+ * that each stage is timed on its own. */
+int lsso_hip_layer_forward_timed(const lsso_hip_mixer_shape* shape,
+                                 const void* x,
+                                 int x_dtype,
+                                 const float* in_weight,
+                                 const float* in_bias,
+                                 const uint8_t* row_mask,
+                                 const float* core_base_raw,
+                                 const float* core_drive_weight,
+                                 const float* eta_raw,
+                                 const float* inverse_frequency,
+                                 const float* centered_positions,
+                                 int positions_mode,
+                                 const float* valid_counts,
+                                 const float* out_weight,
+                                 const float* out_bias,
+                                 void* y,
+                                 int y_dtype,
+                                 void* workspace,
+                                 size_t workspace_bytes,
+                                 void* stream,
+                                 void* const* events);
+
 /* Device scratch bytes needed by lsso_hip_linear. */
 int lsso_hip_linear_workspace_bytes(int64_t rows, int64_t in_features,
                                     int64_t out_features, size_t* bytes);

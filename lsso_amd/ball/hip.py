@@ -48,6 +48,10 @@ _SYMBOLS = (
     "lsso_hip_mixer_backward",
     "lsso_hip_linear_workspace_bytes",
     "lsso_hip_linear",
+    "lsso_hip_layer_supported",
+    "lsso_hip_layer_workspace_bytes",
+    "lsso_hip_layer_forward",
+    "lsso_hip_layer_forward_timed",
 )
 
 
@@ -106,6 +110,20 @@ def _declare(library: ctypes.CDLL) -> None:
     library.lsso_hip_linear.argtypes = [
         vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, i64, vp, ctypes.c_int, vp, ctypes.c_size_t, vp,
     ]  # x, x_dtype, rows, in, stride, weight, bias, row_mask, out, y, y_dtype, ws, ws_bytes, stream
+    library.lsso_hip_layer_supported.restype = ctypes.c_int
+    library.lsso_hip_layer_supported.argtypes = [shape_p]
+    library.lsso_hip_layer_workspace_bytes.restype = ctypes.c_int
+    library.lsso_hip_layer_workspace_bytes.argtypes = [shape_p, ctypes.c_int, size_p]
+    library.lsso_hip_layer_forward.restype = ctypes.c_int
+    library.lsso_hip_layer_forward.argtypes = [
+        shape_p, vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp,
+        ctypes.c_int, vp, ctypes.c_size_t, vp,
+    ]  # shape, x, x_dtype, in_weight, in_bias, row_mask, base, drive, eta, inv_freq, positions,
+    #    mode, counts, out_weight, out_bias, y, y_dtype, workspace, workspace_bytes, stream
+    library.lsso_hip_layer_forward_timed.restype = ctypes.c_int
+    library.lsso_hip_layer_forward_timed.argtypes = [
+        *library.lsso_hip_layer_forward.argtypes, ctypes.POINTER(ctypes.c_void_p),
+    ]  # ... as lsso_hip_layer_forward, then hipEvent_t events[8]
 
 
 def default_library_path() -> Path:
@@ -278,7 +296,27 @@ def _validate_mixer(
             "projected must use bfloat16 under the mixed precision HIP contract, "
             f"got {projected.dtype}"
         )
-    device = projected.device
+    batch, length, width = projected.shape
+    return _validate_core(
+        projected.device, batch, length, width, core_base_raw, core_drive_weight, eta_raw,
+        centered_positions, valid_counts,
+    )
+
+
+def _validate_core(
+    device: torch.device,
+    batch: int,
+    length: int,
+    width: int,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None,
+    valid_counts: torch.Tensor | None,
+) -> tuple[MixerShape, int]:
+    """Checks of the compact parameters, positions and counts for a packed
+    width of ``width`` columns (csrc/ball/common.cuh:194-269)."""
+
     for name, value in (
         ("core_base_raw", core_base_raw),
         ("core_drive_weight", core_drive_weight),
@@ -291,7 +329,6 @@ def _validate_mixer(
             raise RuntimeError(f"{name} must use float32")
     if core_base_raw.dim() != 3 or core_base_raw.shape[1] != core_base_raw.shape[2]:
         raise RuntimeError(f"core_base_raw must have shape [H, R, R], got {tuple(core_base_raw.shape)}")
-    batch, length, width = projected.shape
     heads, rank = core_base_raw.shape[0], core_base_raw.shape[1]
     if batch <= 0 or length <= 0 or heads <= 0:
         raise RuntimeError("B, N, and H must be positive")
@@ -661,6 +698,159 @@ def mix_project(
     return output
 
 
+def _layer_shape(
+    x: torch.Tensor,
+    in_weight: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None,
+    valid_counts: torch.Tensor | None,
+) -> tuple[MixerShape, int]:
+    if x.device.type != "cuda":
+        raise RuntimeError("x must be a CUDA (ROCm device) tensor")
+    if x.dim() != 3 or not x.is_contiguous():
+        raise RuntimeError(f"x must be a contiguous [B, N, D] tensor, got {tuple(x.shape)}")
+    batch, length, dim = x.shape
+    if core_base_raw.dim() != 3:
+        raise RuntimeError(f"core_base_raw must have shape [H, R, R], got {tuple(core_base_raw.shape)}")
+    width = core_base_raw.shape[0] * core_base_raw.shape[1] + dim
+    if in_weight.dtype != torch.float32 or tuple(in_weight.shape) != (width, dim):
+        raise TypeError(f"in_weight must be float32 [{width}, {dim}]")
+    return _validate_core(
+        x.device, batch, length, width, core_base_raw, core_drive_weight, eta_raw,
+        centered_positions, valid_counts,
+    )
+
+
+def layer_supported(
+    x: torch.Tensor,
+    in_weight: torch.Tensor,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+) -> bool:
+    """Whether the fused whole-layer forward covers this geometry."""
+
+    library = _library()
+    shape, _mode = _layer_shape(x, in_weight, core_base_raw, core_drive_weight, eta_raw, None, None)
+    status = library.lsso_hip_layer_supported(ctypes.byref(shape))
+    if status < 0:
+        _check(status, library)
+    return status == 1 and x.dtype in (torch.float16, torch.bfloat16)
+
+
+def layer_forward(
+    x: torch.Tensor,
+    in_weight: torch.Tensor,
+    in_bias: torch.Tensor | None,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None,
+    valid_counts: torch.Tensor | None,
+    out_weight: torch.Tensor,
+    out_bias: torch.Tensor | None,
+    row_mask: torch.Tensor | None = None,
+    stage_events: list | None = None,
+) -> torch.Tensor:
+    """Inference-only native LSSO layer, x -> y, in one call.
+
+    Bitwise ``linear(mix(linear(x, in_weight, in_bias, bf16, row_mask)),
+    out_weight, out_bias, x.dtype, row_mask)``: the input projection runs fused
+    with the token reductions and the output projection with the apply (the
+    orchestration of reference model.py:270-405).
+
+    ``stage_events``: optional 8 recorded ``torch.cuda.Event`` objects (or
+    None); events 2k and 2k + 1 are recorded around stage k (phase table,
+    projection + reductions, compact solve, apply + output projection), for
+    per-kernel timing on the launch stream.
+    """
+
+    if torch.is_grad_enabled() and _any_requires_grad(
+        x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw, centered_positions,
+        valid_counts, out_weight, out_bias,
+    ):
+        raise RuntimeError(
+            "lsso_hip layer_forward is an inference-only entry point and cannot participate in "
+            "autograd; use linear(), fast_mix() and linear()"
+        )
+    library = _library()
+    shape, mode = _layer_shape(
+        x, in_weight, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+    )
+    device = x.device
+    dim = x.shape[-1]
+    width = in_weight.shape[0]
+    dtype_codes = {torch.float16: _F16, torch.bfloat16: _BF16}
+    if x.dtype not in dtype_codes:
+        raise TypeError("the fused layer supports float16/bfloat16 x")
+    if in_bias is not None and (in_bias.dtype != torch.float32 or tuple(in_bias.shape) != (width,)):
+        raise TypeError(f"in_bias must be float32 [{width}]")
+    if out_weight.dtype != torch.float32 or tuple(out_weight.shape) != (dim, dim):
+        raise TypeError(f"out_weight must be float32 [{dim}, {dim}]")
+    if out_bias is not None and (out_bias.dtype != torch.float32 or tuple(out_bias.shape) != (dim,)):
+        raise TypeError(f"out_bias must be float32 [{dim}]")
+    for name, value in (
+        ("in_weight", in_weight), ("in_bias", in_bias), ("out_weight", out_weight), ("out_bias", out_bias),
+    ):
+        if value is not None:
+            _require_device_tensor(value, name, device)
+    in_weight = in_weight.contiguous()
+    in_bias = None if in_bias is None else in_bias.contiguous()
+    out_weight = out_weight.contiguous()
+    out_bias = None if out_bias is None else out_bias.contiguous()
+    mask_ptr = None
+    if row_mask is not None:
+        if row_mask.dtype != torch.bool or tuple(row_mask.shape) != (shape.batch, shape.length):
+            raise ValueError("row_mask must be a bool [B, N] tensor")
+        row_mask = row_mask.contiguous()
+        mask_ptr = row_mask.data_ptr()
+    workspace_bytes = ctypes.c_size_t()
+    _check(library.lsso_hip_layer_workspace_bytes(ctypes.byref(shape), mode, ctypes.byref(workspace_bytes)), library)
+    workspace = torch.empty(workspace_bytes.value, dtype=torch.uint8, device=device)
+    output = torch.empty((shape.batch, shape.length, dim), dtype=x.dtype, device=device)
+    arguments = []
+    entry = library.lsso_hip_layer_forward
+    if stage_events is not None:
+        if len(stage_events) != 8:
+            raise ValueError("stage_events must hold 8 events (or None entries)")
+        handles = []
+        for event in stage_events:
+            handle = 0 if event is None else int(event.cuda_event)
+            if event is not None and handle == 0:
+                raise ValueError("stage events must have been recorded once (torch creates them lazily)")
+            handles.append(handle)
+        arguments = [(ctypes.c_void_p * 8)(*[h or None for h in handles])]
+        entry = library.lsso_hip_layer_forward_timed
+    with torch.cuda.device(device):
+        status = entry(
+            ctypes.byref(shape),
+            x.data_ptr(),
+            dtype_codes[x.dtype],
+            in_weight.data_ptr(),
+            None if in_bias is None else in_bias.data_ptr(),
+            mask_ptr,
+            core_base_raw.data_ptr(),
+            core_drive_weight.data_ptr(),
+            eta_raw.data_ptr(),
+            ctypes.cast(_inverse_frequency(shape.rank), ctypes.c_void_p),
+            None if centered_positions is None else centered_positions.data_ptr(),
+            mode,
+            None if valid_counts is None else valid_counts.data_ptr(),
+            out_weight.data_ptr(),
+            None if out_bias is None else out_bias.data_ptr(),
+            output.data_ptr(),
+            dtype_codes[x.dtype],
+            workspace.data_ptr(),
+            workspace_bytes.value,
+            _stream(device),
+            *arguments,
+        )
+    _check(status, library)
+    return output
+
+
 def _linear_forward(
     value: torch.Tensor,
     weight: torch.Tensor,
@@ -822,6 +1012,8 @@ __all__ = [
     "forward_inference",
     "forward_train",
     "is_available",
+    "layer_forward",
+    "layer_supported",
     "linear",
     "load",
     "mix_project",

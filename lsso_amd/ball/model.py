@@ -278,11 +278,33 @@ class LSSO(nn.Module):
 
         from . import hip
 
-        projected, centered_positions, valid_counts, mask = self._native_inputs(
-            x, valid_mask, position_ids
-        )
         needs_grad = torch.is_grad_enabled() and any(
             parameter.requires_grad for parameter in (x, *self.parameters())
+        )
+        if not needs_grad and x.is_contiguous() and hip.layer_supported(
+            x, self.w_bc.weight, self.core_base_raw, self.core_drive_weight, self.eta_raw
+        ):
+            # Inference: the whole layer in one native call (input projection
+            # fused with the reductions, apply with the output projection),
+            # bitwise equal to the three-step path below.
+            centered_positions, valid_counts, mask = self._native_geometry(
+                x, valid_mask, position_ids
+            )
+            return hip.layer_forward(
+                x,
+                self.w_bc.weight,
+                self.w_bc.bias,
+                self.core_base_raw,
+                self.core_drive_weight,
+                self.eta_raw,
+                centered_positions,
+                valid_counts,
+                self.w_o.weight,
+                self.w_o.bias,
+                row_mask=mask,
+            )
+        projected, centered_positions, valid_counts, mask = self._native_inputs(
+            x, valid_mask, position_ids
         )
         if not needs_grad and hip.mix_project_supported(
             projected, self.core_base_raw, self.core_drive_weight, self.eta_raw
@@ -322,6 +344,21 @@ class LSSO(nn.Module):
 
         from . import hip
 
+        centered_positions, valid_counts, mask = self._native_geometry(x, valid_mask, position_ids)
+        # Masked rows are neither read nor biased: the projection writes zeros
+        # there (reference model.py:371-383, 402-404).
+        projected = hip.linear(x, self.w_bc.weight, self.w_bc.bias, torch.bfloat16, row_mask=mask)
+        return projected, centered_positions, valid_counts, mask
+
+    def _native_geometry(
+        self,
+        x: torch.Tensor,
+        valid_mask: torch.Tensor | None,
+        position_ids: torch.Tensor | None,
+    ):
+        """The mixer's centred positions, valid counts and row mask
+        (reference model.py:270-370)."""
+
         batch, length, _dim = x.shape
         all_valid = valid_mask is None
         mask = (
@@ -349,10 +386,7 @@ class LSSO(nn.Module):
             if all_valid
             else mask.sum(dim=-1).to(dtype=torch.float32).clamp_min(1.0).contiguous()
         )
-        # Masked rows are neither read nor biased: the projection writes zeros
-        # there (reference model.py:371-383, 402-404).
-        projected = hip.linear(x, self.w_bc.weight, self.w_bc.bias, torch.bfloat16, row_mask=mask)
-        return projected, centered_positions, valid_counts, mask
+        return centered_positions, valid_counts, mask
 
     @torch.no_grad()
     def diagnostics(

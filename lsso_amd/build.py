@@ -22,7 +22,14 @@ OUTPUT_DIR = PACKAGE_ROOT / "_lib"
 OBJECT_DIR = REPOSITORY_ROOT / "_build"
 OFFLOAD_ARCH = "gfx950"
 LIBRARY_NAME = f"liblsso_hip_{OFFLOAD_ARCH}.so"
-SOURCES = ("lsso_capi.hip", "lsso_mixer.hip", "lsso_linear.hip", "lsso_fused.hip", "lsso_backward.hip")
+SOURCES = (
+    "lsso_capi.hip",
+    "lsso_mixer.hip",
+    "lsso_linear.hip",
+    "lsso_fused.hip",
+    "lsso_backward.hip",
+    "lsso_project_reduce.hip",
+)
 
 # Packed FP32 VALU forms (v_pk_add/mul/fma_f32) are disabled for all device
 # code: some of their forms have returned wrong results on the MI355X boxes

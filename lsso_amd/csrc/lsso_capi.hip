@@ -86,8 +86,10 @@ int make_plan(const lsso_hip_mixer_shape* shape, int positions_mode, MixerPlan* 
 
     p->cpw = p->head_dim > 32 ? 2 : 1;
     p->column_groups = ceil_div(p->head_dim, 32 * p->cpw);
-    plan_chunks(p->length, p->batch * p->heads * p->column_groups, kReduceTargetWaves, 32,
-                &p->reduce_chunks, &p->reduce_chunk_tokens);
+    // Chunks are whole 64-token tiles, so the fused projection + reduce and
+    // the standalone reduce share one chunking (and their partials agree).
+    plan_chunks(p->length, p->batch * p->heads * p->column_groups, kReduceTargetWaves,
+                lsso_hip::project_reduce_tile_rows(), &p->reduce_chunks, &p->reduce_chunk_tokens);
 
     p->feature_blocks = ceil_div(p->head_dim, 16);
     p->nfbw = p->feature_blocks >= 4 ? 4 : (p->feature_blocks == 3 ? 4 : static_cast<int>(p->feature_blocks));
@@ -207,13 +209,8 @@ bool vector_rows(const MixerPlan& plan, const void* projected, const void* outpu
            aligned(output, 16);
 }
 
-// Phase table, L-reductions and the compact solve: everything up to the
-// apply operand records.
-int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
-                const float* core_base_raw, const float* core_drive_weight, const float* eta_raw,
-                const float* inverse_frequency, const float* centered_positions,
-                int positions_mode, const float* valid_counts, float* tape, bool vec,
-                hipStream_t stream) {
+int run_phase(const MixerPlan& plan, const MixerBuffers& buf, const float* inverse_frequency,
+              const float* centered_positions, int positions_mode, hipStream_t stream) {
     lsso_hip::PhaseArgs phase{};
     phase.positions = positions_mode == LSSO_HIP_POSITIONS_DEFAULT ? nullptr : centered_positions;
     phase.phases = buf.phases;
@@ -225,11 +222,45 @@ int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* proj
             ? inverse_frequency[j]
             : std::pow(10000.0f, -static_cast<float>(j) / static_cast<float>(plan.pairs));
     }
-    hipError_t error = lsso_hip::launch_phase(phase, stream);
-    if (error != hipSuccess) {
-        return hip_failure(error, "phase_kernel launch");
-    }
+    const hipError_t error = lsso_hip::launch_phase(phase, stream);
+    return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "phase_kernel launch");
+}
 
+int run_solve(const MixerPlan& plan, const MixerBuffers& buf, const float* core_base_raw,
+              const float* core_drive_weight, const float* eta_raw, const float* valid_counts,
+              float* tape, hipStream_t stream) {
+    lsso_hip::SolveArgs solve{};
+    solve.partials = buf.partials;
+    solve.chunks = plan.reduce_chunks;
+    solve.partial_stride = plan.partial_stride;
+    solve.batch = plan.batch;
+    solve.length = plan.length;
+    solve.heads = plan.heads;
+    solve.head_dim = plan.head_dim;
+    solve.base = core_base_raw;
+    solve.drive = core_drive_weight;
+    solve.eta_raw = eta_raw;
+    solve.valid_counts = valid_counts;
+    solve.zbuf = buf.zbuf;
+    solve.mop = buf.mop;
+    solve.tape = tape;
+    solve.tape_stride = plan.tape_stride;
+    const hipError_t error = lsso_hip::launch_solve(static_cast<int>(plan.rank), solve,
+                                                    plan.batch * plan.heads, stream);
+    return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "solve_kernel launch");
+}
+
+// Phase table, L-reductions and the compact solve: everything up to the
+// apply operand records.
+int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
+                const float* core_base_raw, const float* core_drive_weight, const float* eta_raw,
+                const float* inverse_frequency, const float* centered_positions,
+                int positions_mode, const float* valid_counts, float* tape, bool vec,
+                hipStream_t stream) {
+    int status = run_phase(plan, buf, inverse_frequency, centered_positions, positions_mode, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
     lsso_hip::ReduceArgs reduce{};
     reduce.projected = static_cast<const uint16_t*>(projected);
     reduce.content = static_cast<const uint16_t*>(projected) + plan.heads * plan.rank;
@@ -248,33 +279,128 @@ int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* proj
     reduce.column_groups = plan.column_groups;
     reduce.partial_stride = plan.partial_stride;
     reduce.total_waves = plan.batch * plan.heads * plan.reduce_chunks * plan.column_groups;
-    error = lsso_hip::launch_reduce(static_cast<int>(plan.rank), reduce, plan.cpw, vec, stream);
+    const hipError_t error =
+        lsso_hip::launch_reduce(static_cast<int>(plan.rank), reduce, plan.cpw, vec, stream);
     if (error != hipSuccess) {
         return hip_failure(error, "reduce_kernel launch");
     }
+    return run_solve(plan, buf, core_base_raw, core_drive_weight, eta_raw, valid_counts, tape,
+                     stream);
+}
 
-    lsso_hip::SolveArgs solve{};
-    solve.partials = buf.partials;
-    solve.chunks = plan.reduce_chunks;
-    solve.partial_stride = plan.partial_stride;
-    solve.batch = plan.batch;
-    solve.length = plan.length;
-    solve.heads = plan.heads;
-    solve.head_dim = plan.head_dim;
-    solve.base = core_base_raw;
-    solve.drive = core_drive_weight;
-    solve.eta_raw = eta_raw;
-    solve.valid_counts = valid_counts;
-    solve.zbuf = buf.zbuf;
-    solve.mop = buf.mop;
-    solve.tape = tape;
-    solve.tape_stride = plan.tape_stride;
-    error = lsso_hip::launch_solve(static_cast<int>(plan.rank), solve, plan.batch * plan.heads,
-                                   stream);
+int run_apply(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
+              const float* eta_raw, int positions_mode, void* output, bool vec,
+              hipStream_t stream) {
+    lsso_hip::ApplyArgs apply{};
+    apply.projected = static_cast<const uint16_t*>(projected);
+    apply.phases = buf.phases;
+    apply.mop = buf.mop;
+    apply.eta_raw = eta_raw;
+    apply.output = static_cast<uint16_t*>(output);
+    apply.batch = plan.batch;
+    apply.length = plan.length;
+    apply.heads = plan.heads;
+    apply.head_dim = plan.head_dim;
+    apply.width = plan.width;
+    apply.out_width = plan.out_width;
+    apply.phase_batch_stride = phase_batch_stride(plan, positions_mode);
+    apply.chunks = plan.apply_chunks;
+    apply.chunk_tokens = plan.apply_chunk_tokens;
+    apply.feature_blocks = plan.feature_blocks;
+    apply.block_groups = plan.block_groups;
+    apply.total_waves = plan.batch * plan.heads * plan.apply_chunks * plan.block_groups;
+    const hipError_t error =
+        lsso_hip::launch_apply(static_cast<int>(plan.rank), apply, plan.nfbw, vec, stream);
+    return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "apply_kernel launch");
+}
+
+int compute_units(int* units) {
+    int device = 0;
+    hipError_t error = hipGetDevice(&device);
     if (error != hipSuccess) {
-        return hip_failure(error, "solve_kernel launch");
+        return hip_failure(error, "hipGetDevice");
+    }
+    error = hipDeviceGetAttribute(units, hipDeviceAttributeMultiprocessorCount, device);
+    if (error != hipSuccess) {
+        return hip_failure(error, "hipDeviceGetAttribute");
     }
     return LSSO_HIP_OK;
+}
+
+// Fused apply + output projection into y (shape inside mix_project_supported).
+int run_mix_project(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
+                    const float* eta_raw, int positions_mode, const float* out_weight,
+                    const float* out_bias, const uint8_t* row_mask, void* y, int y_dtype,
+                    hipStream_t stream) {
+    int units = 0;
+    const int status = compute_units(&units);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    // One persistent workgroup per compute unit, each on a contiguous token
+    // range of one sample (ranges are whole tiles).
+    const int64_t tile = lsso_hip::mix_project_tile_rows();
+    int64_t ranges = ceil_div(units, plan.batch);
+    const int64_t max_ranges = ceil_div(plan.length, tile);
+    if (ranges > max_ranges) ranges = max_ranges;
+    const int64_t range_tokens = ceil_div(ceil_div(plan.length, ranges), tile) * tile;
+    ranges = ceil_div(plan.length, range_tokens);
+
+    lsso_hip::MixProjectArgs mix{};
+    mix.projected = static_cast<const uint16_t*>(projected);
+    mix.phases = buf.phases;
+    mix.mop = buf.mop;
+    mix.eta_raw = eta_raw;
+    mix.weight = out_weight;
+    mix.bias = out_bias;
+    mix.row_mask = row_mask;
+    mix.y = y;
+    mix.batch = plan.batch;
+    mix.length = plan.length;
+    mix.heads = plan.heads;
+    mix.head_dim = plan.head_dim;
+    mix.width = plan.width;
+    mix.out_features = plan.out_width;
+    mix.feature_blocks = plan.feature_blocks;
+    mix.phase_batch_stride = phase_batch_stride(plan, positions_mode);
+    mix.ranges = ranges;
+    mix.range_tokens = range_tokens;
+    const hipError_t error =
+        lsso_hip::launch_mix_project(static_cast<int>(plan.rank), mix, y_dtype, stream);
+    return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "mix_project_kernel launch");
+}
+
+// Biased projection launch (arguments already validated).
+int run_linear(const void* x, int x_dtype, int64_t rows, int64_t in_features,
+               int64_t x_row_stride, const float* weight, const float* bias,
+               const uint8_t* row_mask, int64_t out_features, void* y, int y_dtype,
+               hipStream_t stream) {
+    const int tier = lsso_hip::linear_k_tier(in_features);
+    int units = 0;
+    const int status = compute_units(&units);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    lsso_hip::LinearArgs args{};
+    args.x = x;
+    args.rows = rows;
+    args.in_features = in_features;
+    args.x_stride = x_row_stride;
+    args.weight = weight;
+    args.bias = bias;
+    args.row_mask = row_mask;
+    args.out_features = out_features;
+    args.y = y;
+    args.tiles = ceil_div(rows, lsso_hip::linear_tile_rows());
+    args.column_groups = ceil_div(out_features, lsso_hip::linear_columns_per_group(tier));
+    args.x_vector = (in_features % 8 == 0 && x_row_stride % 8 == 0 && aligned(x, 16)) ? 1 : 0;
+    args.y_vector = (out_features % 8 == 0 && aligned(y, 16)) ? 1 : 0;
+    int64_t groups = units / args.column_groups;
+    if (groups < 1) groups = 1;
+    if (groups > args.tiles) groups = args.tiles;
+    const hipError_t error =
+        lsso_hip::launch_linear(args, tier, x_dtype, y_dtype, static_cast<int>(groups), stream);
+    return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "linear_kernel launch");
 }
 
 bool projected_shape_supported(const MixerPlan& plan) {
@@ -311,30 +437,7 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projec
         return status;
     }
 
-    lsso_hip::ApplyArgs apply{};
-    apply.projected = static_cast<const uint16_t*>(projected);
-    apply.phases = buf.phases;
-    apply.mop = buf.mop;
-    apply.eta_raw = eta_raw;
-    apply.output = static_cast<uint16_t*>(output);
-    apply.batch = plan.batch;
-    apply.length = plan.length;
-    apply.heads = plan.heads;
-    apply.head_dim = plan.head_dim;
-    apply.width = plan.width;
-    apply.out_width = plan.out_width;
-    apply.phase_batch_stride = phase_batch_stride(plan, positions_mode);
-    apply.chunks = plan.apply_chunks;
-    apply.chunk_tokens = plan.apply_chunk_tokens;
-    apply.feature_blocks = plan.feature_blocks;
-    apply.block_groups = plan.block_groups;
-    apply.total_waves = plan.batch * plan.heads * plan.apply_chunks * plan.block_groups;
-    const hipError_t error =
-        lsso_hip::launch_apply(static_cast<int>(plan.rank), apply, plan.nfbw, vec, stream);
-    if (error != hipSuccess) {
-        return hip_failure(error, "apply_kernel launch");
-    }
-    return LSSO_HIP_OK;
+    return run_apply(plan, buf, projected, eta_raw, positions_mode, output, vec, stream);
 }
 
 int lsso_hip_mixer_projected_supported(const lsso_hip_mixer_shape* shape) {
@@ -388,49 +491,8 @@ int lsso_hip_mixer_forward_projected(const lsso_hip_mixer_shape* shape, const vo
         return status;
     }
 
-    int device = 0;
-    hipError_t error = hipGetDevice(&device);
-    if (error != hipSuccess) {
-        return hip_failure(error, "hipGetDevice");
-    }
-    int units = 0;
-    error = hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device);
-    if (error != hipSuccess) {
-        return hip_failure(error, "hipDeviceGetAttribute");
-    }
-    // One persistent workgroup per compute unit, each on a contiguous token
-    // range of one sample (ranges are whole tiles).
-    const int64_t tile = lsso_hip::mix_project_tile_rows();
-    int64_t ranges = ceil_div(units, plan.batch);
-    const int64_t max_ranges = ceil_div(plan.length, tile);
-    if (ranges > max_ranges) ranges = max_ranges;
-    const int64_t range_tokens = ceil_div(ceil_div(plan.length, ranges), tile) * tile;
-    ranges = ceil_div(plan.length, range_tokens);
-
-    lsso_hip::MixProjectArgs mix{};
-    mix.projected = static_cast<const uint16_t*>(projected);
-    mix.phases = buf.phases;
-    mix.mop = buf.mop;
-    mix.eta_raw = eta_raw;
-    mix.weight = out_weight;
-    mix.bias = out_bias;
-    mix.row_mask = row_mask;
-    mix.y = y;
-    mix.batch = plan.batch;
-    mix.length = plan.length;
-    mix.heads = plan.heads;
-    mix.head_dim = plan.head_dim;
-    mix.width = plan.width;
-    mix.out_features = plan.out_width;
-    mix.feature_blocks = plan.feature_blocks;
-    mix.phase_batch_stride = phase_batch_stride(plan, positions_mode);
-    mix.ranges = ranges;
-    mix.range_tokens = range_tokens;
-    error = lsso_hip::launch_mix_project(static_cast<int>(plan.rank), mix, y_dtype, stream);
-    if (error != hipSuccess) {
-        return hip_failure(error, "mix_project_kernel launch");
-    }
-    return LSSO_HIP_OK;
+    return run_mix_project(plan, buf, projected, eta_raw, positions_mode, out_weight, out_bias,
+                           row_mask, y, y_dtype, stream);
 }
 
 }  // extern "C"
@@ -702,40 +764,239 @@ int lsso_hip_linear(const void* x, int x_dtype, int64_t rows, int64_t in_feature
     if (x == nullptr || weight == nullptr || y == nullptr) {
         return fail(LSSO_HIP_EINVAL, "x, weight and y must not be NULL");
     }
-    int device = 0;
-    hipError_t error = hipGetDevice(&device);
-    if (error != hipSuccess) {
-        return hip_failure(error, "hipGetDevice");
-    }
-    int units = 0;
-    error = hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device);
-    if (error != hipSuccess) {
-        return hip_failure(error, "hipDeviceGetAttribute");
-    }
-    lsso_hip::LinearArgs args{};
-    args.x = x;
-    args.rows = rows;
-    args.in_features = in_features;
-    args.x_stride = x_row_stride;
-    args.weight = weight;
-    args.bias = bias;
-    args.row_mask = row_mask;
-    args.out_features = out_features;
-    args.y = y;
-    args.tiles = ceil_div(rows, lsso_hip::linear_tile_rows());
-    args.column_groups = ceil_div(out_features, lsso_hip::linear_columns_per_group(tier));
-    args.x_vector = (in_features % 8 == 0 && x_row_stride % 8 == 0 && aligned(x, 16)) ? 1 : 0;
-    args.y_vector = (out_features % 8 == 0 && aligned(y, 16)) ? 1 : 0;
-    int64_t groups = units / args.column_groups;
-    if (groups < 1) groups = 1;
-    if (groups > args.tiles) groups = args.tiles;
-    error = lsso_hip::launch_linear(args, tier, x_dtype, y_dtype, static_cast<int>(groups), stream_handle
-                                        ? static_cast<hipStream_t>(stream_handle)
-                                        : nullptr);
-    if (error != hipSuccess) {
-        return hip_failure(error, "linear_kernel launch");
-    }
-    return LSSO_HIP_OK;
+    return run_linear(x, x_dtype, rows, in_features, x_row_stride, weight, bias, row_mask,
+                      out_features, y, y_dtype, static_cast<hipStream_t>(stream_handle));
 }
 
 }  // extern "C"
+
+namespace {
+
+// The whole-layer forward: x -> (projection + reductions) -> solve ->
+// (apply + output projection) -> y.  Returns the heads per projection group,
+// or 0 when the geometry is outside the fused projection + reduce envelope.
+int layer_group_heads(const MixerPlan& plan) {
+    return lsso_hip::project_reduce_group_heads(plan.rank, plan.heads, plan.head_dim,
+                                                plan.out_width);
+}
+
+struct LayerPlan {
+    size_t off_packed, off_mixed, total;
+    bool fused_out;
+};
+
+void make_layer_plan(const MixerPlan& plan, LayerPlan* lp) {
+    size_t offset = plan.total;
+    lp->off_packed = offset;
+    offset = align_up(offset + sizeof(uint16_t) * plan.batch * plan.length * plan.width);
+    lp->fused_out = projected_shape_supported(plan);
+    lp->off_mixed = offset;
+    if (!lp->fused_out) {
+        offset = align_up(offset + sizeof(uint16_t) * plan.batch * plan.length * plan.out_width);
+    }
+    lp->total = offset;
+}
+
+int layer_forward_impl(const lsso_hip_mixer_shape* shape, const void* x, int x_dtype,
+                       const float* in_weight, const float* in_bias, const uint8_t* row_mask,
+                       const float* core_base_raw, const float* core_drive_weight,
+                       const float* eta_raw, const float* inverse_frequency,
+                       const float* centered_positions, int positions_mode,
+                       const float* valid_counts, const float* out_weight, const float* out_bias,
+                       void* y, int y_dtype, void* workspace, size_t workspace_bytes,
+                       void* stream_handle, void* const* events);
+
+}  // namespace
+
+extern "C" {
+
+int lsso_hip_layer_supported(const lsso_hip_mixer_shape* shape) {
+    MixerPlan plan;
+    const int status = make_plan(shape, LSSO_HIP_POSITIONS_DEFAULT, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    return layer_group_heads(plan) > 0 ? 1 : 0;
+}
+
+int lsso_hip_layer_workspace_bytes(const lsso_hip_mixer_shape* shape, int positions_mode,
+                                   size_t* bytes) {
+    if (bytes == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "bytes must not be NULL");
+    }
+    MixerPlan plan;
+    const int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    LayerPlan lp;
+    make_layer_plan(plan, &lp);
+    *bytes = lp.total;
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_layer_forward(const lsso_hip_mixer_shape* shape, const void* x, int x_dtype,
+                           const float* in_weight, const float* in_bias, const uint8_t* row_mask,
+                           const float* core_base_raw, const float* core_drive_weight,
+                           const float* eta_raw, const float* inverse_frequency,
+                           const float* centered_positions, int positions_mode,
+                           const float* valid_counts, const float* out_weight,
+                           const float* out_bias, void* y, int y_dtype, void* workspace,
+                           size_t workspace_bytes, void* stream_handle) {
+    return layer_forward_impl(shape, x, x_dtype, in_weight, in_bias, row_mask, core_base_raw,
+                              core_drive_weight, eta_raw, inverse_frequency, centered_positions,
+                              positions_mode, valid_counts, out_weight, out_bias, y, y_dtype,
+                              workspace, workspace_bytes, stream_handle, nullptr);
+}
+
+int lsso_hip_layer_forward_timed(const lsso_hip_mixer_shape* shape, const void* x, int x_dtype,
+                                 const float* in_weight, const float* in_bias,
+                                 const uint8_t* row_mask, const float* core_base_raw,
+                                 const float* core_drive_weight, const float* eta_raw,
+                                 const float* inverse_frequency, const float* centered_positions,
+                                 int positions_mode, const float* valid_counts,
+                                 const float* out_weight, const float* out_bias, void* y,
+                                 int y_dtype, void* workspace, size_t workspace_bytes,
+                                 void* stream_handle, void* const* events) {
+    if (events == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "events must not be NULL");
+    }
+    return layer_forward_impl(shape, x, x_dtype, in_weight, in_bias, row_mask, core_base_raw,
+                              core_drive_weight, eta_raw, inverse_frequency, centered_positions,
+                              positions_mode, valid_counts, out_weight, out_bias, y, y_dtype,
+                              workspace, workspace_bytes, stream_handle, events);
+}
+
+}  // extern "C"
+
+namespace {
+
+int layer_forward_impl(const lsso_hip_mixer_shape* shape, const void* x, int x_dtype,
+                       const float* in_weight, const float* in_bias, const uint8_t* row_mask,
+                       const float* core_base_raw, const float* core_drive_weight,
+                       const float* eta_raw, const float* inverse_frequency,
+                       const float* centered_positions, int positions_mode,
+                       const float* valid_counts, const float* out_weight, const float* out_bias,
+                       void* y, int y_dtype, void* workspace, size_t workspace_bytes,
+                       void* stream_handle, void* const* events) {
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    const int group_heads = layer_group_heads(plan);
+    if (group_heads == 0) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "the fused layer forward supports head_dim a multiple of 16 up to 64 and "
+                    "H*head_dim <= 384; use lsso_hip_linear and lsso_hip_mixer_forward");
+    }
+    if ((x_dtype != LSSO_HIP_F16 && x_dtype != LSSO_HIP_BF16) ||
+        (y_dtype != LSSO_HIP_F16 && y_dtype != LSSO_HIP_BF16)) {
+        return fail(LSSO_HIP_EINVAL, "x_dtype and y_dtype must be LSSO_HIP_F16 or LSSO_HIP_BF16");
+    }
+    if (x == nullptr || in_weight == nullptr || out_weight == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "x, in_weight and out_weight must not be NULL");
+    }
+    if (!aligned(x, 16)) {
+        return fail(LSSO_HIP_EINVAL, "x must be 16-byte aligned");
+    }
+    LayerPlan lp;
+    make_layer_plan(plan, &lp);
+    if (workspace == nullptr || workspace_bytes < lp.total) {
+        return fail(LSSO_HIP_EINVAL, "workspace is smaller than lsso_hip_layer_workspace_bytes()");
+    }
+    MixerBuffers buf{};
+    void* packed = static_cast<char*>(workspace) + lp.off_packed;
+    status = check_mixer_call(plan, packed, core_base_raw, core_drive_weight, eta_raw, y,
+                              centered_positions, positions_mode, workspace, plan.total, &buf);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    if (!aligned(y, 16)) {
+        return fail(LSSO_HIP_EINVAL, "y must be 16-byte aligned");
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    // Optional timing marks: events[2 k] and events[2 k + 1] bracket stage k
+    // (0 phase table, 1 projection + reductions, 2 compact solve, 3 apply +
+    // output projection); NULL entries are skipped.
+    auto mark = [&](int index) -> int {
+        if (events == nullptr || events[index] == nullptr) {
+            return LSSO_HIP_OK;
+        }
+        const hipError_t error = hipEventRecord(static_cast<hipEvent_t>(events[index]), stream);
+        return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "hipEventRecord");
+    };
+    if ((status = mark(0)) != LSSO_HIP_OK) {
+        return status;
+    }
+    status = run_phase(plan, buf, inverse_frequency, centered_positions, positions_mode, stream);
+    if (status != LSSO_HIP_OK || (status = mark(1)) != LSSO_HIP_OK) {
+        return status;
+    }
+
+    int units = 0;
+    status = compute_units(&units);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    lsso_hip::ProjectReduceArgs pr{};
+    pr.x = x;
+    pr.weight = in_weight;
+    pr.bias = in_bias;
+    pr.row_mask = row_mask;
+    pr.phases = buf.phases;
+    pr.phase_batch_stride = phase_batch_stride(plan, positions_mode);
+    pr.packed = static_cast<uint16_t*>(packed);
+    pr.partials = buf.partials;
+    pr.batch = plan.batch;
+    pr.length = plan.length;
+    pr.heads = plan.heads;
+    pr.head_dim = plan.head_dim;
+    pr.in_features = plan.out_width;
+    pr.width = plan.width;
+    pr.chunks = plan.reduce_chunks;
+    pr.chunk_tokens = plan.reduce_chunk_tokens;
+    pr.partial_stride = plan.partial_stride;
+    pr.group_heads = group_heads;
+    pr.head_groups = ceil_div(plan.heads, group_heads);
+    // One persistent workgroup per compute unit; the blocks of the head
+    // groups of one item are dealt to the same XCD when the count allows.
+    const int64_t items = plan.batch * plan.reduce_chunks;
+    int64_t per_group = units / pr.head_groups;
+    if (per_group < 1) per_group = 1;
+    if (per_group > items) per_group = items;
+    if (per_group >= 8) per_group -= per_group % 8;
+    if ((status = mark(2)) != LSSO_HIP_OK) {
+        return status;
+    }
+    const hipError_t error = lsso_hip::launch_project_reduce(
+        static_cast<int>(plan.rank), pr, x_dtype, static_cast<int>(per_group * pr.head_groups),
+        stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "project_reduce_kernel launch");
+    }
+    if ((status = mark(3)) != LSSO_HIP_OK || (status = mark(4)) != LSSO_HIP_OK) {
+        return status;
+    }
+    status = run_solve(plan, buf, core_base_raw, core_drive_weight, eta_raw, valid_counts, nullptr,
+                       stream);
+    if (status != LSSO_HIP_OK || (status = mark(5)) != LSSO_HIP_OK ||
+        (status = mark(6)) != LSSO_HIP_OK) {
+        return status;
+    }
+    if (lp.fused_out) {
+        status = run_mix_project(plan, buf, packed, eta_raw, positions_mode, out_weight, out_bias,
+                                 row_mask, y, y_dtype, stream);
+    } else {
+        void* mixed = static_cast<char*>(workspace) + lp.off_mixed;
+        status = run_apply(plan, buf, packed, eta_raw, positions_mode, mixed, true, stream);
+        if (status == LSSO_HIP_OK) {
+            status = run_linear(mixed, LSSO_HIP_BF16, plan.batch * plan.length, plan.out_width,
+                                plan.out_width, out_weight, out_bias, row_mask, plan.out_width, y,
+                                y_dtype, stream);
+        }
+    }
+    return status != LSSO_HIP_OK ? status : mark(7);
+}
+
+}  // namespace

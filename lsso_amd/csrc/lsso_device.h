@@ -43,6 +43,39 @@ __device__ __forceinline__ float f16_bits_to_float(uint16_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, bits));
 }
 
+// The value unchanged, but opaque to the optimizer: lane-dependent offsets
+// computed from it stay next to their use inside a loop instead of being
+// hoisted out of it and held in registers across the whole loop.
+__device__ __forceinline__ int opaque_int(int value) {
+    asm volatile("" : "+v"(value));
+    return value;
+}
+
+// Raw buffer access.  An access past a buffer's num_records bytes does not
+// touch memory: loads return zero and stores are dropped.  Tile loops use
+// this instead of branches around their edge accesses, so every memory
+// instruction issues unconditionally and the compiler's wait counts stay
+// exact (a conditional access makes the waits before later uses
+// conservative, which serializes a software pipeline).
+typedef __amdgpu_buffer_rsrc_t BufferRsrc;
+constexpr int kBufferConfig = 0x00020000;         // gfx9 raw buffer, 32-bit data format
+constexpr uint32_t kOutOfRange = 0x80000000u;     // an offset past every buffer here
+
+__device__ __forceinline__ BufferRsrc make_buffer(const void* base, int64_t bytes) {
+    const int records = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : static_cast<int>(bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, records, kBufferConfig);
+}
+__device__ __forceinline__ u32x4 buffer_load16(BufferRsrc buffer, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(buffer, offset, 0, 0));
+}
+__device__ __forceinline__ uint32_t buffer_load_byte(BufferRsrc buffer, uint32_t offset) {
+    return __builtin_amdgcn_raw_buffer_load_b8(buffer, offset, 0, 0);
+}
+__device__ __forceinline__ void buffer_store16(u32x4 value, BufferRsrc buffer, uint32_t offset) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, value),
+                                           buffer, offset, 0, 0);
+}
+
 // Round two floats to BF16 (round to nearest even, v_cvt_pk_bf16_f32) and
 // pack them, first value in the low half.
 __device__ __forceinline__ uint32_t pack_bf16(float low, float high) {
@@ -138,16 +171,15 @@ struct ApplyLayout {
     __device__ static constexpr int offset16(int s) { return 8 * s; }
 };
 
-// Resident BF16 slice of an FP32 weight [N, K] for y^T = W x^T on
-// v_mfma_f32_32x32x16_bf16: lane holds row n0 + lane % 32 and columns
-// 16 ks + 8 (lane / 32) + 0..7 (RNE-rounded, zero outside the matrix).  Rows
-// are read as float4 pairs when K is a multiple of 4.
+// Resident BF16 row of an FP32 weight [N, K] for y^T = W x^T on
+// v_mfma_f32_32x32x16_bf16: the lane holds row n (zeros when n < 0) at
+// columns 16 ks + 8 (lane / 32) + 0..7, RNE-rounded, zero past K.  Rows are
+// read as float4 pairs when K is a multiple of 4.
 template <int KSTEPS>
-__device__ __forceinline__ void load_weight_slice(u32x4 (&wreg)[KSTEPS], const float* weight,
-                                                  int64_t N, int64_t K, int64_t n0, int lane) {
+__device__ __forceinline__ void load_weight_row(u32x4 (&wreg)[KSTEPS], const float* weight,
+                                                int64_t n, int64_t K, int lane) {
     const int half = lane >> 5;
-    const int64_t n = n0 + (lane & 31);
-    const bool nv = n < N;
+    const bool nv = n >= 0;
     const float* wrow = weight + (nv ? n : 0) * K;
     const bool vector_rows = (K % 4) == 0;
 #pragma unroll
@@ -178,6 +210,14 @@ __device__ __forceinline__ void load_weight_slice(u32x4 (&wreg)[KSTEPS], const f
         // being hoisted next to the whole BF16 slice.
         __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+// Resident slice of rows n0 .. n0 + 31 (one row per lane % 32).
+template <int KSTEPS>
+__device__ __forceinline__ void load_weight_slice(u32x4 (&wreg)[KSTEPS], const float* weight,
+                                                  int64_t N, int64_t K, int64_t n0, int lane) {
+    const int64_t n = n0 + (lane & 31);
+    load_weight_row<KSTEPS>(wreg, weight, n < N ? n : -1, K, lane);
 }
 
 }  // namespace lsso_hip

@@ -177,6 +177,31 @@ struct LinearArgs {
     int y_vector;               // 16-byte y stores are legal
 };
 
+// Input projection fused with the L-reductions (one pass over x per head
+// group): packed = bf16(x W^T + b) per 64-token tile in LDS, contracted into
+// the G / S partials of each head of the group and optionally written out.
+struct ProjectReduceArgs {
+    const void* x;              // FP16/BF16 [B, N, D], rows contiguous
+    const float* weight;        // FP32 [width, D]
+    const float* bias;          // FP32 [width] or nullptr
+    const uint8_t* row_mask;    // [B * N] or nullptr; 0 rows project to zero
+    const uint32_t* phases;
+    int64_t phase_batch_stride;
+    uint16_t* packed;           // BF16 [B, N, width] or nullptr
+    float* partials;            // [B, H, chunks, partial_stride]
+    int64_t batch;
+    int64_t length;
+    int64_t heads;
+    int64_t head_dim;
+    int64_t in_features;        // D
+    int64_t width;              // H * (rank + head_dim)
+    int64_t chunks;
+    int64_t chunk_tokens;       // multiple of the 64-token tile
+    int64_t partial_stride;
+    int64_t group_heads;        // heads per head group
+    int64_t head_groups;
+};
+
 hipError_t launch_phase(const PhaseArgs& a, hipStream_t stream);
 hipError_t launch_reduce(int rank, const ReduceArgs& a, int cpw, bool vec, hipStream_t stream);
 hipError_t launch_solve(int rank, const SolveArgs& a, int64_t systems, hipStream_t stream);
@@ -201,6 +226,13 @@ hipError_t launch_param_reduce(const ParamReduceArgs& a, hipStream_t stream);
 
 hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,
                          int grid_groups, hipStream_t stream);
+// Heads per group of the fused projection + reduce for this geometry, or 0
+// when the shape is outside the fused envelope.
+int project_reduce_group_heads(int64_t rank, int64_t heads, int64_t head_dim,
+                               int64_t in_features);
+int project_reduce_tile_rows();
+hipError_t launch_project_reduce(int rank, const ProjectReduceArgs& a, int x_dtype, int grid,
+                                 hipStream_t stream);
 int linear_tile_rows();
 int linear_columns_per_group(int k_steps);
 int linear_k_tier(int64_t in_features);

@@ -23,30 +23,9 @@
 
 #include "lsso_device.h"
 #include "lsso_internal.h"
+#include "lsso_reduce.h"
 
 namespace lsso_hip {
-
-// ---------------------------------------------------------------------------
-// Rank layouts.
-//
-// Reduce: lane q = lane % 16 owns relation pairs [kPairSlots*q, +kPairSlots).
-// The MFMA row block `blk` = 2*slot + parity holds rank 2*(kPairSlots*m +
-// slot) + parity in row m.  Tokens are the K index of the MFMA, so the rank
-// permutation is free; it lets every lane feed the MFMA straight from its
-// own contiguous loads.
-template <int R>
-struct ReduceLayout {
-    static constexpr int kPairs = R / 2;
-    static constexpr int kPairSlots = (kPairs + 15) / 16;
-    static constexpr int kRowBlocks = 2 * kPairSlots;
-    static constexpr int kGramBlocks = kRowBlocks * (kRowBlocks + 1) / 2;
-    __device__ static constexpr int rank(int blk, int m) {
-        return 2 * (kPairSlots * m + blk / 2) + (blk & 1);
-    }
-    __device__ static constexpr bool valid(int blk, int m) {
-        return kPairSlots * m + blk / 2 < kPairs;
-    }
-};
 
 // ---------------------------------------------------------------------------
 // Phase table.
@@ -69,130 +48,6 @@ __global__ __launch_bounds__(256) void phase_kernel(PhaseArgs a) {
 
 // ---------------------------------------------------------------------------
 // Reduce.
-template <bool VEC>
-__device__ __forceinline__ uint32_t load_pair(const uint16_t* p, bool second_valid) {
-    if constexpr (VEC) {
-        return *reinterpret_cast<const uint32_t*>(p);
-    } else {
-        const uint32_t low = p[0];
-        const uint32_t high = second_valid ? static_cast<uint32_t>(p[1]) : 0u;
-        return low | (high << 16);
-    }
-}
-
-template <int R, int CPW>
-struct ReduceTile {
-    static constexpr int PS = ReduceLayout<R>::kPairSlots;
-    uint32_t rel[8][PS];
-    uint32_t ph[8][PS];
-    uint32_t con[8][CPW];
-};
-
-template <int R, int CPW, bool VEC>
-__device__ __forceinline__ void reduce_load(ReduceTile<R, CPW>& t, const ReduceArgs& a,
-                                            int64_t b, int64_t h, int cg, int q, int g,
-                                            int64_t t0, int64_t end) {
-    using L = ReduceLayout<R>;
-    constexpr int PS = L::kPairSlots;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int64_t token = t0 + 8 * g + j;
-        const bool live = token < end;
-        const uint16_t* row = a.projected + (b * a.length + (live ? token : 0)) * a.width;
-        const uint32_t* phase_row = a.phases + b * a.phase_batch_stride +
-                                    (live ? token : 0) * L::kPairs;
-        if constexpr (VEC && PS == 2) {
-            const bool pv = live && (PS * q < L::kPairs);
-            u32x2 r = {0u, 0u};
-            u32x2 p = {0u, 0u};
-            if (pv) {
-                r = *reinterpret_cast<const u32x2*>(row + h * R + 2 * PS * q);
-                p = *reinterpret_cast<const u32x2*>(phase_row + PS * q);
-            }
-            t.rel[j][0] = r.x;
-            t.rel[j][1] = r.y;
-            t.ph[j][0] = p.x;
-            t.ph[j][1] = p.y;
-        } else {
-#pragma unroll
-            for (int s = 0; s < PS; ++s) {
-                const int pair = PS * q + s;
-                const bool pv = live && pair < L::kPairs;
-                t.rel[j][s] = pv ? load_pair<VEC>(row + h * R + 2 * pair, true) : 0u;
-                t.ph[j][s] = pv ? phase_row[pair] : 0u;
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < CPW; ++c) {
-            const int64_t feature = 2 * (static_cast<int64_t>(cg) * 16 * CPW + 16 * c + q);
-            const bool fv = live && feature < a.head_dim;
-            const uint16_t* content_row = a.content + (b * a.length + (live ? token : 0)) * a.content_stride;
-            t.con[j][c] = fv ? load_pair<VEC>(content_row + h * a.head_dim + feature,
-                                              feature + 1 < a.head_dim)
-                             : 0u;
-        }
-    }
-}
-
-template <int R, int CPW>
-__device__ __forceinline__ void reduce_compute(const ReduceTile<R, CPW>& t, bool do_gram,
-                                               f32x4 (&acc_g)[ReduceLayout<R>::kGramBlocks],
-                                               f32x4 (&acc_s)[ReduceLayout<R>::kRowBlocks][2 * CPW]) {
-    using L = ReduceLayout<R>;
-    constexpr int PS = L::kPairSlots;
-    constexpr int NRB = L::kRowBlocks;
-    u32x4 a_hi[NRB];
-    u32x4 a_lo[NRB];
-#pragma unroll
-    for (int s = 0; s < PS; ++s) {
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            float x0, y0, x1, y1;
-            rotate_pair(t.rel[2 * jj][s], t.ph[2 * jj][s], x0, y0);
-            rotate_pair(t.rel[2 * jj + 1][s], t.ph[2 * jj + 1][s], x1, y1);
-            uint32_t hi, lo;
-            split_bf16(x0, x1, hi, lo);
-            a_hi[2 * s][jj] = hi;
-            a_lo[2 * s][jj] = lo;
-            split_bf16(y0, y1, hi, lo);
-            a_hi[2 * s + 1][jj] = hi;
-            a_lo[2 * s + 1][jj] = lo;
-        }
-    }
-    u32x4 b_c[2 * CPW];
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const uint32_t first = t.con[2 * jj][c];
-            const uint32_t second = t.con[2 * jj + 1][c];
-            b_c[2 * c][jj] = (first & 0xffffu) | (second << 16);
-            b_c[2 * c + 1][jj] = (first >> 16) | (second & 0xffff0000u);
-        }
-    }
-    if (do_gram) {
-        int ab = 0;
-#pragma unroll
-        for (int x = 0; x < NRB; ++x) {
-#pragma unroll
-            for (int y = 0; y <= x; ++y) {
-                acc_g[ab] = mfma16x16x32(a_hi[x], a_hi[y], acc_g[ab]);
-                acc_g[ab] = mfma16x16x32(a_hi[x], a_lo[y], acc_g[ab]);
-                acc_g[ab] = mfma16x16x32(a_lo[x], a_hi[y], acc_g[ab]);
-                ++ab;
-            }
-        }
-    }
-#pragma unroll
-    for (int x = 0; x < NRB; ++x) {
-#pragma unroll
-        for (int cb = 0; cb < 2 * CPW; ++cb) {
-            acc_s[x][cb] = mfma16x16x32(a_hi[x], b_c[cb], acc_s[x][cb]);
-            acc_s[x][cb] = mfma16x16x32(a_lo[x], b_c[cb], acc_s[x][cb]);
-        }
-    }
-}
-
 template <int R, int CPW, bool VEC>
 __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
     using L = ReduceLayout<R>;
@@ -214,17 +69,24 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
     const int g = lane >> 4;
     const bool do_gram = a.gram != 0 && cg == 0;
 
-    f32x4 acc_g[NGB];
-    f32x4 acc_s[NRB][2 * CPW];
+    // Even and odd 32-token steps of the chunk accumulate separately and are
+    // added at the end (even + odd): the fused projection + reduce kernel
+    // gives the two halves of each tile to two waves and combines them the
+    // same way, so both kernels produce the same partials bit for bit.
+    f32x4 acc_g[2][NGB];
+    f32x4 acc_s[2][NRB][2 * CPW];
 #pragma unroll
-    for (int i = 0; i < NGB; ++i) {
-        acc_g[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    }
+    for (int e = 0; e < 2; ++e) {
 #pragma unroll
-    for (int x = 0; x < NRB; ++x) {
+        for (int i = 0; i < NGB; ++i) {
+            acc_g[e][i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
 #pragma unroll
-        for (int c = 0; c < 2 * CPW; ++c) {
-            acc_s[x][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int x = 0; x < NRB; ++x) {
+#pragma unroll
+            for (int c = 0; c < 2 * CPW; ++c) {
+                acc_s[e][x][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            }
         }
     }
 
@@ -237,62 +99,34 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
         reduce_load<R, CPW, VEC>(tile_b, a, b, h, cg, q, g, begin + 32, end);
     }
     for (int64_t t0 = begin; t0 < end; t0 += 64) {
-        reduce_compute<R, CPW>(tile_a, do_gram, acc_g, acc_s);
+        reduce_compute<R, CPW>(tile_a, do_gram, acc_g[0], acc_s[0]);
         if (t0 + 64 < end) {
             reduce_load<R, CPW, VEC>(tile_a, a, b, h, cg, q, g, t0 + 64, end);
         }
         if (t0 + 32 < end) {
-            reduce_compute<R, CPW>(tile_b, do_gram, acc_g, acc_s);
+            reduce_compute<R, CPW>(tile_b, do_gram, acc_g[1], acc_s[1]);
             if (t0 + 96 < end) {
                 reduce_load<R, CPW, VEC>(tile_b, a, b, h, cg, q, g, t0 + 96, end);
             }
         }
     }
-
-    // D layout of a 16x16 MFMA block: lane holds rows 4g..4g+3 of column q.
-    float* part = a.partials + ((b * a.heads + h) * a.chunks + chunk) * a.partial_stride;
-    float* part_g = part;
-    float* part_s = part + R * R;
-    if (do_gram) {
-        int ab = 0;
 #pragma unroll
-        for (int x = 0; x < NRB; ++x) {
-#pragma unroll
-            for (int y = 0; y <= x; ++y) {
-                const bool cv = L::valid(y, q);
-                const int col = L::rank(y, q);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int m = 4 * g + i;
-                    if (cv && L::valid(x, m)) {
-                        const int row = L::rank(x, m);
-                        part_g[row * R + col] = acc_g[ab][i];
-                        if (x != y) {
-                            part_g[col * R + row] = acc_g[ab][i];
-                        }
-                    }
-                }
-                ++ab;
-            }
-        }
+    for (int i = 0; i < NGB; ++i) {
+        acc_g[0][i] += acc_g[1][i];
     }
 #pragma unroll
     for (int x = 0; x < NRB; ++x) {
 #pragma unroll
-        for (int cb = 0; cb < 2 * CPW; ++cb) {
-            const int64_t feature =
-                2 * (static_cast<int64_t>(cg) * 16 * CPW + 16 * (cb / 2) + q) + (cb & 1);
-            if (feature < a.head_dim) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int m = 4 * g + i;
-                    if (L::valid(x, m)) {
-                        part_s[L::rank(x, m) * a.head_dim + feature] = acc_s[x][cb][i];
-                    }
-                }
-            }
+        for (int c = 0; c < 2 * CPW; ++c) {
+            acc_s[0][x][c] += acc_s[1][x][c];
         }
     }
+
+    float* part = a.partials + ((b * a.heads + h) * a.chunks + chunk) * a.partial_stride;
+    if (do_gram) {
+        store_gram_partial<R>(part, acc_g[0], q, g);
+    }
+    store_cross_partial<R, CPW>(part + R * R, acc_s[0], q, g, cg, a.head_dim);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,156 @@
+"""The whole-layer native forward against the three-call native path (GPU).
+
+``lsso_hip_layer_forward`` runs the input projection fused with the token
+reductions (the packed tile is reduced in LDS, not read back) and the apply
+fused with the output projection.  The reductions run the same MFMA chains
+over the same token chunks as ``reduce_kernel`` and the projection the same
+K order and rounding as ``linear_kernel``, so the result must equal
+``linear -> forward_inference -> linear`` bit for bit.  Parity of that path
+with the FP64 oracle is tested in tests/test_hip_parity.py; one direct oracle
+check is kept here as well.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer_inputs(batch, rank, heads, head_dim, length, seed, dtype=torch.float16, scale=0.05):
+    generator = torch.Generator().manual_seed(seed)
+    dim = heads * head_dim
+    width = heads * rank + dim
+    x = torch.randn(batch, length, dim, generator=generator).to(dtype)
+    in_weight = torch.randn(width, dim, generator=generator) / dim**0.5
+    in_bias = 0.1 * torch.randn(width, generator=generator)
+    base = scale * torch.randn(heads, rank, rank, generator=generator)
+    drive = scale * torch.randn(heads, head_dim, rank, generator=generator)
+    eta_raw = scale * torch.randn(heads, generator=generator)
+    out_weight = torch.randn(dim, dim, generator=generator) / dim**0.5
+    out_bias = 0.1 * torch.randn(dim, generator=generator)
+    return [t.cuda() for t in (x, in_weight, in_bias, base, drive, eta_raw, out_weight, out_bias)]
+
+
+def _three_calls(native, x, in_weight, in_bias, base, drive, eta_raw, positions, counts,
+                 out_weight, out_bias, mask):
+    projected = native.linear(x, in_weight, in_bias, torch.bfloat16, row_mask=mask)
+    mixed = native.forward_inference(projected, base, drive, eta_raw, positions, counts)
+    return native.linear(mixed, out_weight, out_bias, x.dtype, row_mask=mask)
+
+
+@pytest.mark.parametrize(
+    ("batch", "rank", "heads", "head_dim", "length"),
+    [
+        (2, 32, 8, 32, 1000),   # headline geometry: 2 head groups, ragged tail tile
+        (2, 32, 8, 32, 4096),   # headline length: 4 chunks of 1024 tokens
+        (2, 48, 8, 32, 333),    # C5 geometry: 3 head groups, the last with 2 heads
+        (1, 64, 6, 64, 300),    # C4 geometry: D = 384 (4-wave tier), unfused output side
+        (3, 16, 8, 16, 65),     # D = 128, rank 16 (one pair slot per lane)
+        (2, 16, 3, 64, 37),     # C1 geometry, shorter than one tile
+        (1, 48, 2, 64, 130),    # rank 48 with 64-feature heads (two content blocks)
+    ],
+)
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_layer_forward_is_bitwise_the_three_call_path(native, batch, rank, heads, head_dim, length, dtype):
+    x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(
+        batch, rank, heads, head_dim, length, seed=3000 + rank + head_dim + length, dtype=dtype
+    )
+    with torch.no_grad():
+        assert native.layer_supported(x, in_w, base, drive, eta_raw)
+        y = native.layer_forward(x, in_w, in_b, base, drive, eta_raw, None, None, out_w, out_b)
+        expected = _three_calls(native, x, in_w, in_b, base, drive, eta_raw, None, None, out_w, out_b, None)
+    torch.cuda.synchronize()
+    assert y.dtype == dtype
+    assert torch.isfinite(y).all()
+    assert torch.equal(y, expected)
+
+
+def test_layer_forward_masked_per_sample_positions_and_no_bias(native):
+    batch, rank, heads, head_dim, length = 3, 32, 8, 32, 700
+    x, in_w, _in_b, base, drive, eta_raw, out_w, _out_b = _layer_inputs(
+        batch, rank, heads, head_dim, length, seed=91
+    )
+    lengths = torch.tensor([700, 123, 1])
+    mask = (torch.arange(length)[None, :] < lengths[:, None]).cuda()
+    # Garbage (NaN) in masked rows must not leak: masked rows project to zero.
+    x = torch.where(mask[:, :, None], x, torch.full_like(x, float("nan")))
+    positions = (torch.arange(length)[None, :] * torch.tensor([[1.0], [3.0], [7.0]])).cuda()
+    positions = positions - positions.mean(dim=1, keepdim=True)
+    counts = lengths.float().cuda()
+    with torch.no_grad():
+        y = native.layer_forward(x, in_w, None, base, drive, eta_raw, positions, counts, out_w, None,
+                                 row_mask=mask)
+        expected = _three_calls(native, x, in_w, None, base, drive, eta_raw, positions, counts, out_w,
+                                None, mask)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    assert torch.equal(y, expected)
+    assert not y[~mask].any()
+
+
+def test_layer_forward_shared_positions(native):
+    batch, rank, heads, head_dim, length = 2, 48, 8, 32, 200
+    x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(
+        batch, rank, heads, head_dim, length, seed=92
+    )
+    positions = (0.5 * torch.arange(length, dtype=torch.float32) - 20.0).cuda()
+    positions = positions - positions.mean()
+    with torch.no_grad():
+        y = native.layer_forward(x, in_w, in_b, base, drive, eta_raw, positions, None, out_w, out_b)
+        expected = _three_calls(native, x, in_w, in_b, base, drive, eta_raw, positions, None, out_w,
+                                out_b, None)
+    torch.cuda.synchronize()
+    assert torch.equal(y, expected)
+
+
+def test_layer_forward_rejects_unsupported_geometry_and_autograd(native):
+    # D = 512 is past the fused projection's K tiers.
+    x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(1, 32, 8, 64, 40, seed=7)
+    with torch.no_grad():
+        assert not native.layer_supported(x, in_w, base, drive, eta_raw)
+        with pytest.raises(ValueError, match="fused layer"):
+            native.layer_forward(x, in_w, in_b, base, drive, eta_raw, None, None, out_w, out_b)
+    x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(1, 32, 4, 32, 40, seed=8)
+    in_w.requires_grad_(True)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        native.layer_forward(x, in_w, in_b, base, drive, eta_raw, None, None, out_w, out_b)
+
+
+def test_module_runs_the_layer_path_and_matches_the_oracle(native):
+    """Module inference goes through lsso_hip_layer_forward and stays within
+    the reference envelope of the FP64 oracle (rel L2 <= 5e-3,
+    docs/CUDA_CONTRACT.md:93-101 in the reference)."""
+
+    from lsso_amd import LSSO, LSSOConfig
+    from oracle import lsso_reference as oracle
+
+    torch.manual_seed(11)
+    layer = LSSO(LSSOConfig(dim=256, num_heads=8, rank=32, bias=True)).cuda().eval()
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.05)
+        layer.core_drive_weight.normal_(std=0.05)
+        layer.eta_raw.normal_(std=0.3)
+    x = torch.randn(2, 300, 256, generator=torch.Generator().manual_seed(12)).half().cuda()
+    calls = []
+    original = native.layer_forward
+
+    def spy(*args, **kwargs):
+        calls.append(1)
+        return original(*args, **kwargs)
+
+    native.layer_forward = spy
+    try:
+        with torch.no_grad():
+            y = layer(x, implementation="hip")
+    finally:
+        native.layer_forward = original
+    torch.cuda.synchronize()
+    assert calls, "module inference did not take the fused layer path"
+    config = {"dim": 256, "num_heads": 8, "rank": 32, "bias": True}
+    params = {name: p.detach().double().cpu() for name, p in layer.named_parameters()}
+    expected = oracle.lsso_forward(params, config, x.cpu().double())
+    got = y.detach().to(device="cpu", dtype=torch.float64)
+    rel = float((got - expected).norm() / expected.norm())
+    assert rel <= 5e-3, rel
