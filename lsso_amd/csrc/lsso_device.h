@@ -212,6 +212,32 @@ __device__ __forceinline__ void load_weight_row(u32x4 (&wreg)[KSTEPS], const flo
     }
 }
 
+// load_weight_row for K a multiple of 8, through one raw buffer over the
+// whole [N, K] weight (wave-uniform descriptor, per-lane offsets; a row
+// n < 0 and columns past K read as zeros): no per-element fallback, so
+// loading several rows keeps no address registers alive.
+template <int KSTEPS>
+__device__ __forceinline__ void load_weight_row_k8(u32x4 (&wreg)[KSTEPS], const float* weight,
+                                                   int64_t n, int64_t N, int64_t K, int lane) {
+    const int half = lane >> 5;
+    const BufferRsrc buffer = make_buffer(weight, 4 * N * K);
+    const uint32_t row = n >= 0 ? static_cast<uint32_t>(4 * n * K) : kOutOfRange;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+        const uint32_t k0 = 16 * ks + 8 * half;
+        const bool live = n >= 0 && k0 < K;
+        const f32x4 lo = __builtin_bit_cast(f32x4, buffer_load16(buffer, live ? row + 4 * k0 : kOutOfRange));
+        const f32x4 hi = __builtin_bit_cast(f32x4, buffer_load16(buffer, live ? row + 4 * k0 + 16 : kOutOfRange));
+        wreg[ks][0] = pack_bf16(lo[0], lo[1]);
+        wreg[ks][1] = pack_bf16(lo[2], lo[3]);
+        wreg[ks][2] = pack_bf16(hi[0], hi[1]);
+        wreg[ks][3] = pack_bf16(hi[2], hi[3]);
+        // One K step at a time, so the FP32 staging of the whole row is never
+        // live at once.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // Resident slice of rows n0 .. n0 + 31 (one row per lane % 32).
 template <int KSTEPS>
 __device__ __forceinline__ void load_weight_slice(u32x4 (&wreg)[KSTEPS], const float* weight,

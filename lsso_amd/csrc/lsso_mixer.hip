@@ -69,24 +69,20 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
     const int g = lane >> 4;
     const bool do_gram = a.gram != 0 && cg == 0;
 
-    // Even and odd 32-token steps of the chunk accumulate separately and are
-    // added at the end (even + odd): the fused projection + reduce kernel
-    // gives the two halves of each tile to two waves and combines them the
-    // same way, so both kernels produce the same partials bit for bit.
-    f32x4 acc_g[2][NGB];
-    f32x4 acc_s[2][NRB][2 * CPW];
+    // One accumulator per block, 32-token steps in token order: the fused
+    // projection + reduce kernel accumulates in the same order, so both
+    // produce the same partials bit for bit.
+    f32x4 acc_g[NGB];
+    f32x4 acc_s[NRB][2 * CPW];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int i = 0; i < NGB; ++i) {
+        acc_g[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
 #pragma unroll
-        for (int i = 0; i < NGB; ++i) {
-            acc_g[e][i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        }
+    for (int x = 0; x < NRB; ++x) {
 #pragma unroll
-        for (int x = 0; x < NRB; ++x) {
-#pragma unroll
-            for (int c = 0; c < 2 * CPW; ++c) {
-                acc_s[e][x][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-            }
+        for (int c = 0; c < 2 * CPW; ++c) {
+            acc_s[x][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
 
@@ -99,34 +95,23 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
         reduce_load<R, CPW, VEC>(tile_b, a, b, h, cg, q, g, begin + 32, end);
     }
     for (int64_t t0 = begin; t0 < end; t0 += 64) {
-        reduce_compute<R, CPW>(tile_a, do_gram, acc_g[0], acc_s[0]);
+        reduce_compute<R, CPW>(tile_a, do_gram, acc_g, acc_s);
         if (t0 + 64 < end) {
             reduce_load<R, CPW, VEC>(tile_a, a, b, h, cg, q, g, t0 + 64, end);
         }
         if (t0 + 32 < end) {
-            reduce_compute<R, CPW>(tile_b, do_gram, acc_g[1], acc_s[1]);
+            reduce_compute<R, CPW>(tile_b, do_gram, acc_g, acc_s);
             if (t0 + 96 < end) {
                 reduce_load<R, CPW, VEC>(tile_b, a, b, h, cg, q, g, t0 + 96, end);
             }
         }
     }
-#pragma unroll
-    for (int i = 0; i < NGB; ++i) {
-        acc_g[0][i] += acc_g[1][i];
-    }
-#pragma unroll
-    for (int x = 0; x < NRB; ++x) {
-#pragma unroll
-        for (int c = 0; c < 2 * CPW; ++c) {
-            acc_s[0][x][c] += acc_s[1][x][c];
-        }
-    }
 
     float* part = a.partials + ((b * a.heads + h) * a.chunks + chunk) * a.partial_stride;
     if (do_gram) {
-        store_gram_partial<R>(part, acc_g[0], q, g);
+        store_gram_partial<R>(part, acc_g, q, g);
     }
-    store_cross_partial<R, CPW>(part + R * R, acc_s[0], q, g, cg, a.head_dim);
+    store_cross_partial<R, CPW>(part + R * R, acc_s, q, g, cg, a.head_dim);
 }
 
 // ---------------------------------------------------------------------------
