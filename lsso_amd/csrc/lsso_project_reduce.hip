@@ -103,6 +103,7 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
     __shared__ __attribute__((aligned(16))) uint16_t s_y[2][kPrTile * YP];
     __shared__ __attribute__((aligned(16))) uint32_t s_ph[3][kPrTile * PHP];
     __shared__ int s_keep[2][kPrTile];
+    __shared__ int s_keep_all[2];
     __shared__ __attribute__((aligned(16))) float s_bias[VW];
     __shared__ int s_col[VW];
 
@@ -144,35 +145,45 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
     }
 
     // A tile of the workgroup's sequence: tokens [t0, t0 + 64) of item
-    // (sample b, chunk); item >= items marks the end of the sequence.
+    // (sample b, chunk); item >= items marks the end of the sequence.  The
+    // bookkeeping is 32-bit (the host keeps B * N below 2^31).
+    const int n_items = static_cast<int>(items);
+    const int n_slots = static_cast<int>(slots);
+    const int n_chunks = static_cast<int>(a.chunks);
+    const int chunk_tokens = static_cast<int>(a.chunk_tokens);
+    const int length = static_cast<int>(a.length);
     struct Cursor {
-        int64_t item, b, chunk, end, t0;
+        int item, b, chunk, end, t0;
     };
-    auto open_item = [&](int64_t item) {
+    auto open_item = [&](int item) {
         Cursor c;
         c.item = item;
-        c.b = item / a.chunks;
-        c.chunk = item - c.b * a.chunks;
-        c.t0 = c.chunk * a.chunk_tokens;
-        c.end = c.t0 + a.chunk_tokens < a.length ? c.t0 + a.chunk_tokens : a.length;
+        c.b = item / n_chunks;
+        c.chunk = item - c.b * n_chunks;
+        c.t0 = c.chunk * chunk_tokens;
+        c.end = c.t0 + chunk_tokens < length ? c.t0 + chunk_tokens : length;
         return c;
     };
     auto advance = [&](const Cursor& c) {
-        if (c.item >= items || c.t0 + kPrTile < c.end) {
+        if (c.item >= n_items || c.t0 + kPrTile < c.end) {
             Cursor n = c;
             n.t0 += kPrTile;
             return n;
         }
-        const int64_t next_item = c.item + slots;
-        if (next_item < items) {
+        const int next_item = c.item + n_slots;
+        if (next_item < n_items) {
             return open_item(next_item);
         }
         Cursor n = c;
-        n.item = items;
+        n.item = n_items;
         return n;
     };
     auto tile_rows = [&](const Cursor& c) -> int {
-        return c.item < items ? static_cast<int>(c.end - c.t0 < kPrTile ? c.end - c.t0 : kPrTile) : 0;
+        return c.item < n_items ? (c.end - c.t0 < kPrTile ? c.end - c.t0 : kPrTile) : 0;
+    };
+    // First row of a cursor's tile in the [B * N] row space.
+    auto tile_row0 = [&](const Cursor& c) -> int64_t {
+        return static_cast<int64_t>(c.b) * length + c.t0;
     };
 
     if (wave < kProj) {
@@ -191,29 +202,39 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
         // chunk (or an absent tile) fall outside the buffer and are dropped.
         constexpr int kProjStores = kPrTile * VW / 8 / (kProj * 64);
         static_assert(kProjStores % 2 == 0 && KSTEPS % (kProjStores / 2) == 0, "store interleave");
-        auto store_piece = [&](const Cursor& prev, const uint16_t* yprev, int i) {
-            const BufferRsrc obuf = make_buffer(
-                a.packed + (a.packed != nullptr ? (prev.b * a.length + prev.t0) * a.width : 0),
-                a.packed != nullptr ? int64_t{2} * tile_rows(prev) * a.width : 0);
-            const int piece = opaque_int(tid) + i * kProj * 64;
-            const int mr = piece / (VW / 8);
-            const int c8 = 8 * (piece - mr * (VW / 8));
-            const int n = static_cast<int>(packed_column(c8));
-            const u32x2 lo = *reinterpret_cast<const u32x2*>(&yprev[mr * YP + c8]);
-            const u32x2 hi = *reinterpret_cast<const u32x2*>(&yprev[mr * YP + c8 + 4]);
+        static_assert((kProj * 64) % (VW / 8) == 0, "store pieces keep their column");
+        // Piece i of this thread: row tid / (VW / 8) + i * kPieceRows, the
+        // same 8 virtual columns for every i, so one offset per thread serves
+        // all pieces (plus a constant row stride).
+        constexpr int kPieceRows = kProj * 64 / (VW / 8);
+        const int store_row = tid / (VW / 8);
+        const int store_c8 = 8 * (tid - store_row * (VW / 8));
+        const int store_col = static_cast<int>(packed_column(store_c8));
+        const uint32_t store_base = store_col >= 0
+            ? 2u * static_cast<uint32_t>(store_row * static_cast<int>(a.width) + store_col) : kOutOfRange;
+        const uint32_t store_step = 2u * static_cast<uint32_t>(kPieceRows * a.width);
+        const int store_lds = store_row * YP + store_c8;
+        auto store_piece = [&](const BufferRsrc& obuf, const uint16_t* yprev, int i) {
+            const u32x2 lo = *reinterpret_cast<const u32x2*>(&yprev[store_lds + i * kPieceRows * YP]);
+            const u32x2 hi = *reinterpret_cast<const u32x2*>(&yprev[store_lds + i * kPieceRows * YP + 4]);
             const u32x4 v = {lo.x, lo.y, hi.x, hi.y};
-            const uint32_t offset =
-                n >= 0 ? 2u * static_cast<uint32_t>(mr * static_cast<int>(a.width) + n) : kOutOfRange;
-            buffer_store16(v, obuf, offset);
+            buffer_store16(v, obuf, store_base + static_cast<uint32_t>(i) * store_step);
         };
-        Cursor cur = open_item(slot);
+        auto store_buffer = [&](const Cursor& prev) {
+            return make_buffer(a.packed + (a.packed != nullptr ? tile_row0(prev) * a.width : 0),
+                               a.packed != nullptr ? int64_t{2} * tile_rows(prev) * a.width : 0);
+        };
+        Cursor cur = open_item(static_cast<int>(slot));
         Cursor prev = cur;
-        prev.item = items;
+        prev.item = n_items;
         int k2 = 0;
-        while (cur.item < items) {
+        while (cur.item < n_items) {
             const uint16_t* xt = s_x[k2];
             uint16_t* yt = s_y[k2];
             const uint16_t* yprev = s_y[k2 ^ 1];
+            const BufferRsrc obuf = store_buffer(prev);
+            // Rows are all kept unless the tile is partial or masked.
+            const bool all_keep = __builtin_amdgcn_readfirstlane(s_keep_all[k2]) != 0;
             // Two 32-row halves of the tile, each with both column blocks.
 #pragma unroll 1
             for (int mb = 0; mb < 2; ++mb) {
@@ -242,13 +263,13 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
                     }
                     constexpr int kEvery = KSTEPS / (kProjStores / 2);
                     if (ks % kEvery == kEvery - 1) {
-                        store_piece(prev, yprev, mb * (kProjStores / 2) + ks / kEvery);
+                        store_piece(obuf, yprev, mb * (kProjStores / 2) + ks / kEvery);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 // Bias, row mask and BF16 rounding into the packed tile.
                 const int mr = mb * 32 + row_k;
-                const bool keep = s_keep[k2][mr] != 0;
+                const bool keep = all_keep || s_keep[k2][mr] != 0;
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
@@ -273,9 +294,12 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
         }
         // Drain: the last tile's packed store, beside the reduction waves'
         // last step.
+        {
+            const BufferRsrc obuf = store_buffer(prev);
 #pragma unroll
-        for (int i = 0; i < kProjStores; ++i) {
-            store_piece(prev, s_y[k2 ^ 1], i);
+            for (int i = 0; i < kProjStores; ++i) {
+                store_piece(obuf, s_y[k2 ^ 1], i);
+            }
         }
         __syncthreads();
         return;
@@ -315,26 +339,43 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
         uint32_t mask;
         int rows;
     };
+    // Per-thread addressing of the staging work: chunk i of thread io is x
+    // piece io + i * kIo; when kIo is a multiple of the pieces per row, every
+    // chunk of a thread sits in the same column at a fixed row stride, so a
+    // single base plus constants addresses all of them.
+    constexpr bool kRowStride = kIo % kChunksPerRow == 0;
+    constexpr int kRowStep = kIo / kChunksPerRow;
+    constexpr bool kPhaseStride = kIo % (PAIRS / 4) == 0;
     auto load_stage = [&](Stage& st, const Cursor& c) {
         const int io_o = opaque_int(io);
         const int rows = tile_rows(c);
         st.rows = rows;
         const BufferRsrc mbuf = make_buffer(
-            a.row_mask + (a.row_mask != nullptr ? c.b * a.length + c.t0 : 0),
+            a.row_mask + (a.row_mask != nullptr ? tile_row0(c) : 0),
             a.row_mask != nullptr ? rows : 0);
         st.mask = buffer_load_byte(mbuf, static_cast<uint32_t>(io_o));
         const BufferRsrc xbuf = make_buffer(
-            static_cast<const uint16_t*>(a.x) + (c.b * a.length + c.t0) * D, int64_t{2} * rows * D);
+            static_cast<const uint16_t*>(a.x) + tile_row0(c) * D, int64_t{2} * rows * D);
+        const int Di = static_cast<int>(D);
+        if constexpr (kRowStride) {
+            const int rr0 = io_o / kChunksPerRow;
+            const int cc = io_o - rr0 * kChunksPerRow;
+            const uint32_t base = 8 * cc < Di ? 2u * static_cast<uint32_t>(rr0 * Di + 8 * cc) : kOutOfRange;
 #pragma unroll
-        for (int i = 0; i < kXChunks; ++i) {
-            const int chunk = io_o + i * kIo;
-            const int rr = chunk / kChunksPerRow;
-            const int cc = chunk - rr * kChunksPerRow;
-            const uint32_t offset = 8 * cc < D ? 2u * static_cast<uint32_t>(rr * static_cast<int>(D) + 8 * cc)
-                                               : kOutOfRange;
-            st.x[i] = buffer_load16(xbuf, offset);
+            for (int i = 0; i < kXChunks; ++i) {
+                st.x[i] = buffer_load16(xbuf, base + 2u * static_cast<uint32_t>(i * kRowStep * Di));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kXChunks; ++i) {
+                const int chunk = io_o + i * kIo;
+                const int rr = chunk / kChunksPerRow;
+                const int cc = chunk - rr * kChunksPerRow;
+                const uint32_t offset = 8 * cc < Di ? 2u * static_cast<uint32_t>(rr * Di + 8 * cc) : kOutOfRange;
+                st.x[i] = buffer_load16(xbuf, offset);
+            }
         }
-        const BufferRsrc pbuf = make_buffer(a.phases + c.b * a.phase_batch_stride + c.t0 * PAIRS,
+        const BufferRsrc pbuf = make_buffer(a.phases + c.b * a.phase_batch_stride + int64_t{c.t0} * PAIRS,
                                             int64_t{4} * rows * PAIRS);
 #pragma unroll
         for (int p = 0; p < kPhaseChunks; ++p) {
@@ -347,30 +388,56 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
     auto write_stage = [&](const Stage& st, int x_buf, int phase_buf) {
         const int io_o = opaque_int(io);
         if (io_o < kPrTile) {
-            s_keep[x_buf][io_o] = io_o < st.rows && (a.row_mask == nullptr || st.mask != 0);
+            const bool keep = io_o < st.rows && (a.row_mask == nullptr || st.mask != 0);
+            s_keep[x_buf][io_o] = keep;
+            // The first reduction wave holds the tile's 64 rows.
+            const bool all = __ballot(keep) == ~0ull;
+            if (io_o == 0) {
+                s_keep_all[x_buf] = all;
+            }
         }
-#pragma unroll
-        for (int i = 0; i < kXChunks; ++i) {
-            const int chunk = io_o + i * kIo;
-            const int rr = chunk / kChunksPerRow;
-            const int cc = chunk - rr * kChunksPerRow;
+        auto convert = [&](const u32x4& raw) {
             u32x4 v;
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                uint32_t value = st.x[i][p];
+                uint32_t value = raw[p];
                 if constexpr (XT == LSSO_HIP_F16) {
                     value = pack_bf16(f16_lo(value), f16_hi(value));
                 }
                 v[p] = value;
             }
-            *reinterpret_cast<u32x4*>(&s_x[x_buf][rr * KP + 8 * cc]) = v;
+            return v;
+        };
+        if constexpr (kRowStride) {
+            const int rr0 = io_o / kChunksPerRow;
+            const int cc = io_o - rr0 * kChunksPerRow;
+            uint16_t* base = &s_x[x_buf][rr0 * KP + 8 * cc];
+#pragma unroll
+            for (int i = 0; i < kXChunks; ++i) {
+                *reinterpret_cast<u32x4*>(base + i * kRowStep * KP) = convert(st.x[i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kXChunks; ++i) {
+                const int chunk = io_o + i * kIo;
+                const int rr = chunk / kChunksPerRow;
+                const int cc = chunk - rr * kChunksPerRow;
+                *reinterpret_cast<u32x4*>(&s_x[x_buf][rr * KP + 8 * cc]) = convert(st.x[i]);
+            }
         }
 #pragma unroll
         for (int p = 0; p < kPhaseChunks; ++p) {
             const int piece = io_o + p * kIo;
             if (kPhasePieces % kIo == 0 || piece < kPhasePieces) {
-                const int rr = piece / (PAIRS / 4);
-                const int pc = piece - rr * (PAIRS / 4);
+                int rr, pc;
+                if constexpr (kPhaseStride) {
+                    const int rr0 = io_o / (PAIRS / 4);
+                    pc = io_o - rr0 * (PAIRS / 4);
+                    rr = rr0 + p * (kIo / (PAIRS / 4));
+                } else {
+                    rr = piece / (PAIRS / 4);
+                    pc = piece - rr * (PAIRS / 4);
+                }
                 uint32_t* dst = &s_ph[phase_buf][rr * PHP + 4 * pc];
                 *reinterpret_cast<u32x2*>(dst) = (u32x2){st.ph[p][0], st.ph[p][1]};
                 *reinterpret_cast<u32x2*>(dst + 2) = (u32x2){st.ph[p][2], st.ph[p][3]};
@@ -380,38 +447,36 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
 
     // Reduction operands of this wave's head for the 32 tokens of half st
     // of a packed tile (the reduce_load layout: lane (q, g) holds tokens
-    // 8 g .. 8 g + 7).
+    // 8 g .. 8 g + 7).  One base per operand; the rows are constant offsets.
     auto lds_tile = [&](ReduceTile<R, CPW>& t, const uint16_t* yt, const uint32_t* pt, int st) {
         const int lane_o = opaque_int(lane);
         const int q = lane_o & 15;
         const int g = lane_o >> 4;
+        const uint16_t* rbase = yt + (32 * st + 8 * g) * YP + unit_head * R + 2 * PS * q;
+        const uint32_t* pbase = pt + (32 * st + 8 * g) * PHP + PS * q;
+        const uint16_t* cbase = yt + (32 * st + 8 * g) * YP + hg * R + unit_head * d + 2 * q;
+        const bool pv = PS * q < PAIRS;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-            const int row = 32 * st + 8 * g + jj;
-            const uint16_t* yrow = yt + row * YP;
-            const uint32_t* prow = pt + row * PHP;
             if constexpr (PS == 2) {
-                const bool pv = PS * q < PAIRS;
                 u32x2 r = {0u, 0u};
                 u32x2 p = {0u, 0u};
                 if (pv) {
-                    r = *reinterpret_cast<const u32x2*>(yrow + unit_head * R + 2 * PS * q);
-                    p = *reinterpret_cast<const u32x2*>(prow + PS * q);
+                    r = *reinterpret_cast<const u32x2*>(rbase + jj * YP);
+                    p = *reinterpret_cast<const u32x2*>(pbase + jj * PHP);
                 }
                 t.rel[jj][0] = r.x;
                 t.rel[jj][1] = r.y;
                 t.ph[jj][0] = p.x;
                 t.ph[jj][1] = p.y;
             } else {
-                const bool pv = q < PAIRS;
-                t.rel[jj][0] = pv ? *reinterpret_cast<const uint32_t*>(yrow + unit_head * R + 2 * q) : 0u;
-                t.ph[jj][0] = pv ? prow[q] : 0u;
+                t.rel[jj][0] = pv ? *reinterpret_cast<const uint32_t*>(rbase + jj * YP) : 0u;
+                t.ph[jj][0] = pv ? pbase[jj * PHP] : 0u;
             }
 #pragma unroll
             for (int c = 0; c < CPW; ++c) {
-                const int feature = 2 * (16 * c + q);
-                t.con[jj][c] = feature < d
-                    ? *reinterpret_cast<const uint32_t*>(yrow + hg * R + unit_head * d + feature)
+                t.con[jj][c] = 2 * (16 * c + q) < d
+                    ? *reinterpret_cast<const uint32_t*>(cbase + jj * YP + 32 * c)
                     : 0u;
             }
         }
@@ -422,11 +487,13 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
     auto step = [&](const Cursor& prev, const Cursor& cur, const Cursor& nx1, const Cursor& ahead,
                     Stage& load, const Stage& next, int k2, int k3) {
         load_stage(load, ahead);
-        if (prev.item < items) {
+        if (prev.item < n_items) {
             const uint16_t* yt = s_y[k2 ^ 1];
             const uint32_t* pt = s_ph[k3 == 0 ? 2 : k3 - 1];
             if (unit_active) {
-#pragma unroll
+                // One half at a time: the operands of one 32-token half are
+                // live at once.
+#pragma unroll 1
                 for (int st = 0; st < 2; ++st) {
                     if (prev.t0 + 32 * st < prev.end) {
                         ReduceTile<R, CPW> t;
@@ -437,9 +504,8 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
             }
             if (cur.item != prev.item) {
                 if (unit_active) {
-                    const int lane_o = opaque_int(lane);
-                    const int q = lane_o & 15;
-                    const int g = lane_o >> 4;
+                    const int q = lane & 15;
+                    const int g = lane >> 4;
                     float* part = a.partials +
                                   ((prev.b * a.heads + h0 + unit_head) * a.chunks + prev.chunk) *
                                       a.partial_stride;
@@ -449,7 +515,7 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
                 clear_units();
             }
         }
-        if (nx1.item < items) {
+        if (nx1.item < n_items) {
             write_stage(next, k2 ^ 1, k3 == 2 ? 0 : k3 + 1);
         }
         __syncthreads();
@@ -457,14 +523,14 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
 
     Stage stage_a;
     Stage stage_b;
-    Cursor cur = open_item(slot);
+    Cursor cur = open_item(static_cast<int>(slot));
     Cursor nx1 = advance(cur);
     load_stage(stage_a, cur);
     load_stage(stage_b, nx1);
     write_stage(stage_a, 0, 0);
     __syncthreads();   // s_bias, s_col and tile 0 are in LDS
     Cursor prev = cur;
-    prev.item = items;
+    prev.item = n_items;
     // Tile k is staged in registers stage k % 2, its x and packed tile in
     // buffers k % 2 and its phases in buffer k % 3; the loop body is
     // unrolled twice so that the stages keep fixed registers.  The step
@@ -473,7 +539,7 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
     while (true) {
         Cursor nx2 = advance(nx1);
         step(prev, cur, nx1, nx2, stage_a, stage_b, 0, k3);
-        if (cur.item >= items) {
+        if (cur.item >= n_items) {
             break;
         }
         prev = cur;
@@ -482,7 +548,7 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
         k3 = k3 == 2 ? 0 : k3 + 1;
         nx2 = advance(nx1);
         step(prev, cur, nx1, nx2, stage_b, stage_a, 1, k3);
-        if (cur.item >= items) {
+        if (cur.item >= n_items) {
             break;
         }
         prev = cur;
