@@ -116,53 +116,64 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
     }
 
     // Staging of upcoming tiles: packed chunks and phases held in registers
-    // (DEPTH tiles ahead) while the current tile is processed.
-    const int row_chunks = static_cast<int>(W / 8);
+    // (DEPTH tiles ahead) while the current tile is processed.  A tile's
+    // packed rows are one contiguous block, so chunk c of this thread is
+    // bytes 16 (tid + c kMixThreads) of it; the LDS slots (padded pitch) and
+    // the store pieces are fixed per thread and computed once.  Loads and
+    // stores go through raw buffers sized to the tile's valid rows, so rows
+    // past the range read as zeros and are not stored, without branches.
+    const int Wi = static_cast<int>(W);
+    const int Di = static_cast<int>(D);
+    const int row_chunks = Wi / 8;
     const int tile_chunks = kMixRows * row_chunks;
+    int lds_chunk[kMixChunks];
+#pragma unroll
+    for (int c = 0; c < kMixChunks; ++c) {
+        const int idx = tid + c * kMixThreads;
+        const int row = idx / row_chunks;
+        lds_chunk[c] = idx < tile_chunks ? row * kMixPitch + 8 * (idx - row * row_chunks) : -1;
+    }
+    const int phase_lds = tid < kMixRows * (PAIRS / 4)
+        ? (tid / (PAIRS / 4)) * PHP + 4 * (tid % (PAIRS / 4)) : -1;
+    const int row_pieces = Di / 8;
+    int store_lds[kMixStoreChunks];
+    uint32_t store_off[kMixStoreChunks];
+#pragma unroll
+    for (int i = 0; i < kMixStoreChunks; ++i) {
+        const int idx = tid + i * kMixThreads;
+        const int row = idx / row_pieces;
+        const int c8 = 8 * (idx - row * row_pieces);
+        store_lds[i] = row * kMixDPitch + c8;
+        store_off[i] = row < kMixRows ? 2u * static_cast<uint32_t>(row * Di + c8) : kOutOfRange;
+    }
+    const int end_i = static_cast<int>(end);
     const uint16_t* sample_rows = a.projected + b * a.length * W;
     const uint32_t* sample_phases = a.phases + b * a.phase_batch_stride;
+    auto tile_rows = [&](int t0) { return end_i - t0 < kMixRows ? end_i - t0 : kMixRows; };
     struct Stage {
         u32x4 chunk[kMixChunks];
         u32x4 phase;
-        uint32_t live;
     };
-    auto fetch = [&](Stage& st, int64_t t0) {
-        st.live = 0;
+    auto fetch = [&](Stage& st, int t0) {
+        const int rows = tile_rows(t0);
+        const BufferRsrc pk = make_buffer(sample_rows + static_cast<int64_t>(t0) * Wi, int64_t{2} * rows * Wi);
 #pragma unroll
         for (int c = 0; c < kMixChunks; ++c) {
-            const int idx = tid + c * kMixThreads;
-            const int row = idx / row_chunks;
-            const int col = idx - row * row_chunks;
-            const bool live = idx < tile_chunks && t0 + row < end;
-            const int64_t token = live ? t0 + row : begin;
-            st.chunk[c] = *reinterpret_cast<const u32x4*>(sample_rows + token * W + 8 * (live ? col : 0));
-            st.live |= live ? (1u << c) : 0u;
+            st.chunk[c] = buffer_load16(pk, 16u * static_cast<uint32_t>(tid + c * kMixThreads));
         }
-        const int row = tid / (PAIRS / 4);
-        const int quad = tid - row * (PAIRS / 4);
-        const bool live = tid < kMixRows * (PAIRS / 4) && t0 + row < end;
-        const int64_t token = live ? t0 + row : begin;
-        st.phase = *reinterpret_cast<const u32x4*>(sample_phases + token * PAIRS + 4 * (live ? quad : 0));
-        st.live |= live ? (1u << kMixChunks) : 0u;
+        const BufferRsrc ph = make_buffer(sample_phases + static_cast<int64_t>(t0) * PAIRS,
+                                          int64_t{4} * rows * PAIRS);
+        st.phase = buffer_load16(ph, phase_lds >= 0 ? 16u * static_cast<uint32_t>(tid) : kOutOfRange);
     };
     auto commit = [&](const Stage& st) {
 #pragma unroll
         for (int c = 0; c < kMixChunks; ++c) {
-            const int idx = tid + c * kMixThreads;
-            if (idx < tile_chunks) {
-                const int row = idx / row_chunks;
-                const int col = idx - row * row_chunks;
-                const bool live = (st.live >> c) & 1u;
-                *reinterpret_cast<u32x4*>(s_pk + row * kMixPitch + 8 * col) =
-                    live ? st.chunk[c] : (u32x4){0u, 0u, 0u, 0u};
+            if (lds_chunk[c] >= 0) {
+                *reinterpret_cast<u32x4*>(s_pk + lds_chunk[c]) = st.chunk[c];
             }
         }
-        if (tid < kMixRows * (PAIRS / 4)) {
-            const int row = tid / (PAIRS / 4);
-            const int quad = tid - row * (PAIRS / 4);
-            const bool live = (st.live >> kMixChunks) & 1u;
-            *reinterpret_cast<u32x4*>(s_ph + row * PHP + 4 * quad) =
-                live ? st.phase : (u32x4){0u, 0u, 0u, 0u};
+        if (phase_lds >= 0) {
+            *reinterpret_cast<u32x4*>(s_ph + phase_lds) = st.phase;
         }
     };
 
@@ -172,15 +183,19 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
     // The wait counter retires memory operations in issue order, so the
     // mask bytes are requested before the next rows and the rows consumed
     // before this tile's stores are issued.
-    auto iteration = [&](int64_t t0, Stage& issue, Stage& consume) {
+    auto iteration = [&](int t0, Stage& issue, Stage& consume) {
+        const int rows = tile_rows(t0);
+        const BufferRsrc mbuf = make_buffer(
+            a.row_mask + (a.row_mask != nullptr ? b * a.length + t0 : 0), a.row_mask != nullptr ? rows : 0);
         bool keep[kMixRowBlocks];
 #pragma unroll
         for (int mb = 0; mb < kMixRowBlocks; ++mb) {
-            const int64_t m = t0 + mb * 32 + (lane & 31);
-            keep[mb] = m < end && (a.row_mask == nullptr || a.row_mask[b * a.length + (m < end ? m : begin)] != 0);
+            const int m = mb * 32 + (lane & 31);
+            const uint32_t byte = buffer_load_byte(mbuf, static_cast<uint32_t>(m));
+            keep[mb] = m < rows && (a.row_mask == nullptr || byte != 0);
         }
-        const int64_t ahead = t0 + DEPTH * kMixRows;
-        if (ahead < end) {
+        const int ahead = t0 + DEPTH * kMixRows;
+        if (ahead < end_i) {
             fetch(issue, ahead);
         }
 
@@ -329,32 +344,27 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
         }
         // The next tile's rows replace this tile's (read before the barrier
         // above); the stage is complete after this barrier.
-        if (t0 + kMixRows < end) {
+        if (t0 + kMixRows < end_i) {
             commit(consume);
         }
         __syncthreads();
         {
-            const int row_pieces = static_cast<int>(D / 8);
-            uint16_t* y_rows = static_cast<uint16_t*>(a.y) + b * a.length * D;
+            const BufferRsrc ybuf = make_buffer(
+                static_cast<uint16_t*>(a.y) + (b * a.length + t0) * D, int64_t{2} * rows * Di);
 #pragma unroll
             for (int i = 0; i < kMixStoreChunks; ++i) {
-                const int idx = tid + i * kMixThreads;
-                const int row = idx / row_pieces;
-                const int c8 = 8 * (idx - row * row_pieces);
-                if (row < kMixRows && t0 + row < end) {
-                    *reinterpret_cast<u32x4*>(y_rows + (t0 + row) * D + c8) =
-                        *reinterpret_cast<const u32x4*>(s_st + row * kMixDPitch + c8);
-                }
+                buffer_store16(*reinterpret_cast<const u32x4*>(s_st + store_lds[i]), ybuf, store_off[i]);
             }
         }
     };
 
+    const int begin_i = static_cast<int>(begin);
     Stage stage_a;
     Stage stage_b;
-    fetch(stage_a, begin);
+    fetch(stage_a, begin_i);
     if constexpr (DEPTH == 2) {
-        if (begin + kMixRows < end) {
-            fetch(stage_b, begin + kMixRows);
+        if (begin_i + kMixRows < end_i) {
+            fetch(stage_b, begin_i + kMixRows);
         }
     }
     commit(stage_a);
@@ -362,14 +372,14 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
     if constexpr (DEPTH == 2) {
         // Tiles alternate between the two stage sets: tile t consumes the set
         // issued two tiles earlier and reissues it.
-        for (int64_t t0 = begin; t0 < end; t0 += 2 * kMixRows) {
+        for (int t0 = begin_i; t0 < end_i; t0 += 2 * kMixRows) {
             iteration(t0, stage_a, stage_b);
-            if (t0 + kMixRows < end) {
+            if (t0 + kMixRows < end_i) {
                 iteration(t0 + kMixRows, stage_b, stage_a);
             }
         }
     } else {
-        for (int64_t t0 = begin; t0 < end; t0 += kMixRows) {
+        for (int t0 = begin_i; t0 < end_i; t0 += kMixRows) {
             iteration(t0, stage_a, stage_a);
         }
     }
