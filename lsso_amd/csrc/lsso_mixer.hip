@@ -117,7 +117,8 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
 // ---------------------------------------------------------------------------
 // Solve: one 256-thread workgroup per (b, h) system.
 //
-//   A = G / n + I = L L^T            Cholesky; L^-1 from the same steps
+//   A = G / n + I = L L^T            Cholesky
+//   L^-1                             forward substitution, one column per lane
 //   Z = L^-1 S / sqrt(n)             product
 //   Theta = Theta0 + Z W / sqrt(n)   product
 //   I + K = I + F F^T + Omega        product
@@ -125,11 +126,12 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
 //   U = (I + K)^-1 Z, X = 2U - (1 + eta) Z, M' = L^-T X / sqrt(n)   products
 //
 // The two factorizations are sequential (one step per rank) and run in wave 0
-// with one matrix row per lane held in registers; a step's pivot column or
-// row reaches the other lanes through LDS (in-order within one wave, so no
-// barrier).  The products use all four waves.  Step loops stay rolled: the
-// instruction stream runs once per system, so code size sets the speed of
-// this kernel more than instruction count.
+// with one matrix row per lane held in registers.  A step's pivot row reaches
+// the other lanes by v_readlane into scalar registers, one element per
+// column, so a step is one chain of VALU instructions with no LDS round trip.
+// Step loops stay rolled (the pivot lane and column are wave-uniform
+// registers); the substitution for L^-1 has no cross-lane traffic and is
+// unrolled.  The products use all four waves.
 extern "C" __device__ unsigned int __ockl_wfred_max_u32(unsigned int);
 
 constexpr int kSolveThreads = 256;
@@ -140,7 +142,6 @@ struct SolveLayout {
     static constexpr int kLD = R + 4;              // R x R matrices (16-byte rows)
     static constexpr int kPLD = kSolvePanel + 4;   // R x panel matrices
     static constexpr int kChunks = R / 16;         // 16-float register chunks per row
-    static constexpr bool kSplit = R <= 32;        // Cholesky rows and L^-1 rows on separate lanes
     static constexpr int kThetaQuads = (R * R / 4 + kSolveThreads - 1) / kSolveThreads;
     static constexpr int kChunkBatch = R <= 32 ? 8 : 4;    // chunk loads in flight per element
     static constexpr int kLinv = 0;                       // L^-1 rows
@@ -150,9 +151,8 @@ struct SolveLayout {
     static constexpr int kSys = kWork + R * kLD;          // I + K, then (I + K)^-1
     static constexpr int kPanelA = kSys + R * kLD;        // S panel; drive panel; X panel
     static constexpr int kPanelB = kPanelA + R * kPLD;    // Z panel; M' panel
-    static constexpr int kColumn = kPanelB + R * kPLD;    // 2 x 64 step columns
-    static constexpr int kRow = kColumn + 128;            // 2 x R step rows
-    static constexpr int kPivot = kRow + 2 * R;           // pivot row of each step
+    static constexpr int kColumn = kPanelB + R * kPLD;    // 1 / L_ii
+    static constexpr int kPivot = kColumn + 64;           // pivot row of each step
     static constexpr int kTotal = kPivot + R;
 };
 
@@ -298,6 +298,46 @@ __device__ __forceinline__ void wave_lds_order() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// r -= f * (row of lane `source` of r), the source row read by v_readlane
+// element by element.  The source lane must pass f = 0, so its row is the
+// same before and after each element's update.
+template <int Q, int q = 0>
+__device__ __forceinline__ void row_axpy_lane(const RegRow<Q>& r, float f, int source) {
+    if constexpr (q < Q) {
+        f32x16 t = r.template at<q>();
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float pivot_row = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[e]), source));
+            t[e] = fmaf(-f, pivot_row, t[e]);
+        }
+        r.template at<q>() = t;
+        row_axpy_lane<Q, q + 1>(r, f, source);
+    }
+}
+
+// Column `lane` of L^-1 for lower-triangular L (row-major in LDS, row stride
+// LD) and the reciprocal diagonal: x_i = (delta_i,lane - sum_{m<i} L_im x_m)
+// / L_ii, summed in ascending m.  Rows of L are wave-uniform LDS reads.
+template <int R, int LD>
+__device__ __forceinline__ void lower_inverse_column(const float* l, const float* inv_diag, int lane,
+                                                     float (&x)[R]) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        float acc = lane == i ? 1.0f : 0.0f;
+#pragma unroll
+        for (int m = 0; m < i; m += 4) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(l + i * LD + m);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (m + e < i) {
+                    acc = fmaf(-l4[e], x[m + e], acc);
+                }
+            }
+        }
+        x[i] = acc * inv_diag[i];
+    }
+}
+
 template <int R>
 __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
     using SL = SolveLayout<R>;
@@ -379,84 +419,65 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
     }
     __syncthreads();
 
-    // ---- Cholesky in wave 0, LDL^T-update form with the unit-lower inverse
-    // carried along: step k subtracts (a_ik / a_kk) times row k from every
-    // row i > k of [A | I].  Then L = L_u D^1/2 and L^-1 = D^-1/2 L_u^-1.
+    // ---- Cholesky in wave 0, right-looking: step k takes f_i = a_ik / a_kk
+    // and subtracts f_i times row k from every row i > k of the trailing
+    // matrix; column k of L is a_ik / sqrt(a_kk).  Row k comes from lane k by
+    // v_readlane.  Columns left of k in `work` are no longer read (L is built
+    // in `lrow`).
     if (wave == 0) {
-        constexpr bool kSplit = SL::kSplit;
-        const int row = kSplit ? (lane & 31) : lane;
-        const bool inverse_lane = kSplit && lane >= 32;
-        const bool live = row < R;
-        LSSO_REG_ROW(work);    // A row (L^-1 row on inverse lanes when split)
-        LSSO_REG_ROW(carry);   // L^-1 row (unsplit only)
-        if (live && !inverse_lane) {
-            row_load(work, s_work + row * LD);
-        }
+        const bool live = lane < R;
+        LSSO_REG_ROW(work);
+        LSSO_REG_ROW(lrow);
         if (live) {
-            if (kSplit) {
-                if (inverse_lane) {
-                    row_identity(work, row);
-                }
-            } else {
-                row_identity(carry, row);
-            }
+            row_load(work, s_work + lane * LD);
         }
         float own_inv_root = 1.0f;
 #pragma unroll 1
         for (int k = 0; k < R; ++k) {
-            float* column = smem + SL::kColumn + (k & 1) * 64;
-            float* step_row = smem + SL::kRow + (k & 1) * R;
             const float x = row_get(work, k);
-            // a_kk straight from lane k; only the column and row k go through LDS.
             const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
-            if (!inverse_lane) {
-                column[row] = row >= k ? x : 0.0f;
-            }
-            if (lane == (kSplit ? 32 + k : k)) {
-                if constexpr (kSplit) {
-                    row_store(step_row, work);
-                } else {
-                    row_store(step_row, carry);
-                }
-            }
-            wave_lds_order();
             // Pivots of A = G/n + I are >= 1, so the hardware reciprocal,
             // square root and reciprocal square root (1 ulp) need no range
             // handling.
             const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
             const float inv_root = __builtin_amdgcn_rsqf(pivot);
             const float root_pivot = __builtin_amdgcn_sqrtf(pivot);
-            const float own = inverse_lane ? column[row] : x;
-            const float f = row > k ? own * inv_pivot : 0.0f;
-            LSSO_REG_ROW(source);
-            row_load(source, kSplit && inverse_lane ? step_row : column);
-            row_axpy(work, f, source);
-            if (!kSplit) {
-                LSSO_REG_ROW(aug);
-                row_load(aug, step_row);
-                row_axpy(carry, f, aug);
-            }
-            if (!inverse_lane) {
-                row_set(work, k, row > k ? x * inv_root : (row == k ? root_pivot : 0.0f));
-            }
-            own_inv_root = row == k ? inv_root : own_inv_root;
+            const float f = lane > k ? x * inv_pivot : 0.0f;
+            row_axpy_lane(work, f, k);
+            row_set(lrow, k, lane > k ? x * inv_root : (lane == k ? root_pivot : 0.0f));
+            own_inv_root = lane == k ? inv_root : own_inv_root;
         }
+        // L and 1 / L_ii to LDS for the substitution (A in s_work is spent).
         if (live) {
-            const RegRow<Q>& inverse = kSplit ? work : carry;
-            if (!kSplit || inverse_lane) {
-                row_scale(inverse, own_inv_root);
-                row_store(s_linv + row * LD, inverse);
-                row_store_column(s_linvt, LD, row, inverse);
-                if (tape != nullptr) {
-                    row_store(tape + 3 * R * R + row * R, inverse);
-                }
+            row_store(s_work + lane * LD, lrow);
+            smem[SL::kColumn + lane] = own_inv_root;
+            if (tape != nullptr) {
+                row_store(tape + lane * R, lrow);
             }
-            if (!inverse_lane && tape != nullptr) {
-                row_store(tape + row * R, work);
+        }
+        wave_lds_order();
+        if (live) {
+            float x[R];
+            lower_inverse_column<R, LD>(s_work, smem + SL::kColumn, lane, x);
+            // Lane c holds column c of L^-1: row c of L^-T and column c of L^-1.
+#pragma unroll
+            for (int i = 0; i < R; i += 4) {
+                *reinterpret_cast<f32x4*>(s_linvt + lane * LD + i) = (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                s_linv[i * LD + lane] = x[i];
             }
         }
     }
     __syncthreads();
+    if (tape != nullptr) {
+        for (int q = tid; q < R * R / 4; q += kSolveThreads) {
+            const int i = (4 * q) / R;
+            const int j = 4 * q - i * R;
+            *reinterpret_cast<f32x4*>(tape + 3 * R * R + 4 * q) = *reinterpret_cast<const f32x4*>(s_linv + i * LD + j);
+        }
+    }
 
     // ---- Z panels (Z = L^-1 S / sqrt(n)) and Theta = Z W accumulation ------
     float* zbuf = a.zbuf + system * R * d;
@@ -640,7 +661,6 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
         float own_pivot = 1.0f;
 #pragma unroll 1
         for (int k = 0; k < R; ++k) {
-            float* step_row = smem + SL::kRow + (k & 1) * R;
             const float x = row_get(rowv, k);
             const unsigned magnitude = __float_as_uint(fabsf(x));
             const unsigned best = __builtin_amdgcn_readfirstlane(__ockl_wfred_max_u32(open ? magnitude : 0u));
@@ -648,8 +668,10 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
             const int p = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(ties)));
             const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), p));
             const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
+            const float f = lane == p ? 0.0f : x * inv_pivot;
+            row_axpy_lane(rowv, f, p);
+            row_set(rowv, k, lane == p ? 1.0f : -f);
             if (lane == p) {
-                row_store(step_row, rowv);
                 open = false;
                 own_step = k;
                 own_pivot = pivot;
@@ -657,12 +679,6 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
             if (lane == 0) {
                 s_pivot[k] = p;
             }
-            wave_lds_order();
-            LSSO_REG_ROW(pivot_row);
-            row_load(pivot_row, step_row);
-            const float f = lane == p ? 0.0f : x * inv_pivot;
-            row_axpy(rowv, f, pivot_row);
-            row_set(rowv, k, lane == p ? 1.0f : -f);
         }
         if (live) {
             row_scale(rowv, __builtin_amdgcn_rcpf(own_pivot));
