@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
 // ---------------------------------------------------------------------------
 // Solve: one 256-thread workgroup per (b, h) system.
 //
-//   A = G / n + I = L L^T            Cholesky
+//   A = G / n + I = L L^T            blocked Cholesky
 //   L^-1                             forward substitution, one column per lane
 //   Z = L^-1 S / sqrt(n)             product
 //   Theta = Theta0 + Z W / sqrt(n)   product
@@ -142,7 +142,8 @@ struct SolveLayout {
     static constexpr int kLD = R + 4;              // R x R matrices (16-byte rows)
     static constexpr int kPLD = kSolvePanel + 4;   // R x panel matrices
     static constexpr int kChunks = R / 16;         // 16-float register chunks per row
-    static constexpr int kThetaQuads = (R * R / 4 + kSolveThreads - 1) / kSolveThreads;
+    static constexpr int kTiles = (R / 16) * (R / 16);     // 16 x 16 tiles of an R x R matrix
+    static constexpr int kTilesPerWave = (kTiles + 3) / 4;
     static constexpr int kChunkBatch = R <= 32 ? 8 : 4;    // chunk loads in flight per element
     static constexpr int kLinv = 0;                       // L^-1 rows
     static constexpr int kLinvT = kLinv + R * kLD;        // L^-1 transposed
@@ -151,8 +152,7 @@ struct SolveLayout {
     static constexpr int kSys = kWork + R * kLD;          // I + K, then (I + K)^-1
     static constexpr int kPanelA = kSys + R * kLD;        // S panel; drive panel; X panel
     static constexpr int kPanelB = kPanelA + R * kPLD;    // Z panel; M' panel
-    static constexpr int kColumn = kPanelB + R * kPLD;    // 1 / L_ii
-    static constexpr int kPivot = kColumn + 64;           // pivot row of each step
+    static constexpr int kPivot = kPanelB + R * kPLD;     // pivot row of each step
     static constexpr int kTotal = kPivot + R;
 };
 
@@ -176,14 +176,6 @@ struct RegRow {
         }
     }
 };
-
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_zero(const RegRow<Q>& r) {
-    if constexpr (q < Q) {
-        r.template at<q>() = 0.0f;
-        row_zero<Q, q + 1>(r);
-    }
-}
 
 // Element k of a register row for a wave-uniform k.
 template <int Q, int q = 0>
@@ -237,53 +229,11 @@ __device__ __forceinline__ void row_store(float* p, const RegRow<Q>& r) {
     }
 }
 
-// r -= f * x
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_axpy(const RegRow<Q>& r, float f, const RegRow<Q>& x) {
-    if constexpr (q < Q) {
-        f32x16 t = r.template at<q>();
-        const f32x16 xt = x.template at<q>();
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            t[e] = fmaf(-f, xt[e], t[e]);
-        }
-        r.template at<q>() = t;
-        row_axpy<Q, q + 1>(r, f, x);
-    }
-}
-
 template <int Q, int q = 0>
 __device__ __forceinline__ void row_scale(const RegRow<Q>& r, float factor) {
     if constexpr (q < Q) {
         r.template at<q>() = r.template at<q>() * factor;
         row_scale<Q, q + 1>(r, factor);
-    }
-}
-
-// Row `row` of the identity (row may differ between lanes).
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_identity(const RegRow<Q>& r, int row) {
-    if constexpr (q < Q) {
-        f32x16 t;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            t[e] = 16 * q + e == row ? 1.0f : 0.0f;
-        }
-        r.template at<q>() = t;
-        row_identity<Q, q + 1>(r, row);
-    }
-}
-
-// Column `column` of an LDS matrix with row stride ld receives the row.
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_store_column(float* p, int ld, int column, const RegRow<Q>& r) {
-    if constexpr (q < Q) {
-        const f32x16 t = r.template at<q>();
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            p[(16 * q + e) * ld + column] = t[e];
-        }
-        row_store_column<Q, q + 1>(p, ld, column, r);
     }
 }
 
@@ -315,27 +265,213 @@ __device__ __forceinline__ void row_axpy_lane(const RegRow<Q>& r, float f, int s
     }
 }
 
-// Column `lane` of L^-1 for lower-triangular L (row-major in LDS, row stride
-// LD) and the reciprocal diagonal: x_i = (delta_i,lane - sum_{m<i} L_im x_m)
-// / L_ii, summed in ascending m.  Rows of L are wave-uniform LDS reads.
-template <int R, int LD>
-__device__ __forceinline__ void lower_inverse_column(const float* l, const float* inv_diag, int lane,
-                                                     float (&x)[R]) {
+// Blocked Cholesky of the SPD matrix in LDS (row stride LD), one row per lane
+// (lanes >= R hold zero rows), 8-column panels.  Per panel:
+//   1. rows c0..c0+7 of the diagonal block go through LDS to every lane, and
+//      every lane factors the 8 x 8 block itself (right-looking, in registers);
+//   2. each lane solves its own panel entries against that factor,
+//      L_i,m = (a_im - sum_{m'<m} L_i,m' L_m,m') / L_mm, in ascending m' (the
+//      order of the block factorization, so the block's own lanes reproduce
+//      it bit for bit; L_mm = p * rsq(p) in both);
+//   3. the panel goes through LDS and each lane applies the rank-8 update
+//      a_ij -= sum_m L_im L_jm to its columns right of the panel.
+// Two LDS round trips per panel instead of one per column.  s_diag holds 64
+// floats, s_panel 8 R, s_inv_diag R (16-byte aligned).  Panels recurse at
+// compile time so every register index is static.  On return l is row `lane`
+// of L (zero above the diagonal) and s_inv_diag[m] = 1 / L_mm.
+template <int R, int LD, int C0>
+__device__ __forceinline__ void cholesky_panel(float* s_diag, float* s_panel, float* s_inv_diag, int lane,
+                                               float (&l)[R]) {
+    if constexpr (C0 < R) {
+        constexpr int B = 8;
+        wave_lds_order();
+        if (lane >= C0 && lane < C0 + B) {
+            *reinterpret_cast<f32x4*>(s_diag + (lane - C0) * B) = (f32x4){l[C0], l[C0 + 1], l[C0 + 2], l[C0 + 3]};
+            *reinterpret_cast<f32x4*>(s_diag + (lane - C0) * B + 4) =
+                (f32x4){l[C0 + 4], l[C0 + 5], l[C0 + 6], l[C0 + 7]};
+        }
+        wave_lds_order();
+        float d[B][B];
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-        float acc = lane == i ? 1.0f : 0.0f;
+        for (int r = 0; r < B; ++r) {
 #pragma unroll
-        for (int m = 0; m < i; m += 4) {
-            const f32x4 l4 = *reinterpret_cast<const f32x4*>(l + i * LD + m);
+            for (int c = 0; c < B; c += 4) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(s_diag + r * B + c);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if (m + e < i) {
-                    acc = fmaf(-l4[e], x[m + e], acc);
+                for (int e = 0; e < 4; ++e) {
+                    d[r][c + e] = v[e];
                 }
             }
         }
-        x[i] = acc * inv_diag[i];
+        // Pivots of A = G/n + I stay >= 1, so rsq needs no range handling.
+        float rs[B];
+#pragma unroll
+        for (int m = 0; m < B; ++m) {
+            const float pivot = d[m][m];
+            rs[m] = __builtin_amdgcn_rsqf(pivot);
+            d[m][m] = pivot * rs[m];
+#pragma unroll
+            for (int r = m + 1; r < B; ++r) {
+                d[r][m] *= rs[m];
+            }
+#pragma unroll
+            for (int r = m + 1; r < B; ++r) {
+#pragma unroll
+                for (int c = m + 1; c <= r; ++c) {
+                    d[r][c] = fmaf(-d[r][m], d[c][m], d[r][c]);
+                }
+            }
+        }
+        float x[B];
+#pragma unroll
+        for (int m = 0; m < B; ++m) {
+            float acc = l[C0 + m];
+#pragma unroll
+            for (int mp = 0; mp < m; ++mp) {
+                acc = fmaf(-x[mp], d[m][mp], acc);
+            }
+            x[m] = acc * rs[m];
+        }
+#pragma unroll
+        for (int m = 0; m < B; ++m) {
+            x[m] = lane < C0 + m ? 0.0f : x[m];
+            l[C0 + m] = x[m];
+        }
+        if (lane == 0) {
+            *reinterpret_cast<f32x4*>(s_inv_diag + C0) = (f32x4){rs[0], rs[1], rs[2], rs[3]};
+            *reinterpret_cast<f32x4*>(s_inv_diag + C0 + 4) = (f32x4){rs[4], rs[5], rs[6], rs[7]};
+        }
+        if constexpr (C0 + B < R) {
+            wave_lds_order();
+            if (lane < R) {
+                *reinterpret_cast<f32x4*>(s_panel + lane * B) = (f32x4){x[0], x[1], x[2], x[3]};
+                *reinterpret_cast<f32x4*>(s_panel + lane * B + 4) = (f32x4){x[4], x[5], x[6], x[7]};
+            }
+            wave_lds_order();
+#pragma unroll
+            for (int j = C0 + B; j < R; ++j) {
+                const f32x4 p0 = *reinterpret_cast<const f32x4*>(s_panel + j * B);
+                const f32x4 p1 = *reinterpret_cast<const f32x4*>(s_panel + j * B + 4);
+                float acc = l[j];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    acc = fmaf(-x[m], p0[m], acc);
+                }
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    acc = fmaf(-x[4 + m], p1[m], acc);
+                }
+                l[j] = acc;
+            }
+        }
+        cholesky_panel<R, LD, C0 + B>(s_diag, s_panel, s_inv_diag, lane, l);
     }
+}
+
+template <int R, int LD>
+__device__ __forceinline__ void blocked_cholesky(const float* s_a, float* s_diag, float* s_panel, float* s_inv_diag,
+                                                 int lane, float (&l)[R]) {
+    const bool live = lane < R;
+    const float* own = s_a + (live ? lane : 0) * LD;
+#pragma unroll
+    for (int j = 0; j < R; j += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(own + j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            l[j + e] = live ? v[e] : 0.0f;
+        }
+    }
+    cholesky_panel<R, LD, 0>(s_diag, s_panel, s_inv_diag, lane, l);
+}
+
+// Column `lane` of L^-1 from L^T (row-major in LDS, row stride LD) and the
+// reciprocal diagonal (LDS), right-looking: x_i = x_i / L_ii, then x_i' -= L_i'i x_i
+// for every i' > i, so each x_i' sums its terms in ascending i.
+template <int R, int LD, int I>
+__device__ __forceinline__ void lower_inverse_step(const float* lt, const float* inv_diag, float (&x)[R]) {
+    if constexpr (I < R) {
+        x[I] *= inv_diag[I];
+#pragma unroll
+        for (int c = (I + 1) & ~3; c < R; c += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(lt + I * LD + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (c + e > I) {
+                    x[c + e] = fmaf(-v[e], x[I], x[c + e]);
+                }
+            }
+        }
+        lower_inverse_step<R, LD, I + 1>(lt, inv_diag, x);
+    }
+}
+
+template <int R, int LD>
+__device__ __forceinline__ void lower_inverse_column(const float* lt, const float* inv_diag, int lane,
+                                                     float (&x)[R]) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        x[i] = lane == i ? 1.0f : 0.0f;
+    }
+    lower_inverse_step<R, LD, 0>(lt, inv_diag, x);
+}
+
+// Rows first, first + step, ... (< R) of columns c0 .. c0 + width of
+// S / sqrt(n), S = the cross-moment partials summed over chunks in ascending
+// order, into an LDS panel (row stride pld), one column per lane; columns
+// past the width store zero.  ROWS >= the rows per caller wave.
+template <int R, int ROWS, int BATCH>
+__device__ __forceinline__ void load_cross_panel(const float* part, int64_t stride, int chunks, int d, int c0,
+                                                 int width, float root, float* panel, int pld, int lane,
+                                                 int first, int step) {
+    const int c = lane < width ? lane : width - 1;
+    float acc[ROWS];
+#pragma unroll
+    for (int t = 0; t < ROWS; ++t) {
+        acc[t] = 0.0f;
+    }
+    const float* src = part + R * R + c0 + c;
+    for (int ch0 = 0; ch0 < chunks; ch0 += BATCH) {
+        float v[ROWS][BATCH];
+#pragma unroll
+        for (int t = 0; t < ROWS; ++t) {
+            const int i = first + step * t;
+            const int row = i < R ? i : first;
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) {
+                const int ch = ch0 + u < chunks ? ch0 + u : chunks - 1;
+                v[t][u] = src[ch * stride + row * d];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < ROWS; ++t) {
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) {
+                if (ch0 + u < chunks) {
+                    acc[t] += v[t][u];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < ROWS; ++t) {
+        const int i = first + step * t;
+        if (i < R) {
+            panel[i * pld + lane] = lane < width ? acc[t] / root : 0.0f;
+        }
+    }
+}
+
+// acc + one 16 x 16 tile of A B on v_mfma_f32_16x16x4_f32, k over [0, k_end)
+// in steps of 4: lane (r, q) = (lane % 16, lane / 16) supplies A[r][k + q]
+// through a(k) and B[k + q][r] through b(k); element m of the result is row
+// 4 q + m, column r of the tile.  Each operand element is read once per
+// tile (a wave-uniform LDS read would return it to all 64 lanes).
+template <typename LoadA, typename LoadB>
+__device__ __forceinline__ f32x4 mfma_tile_f32(f32x4 acc, int k_end, LoadA a, LoadB b) {
+    for (int k = 0; k < k_end; k += 4) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a(k), b(k), acc, 0, 0, 0);
+    }
+    return acc;
 }
 
 template <int R>
@@ -369,6 +505,39 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
     const float eta = bounded_complement(a.eta_raw[h]);
     const float* part = a.partials + system * chunks * stride;
     float* tape = a.tape != nullptr ? a.tape + system * a.tape_stride : nullptr;
+    const int r16 = lane & 15;
+    const int q4 = lane >> 4;
+    const int first_width = d < kSolvePanel ? d : kSolvePanel;
+    const float* drive = a.drive + h * d * R;
+
+    // Theta0 entries of this wave's Theta tiles and the first drive panel
+    // (rows 0 .. 63 of W, zero past d), loaded now so that their latency
+    // overlaps the factorization.
+    f32x4 base_pre[SL::kTilesPerWave];
+#pragma unroll
+    for (int t = 0; t < SL::kTilesPerWave; ++t) {
+        const int tile = wave + 4 * t < SL::kTiles ? wave + 4 * t : 0;
+        const int i0 = 16 * (tile / (R / 16)) + 4 * q4;
+        const int j = 16 * (tile % (R / 16)) + r16;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            base_pre[t][m] = a.base[(h * R + i0 + m) * R + j];
+        }
+    }
+    auto drive_quad = [&](int c0, int width, int e) {
+        const int c = (4 * e) / R;
+        f32x4 w = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (c < width) {
+            w = *reinterpret_cast<const f32x4*>(drive + (c0 + c) * R + (4 * e - c * R));
+        }
+        return w;
+    };
+    constexpr int kDriveQuads = kSolvePanel * R / 4 / kSolveThreads;
+    f32x4 drive_pre[kDriveQuads];
+#pragma unroll
+    for (int u = 0; u < kDriveQuads; ++u) {
+        drive_pre[u] = drive_quad(0, first_width, tid + u * kSolveThreads);
+    }
 
     // ---- A = G / n + I; chunk partials summed in ascending order, each
     // thread keeping kChunkBatch chunks of loads in flight --------------------
@@ -419,46 +588,33 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
     }
     __syncthreads();
 
-    // ---- Cholesky in wave 0, right-looking: step k takes f_i = a_ik / a_kk
-    // and subtracts f_i times row k from every row i > k of the trailing
-    // matrix; column k of L is a_ik / sqrt(a_kk).  Row k comes from lane k by
-    // v_readlane.  Columns left of k in `work` are no longer read (L is built
-    // in `lrow`).
+    // ---- Cholesky (blocked, wave 0), then L^-1 one column per lane; waves
+    // 1-3 meanwhile sum the first S panel ------------------------------------
     if (wave == 0) {
         const bool live = lane < R;
-        LSSO_REG_ROW(work);
-        LSSO_REG_ROW(lrow);
+        float lrow[R];
+        // Theta's LDS is free until the Theta assembly.
+        float* s_inv_diag = s_theta + 64 + 8 * R;
+        blocked_cholesky<R, LD>(s_work, s_theta, s_theta + 64, s_inv_diag, lane, lrow);
+        // L^T to LDS for the substitution (A in s_work is spent).
+        wave_lds_order();
         if (live) {
-            row_load(work, s_work + lane * LD);
-        }
-        float own_inv_root = 1.0f;
-#pragma unroll 1
-        for (int k = 0; k < R; ++k) {
-            const float x = row_get(work, k);
-            const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
-            // Pivots of A = G/n + I are >= 1, so the hardware reciprocal,
-            // square root and reciprocal square root (1 ulp) need no range
-            // handling.
-            const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
-            const float inv_root = __builtin_amdgcn_rsqf(pivot);
-            const float root_pivot = __builtin_amdgcn_sqrtf(pivot);
-            const float f = lane > k ? x * inv_pivot : 0.0f;
-            row_axpy_lane(work, f, k);
-            row_set(lrow, k, lane > k ? x * inv_root : (lane == k ? root_pivot : 0.0f));
-            own_inv_root = lane == k ? inv_root : own_inv_root;
-        }
-        // L and 1 / L_ii to LDS for the substitution (A in s_work is spent).
-        if (live) {
-            row_store(s_work + lane * LD, lrow);
-            smem[SL::kColumn + lane] = own_inv_root;
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                s_work[j * LD + lane] = lrow[j];
+            }
             if (tape != nullptr) {
-                row_store(tape + lane * R, lrow);
+#pragma unroll
+                for (int j = 0; j < R; j += 4) {
+                    *reinterpret_cast<f32x4*>(tape + lane * R + j) =
+                        (f32x4){lrow[j], lrow[j + 1], lrow[j + 2], lrow[j + 3]};
+                }
             }
         }
         wave_lds_order();
+        float x[R];
+        lower_inverse_column<R, LD>(s_work, s_inv_diag, lane, x);
         if (live) {
-            float x[R];
-            lower_inverse_column<R, LD>(s_work, smem + SL::kColumn, lane, x);
             // Lane c holds column c of L^-1: row c of L^-T and column c of L^-1.
 #pragma unroll
             for (int i = 0; i < R; i += 4) {
@@ -469,6 +625,9 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
                 s_linv[i * LD + lane] = x[i];
             }
         }
+    } else {
+        load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root, s_pa,
+                                                          PLD, lane, wave - 1, 3);
     }
     __syncthreads();
     if (tape != nullptr) {
@@ -479,102 +638,60 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
         }
     }
 
-    // ---- Z panels (Z = L^-1 S / sqrt(n)) and Theta = Z W accumulation ------
+    // ---- Z panels (Z = L^-1 S / sqrt(n)) and Theta = Z W accumulation, on
+    // FP32 MFMA 16 x 16 tiles; wave w takes tiles w, w + 4, ... --------------
     float* zbuf = a.zbuf + system * R * d;
-    const float* drive = a.drive + h * d * R;
-    f32x4 theta_acc[SL::kThetaQuads];
+    f32x4 theta_acc[SL::kTilesPerWave];
 #pragma unroll
-    for (int t = 0; t < SL::kThetaQuads; ++t) {
+    for (int t = 0; t < SL::kTilesPerWave; ++t) {
         theta_acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     }
     for (int c0 = 0; c0 < d; c0 += kSolvePanel) {
         const int width = d - c0 < kSolvePanel ? d - c0 : kSolvePanel;
-        {
-            // S panel: thread (row wave + 4 t, column lane); columns past the
-            // panel width load a clamped column and store zero.
-            constexpr int kRows = R / 4;
-            const int c = lane < width ? lane : width - 1;
-            float acc[kRows];
-#pragma unroll
-            for (int t = 0; t < kRows; ++t) {
-                acc[t] = 0.0f;
-            }
-            const float* src = part + R * R + wave * d + c0 + c;
-            for (int ch0 = 0; ch0 < chunks; ch0 += SL::kChunkBatch) {
-                float v[kRows][SL::kChunkBatch];
-#pragma unroll
-                for (int t = 0; t < kRows; ++t) {
-#pragma unroll
-                    for (int u = 0; u < SL::kChunkBatch; ++u) {
-                        const int ch = ch0 + u < chunks ? ch0 + u : chunks - 1;
-                        v[t][u] = src[ch * stride + 4 * t * d];
-                    }
-                }
-#pragma unroll
-                for (int t = 0; t < kRows; ++t) {
-#pragma unroll
-                    for (int u = 0; u < SL::kChunkBatch; ++u) {
-                        if (ch0 + u < chunks) {
-                            acc[t] += v[t][u];
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < kRows; ++t) {
-                s_pa[(wave + 4 * t) * PLD + lane] = lane < width ? acc[t] / root : 0.0f;
-            }
+        const int ncols = (width + 15) / 16;   // column tiles; S is zero past the width
+        if (c0 > 0) {
+            load_cross_panel<R, R / 4, SL::kChunkBatch>(part, stride, chunks, d, c0, width, root, s_pa, PLD, lane,
+                                                        wave, 4);
+            __syncthreads();
         }
-        __syncthreads();
-        {
-            float scol[R];
+        for (int tile = wave; tile < (R / 16) * ncols; tile += 4) {
+            const int i0 = 16 * (tile / ncols);
+            const int j0 = 16 * (tile - (tile / ncols) * ncols);
+            const f32x4 z = mfma_tile_f32(
+                (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, R, [&](int k) { return s_linv[(i0 + r16) * LD + k + q4]; },
+                [&](int k) { return s_pa[(k + q4) * PLD + j0 + r16]; });
+            const int c = j0 + r16;
 #pragma unroll
-            for (int k = 0; k < R; ++k) {
-                scol[k] = s_pa[k * PLD + lane];
-            }
-#pragma unroll 1
-            for (int i = wave; i < R; i += 4) {
-                const float* lrow = s_linv + i * LD;
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < R; k += 4) {
-                    const f32x4 l4 = *reinterpret_cast<const f32x4*>(lrow + k);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        acc = fmaf(l4[e], scol[k + e], acc);
+            for (int m = 0; m < 4; ++m) {
+                const int i = i0 + 4 * q4 + m;
+                s_pb[i * PLD + c] = z[m];
+                if (c < width) {
+                    if (d > kSolvePanel) {
+                        zbuf[i * d + c0 + c] = z[m];
                     }
-                }
-                s_pb[i * PLD + lane] = acc;
-                if (lane < width) {
-                    zbuf[i * d + c0 + lane] = acc;
                     if (tape != nullptr) {
-                        tape[4 * R * R + i * d + c0 + lane] = acc;
+                        tape[4 * R * R + i * d + c0 + c] = z[m];
                     }
                 }
             }
         }
         __syncthreads();
-        for (int e = tid; e < kSolvePanel * R / 4; e += kSolveThreads) {
-            const int c = (4 * e) / R;
-            f32x4 w = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (c < width) {
-                w = *reinterpret_cast<const f32x4*>(drive + (c0 + c) * R + (4 * e - c * R));
-            }
-            *reinterpret_cast<f32x4*>(s_pa + 4 * e) = w;
+        // Drive rows c0 .. c0 + 63 (zero past the width), row stride R.
+#pragma unroll
+        for (int u = 0; u < kDriveQuads; ++u) {
+            const int e = tid + u * kSolveThreads;
+            *reinterpret_cast<f32x4*>(s_pa + 4 * e) = c0 == 0 ? drive_pre[u] : drive_quad(c0, width, e);
         }
         __syncthreads();
 #pragma unroll
-        for (int t = 0; t < SL::kThetaQuads; ++t) {
-            const int q = tid + t * kSolveThreads;
-            if (q < R * R / 4) {
-                const int i = q / (R / 4);
-                const int j = 4 * (q - i * (R / 4));
-#pragma unroll 8
-                for (int c = 0; c < width; ++c) {
-                    const float z = s_pb[i * PLD + c];
-                    const f32x4 w = *reinterpret_cast<const f32x4*>(s_pa + c * R + j);
-                    theta_acc[t] = z * w + theta_acc[t];
-                }
+        for (int t = 0; t < SL::kTilesPerWave; ++t) {
+            const int tile = wave + 4 * t;
+            if (tile < SL::kTiles) {
+                const int i0 = 16 * (tile / (R / 16));
+                const int j0 = 16 * (tile % (R / 16));
+                theta_acc[t] = mfma_tile_f32(
+                    theta_acc[t], 16 * ncols, [&](int k) { return s_pb[(i0 + r16) * PLD + k + q4]; },
+                    [&](int k) { return s_pa[(k + q4) * R + j0 + r16]; });
             }
         }
         __syncthreads();
@@ -582,64 +699,55 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
 
     // ---- Theta = Theta0 + acc / sqrt(n); F = tril(Theta, -1) + diag(softplus)
 #pragma unroll
-    for (int t = 0; t < SL::kThetaQuads; ++t) {
-        const int q = tid + t * kSolveThreads;
-        if (q < R * R / 4) {
-            const int i = q / (R / 4);
-            const int j = 4 * (q - i * (R / 4));
-            const f32x4 base = *reinterpret_cast<const f32x4*>(a.base + (h * R + i) * R + j);
-            const f32x4 theta = base + theta_acc[t] / root;
-            *reinterpret_cast<f32x4*>(s_theta + i * LD + j) = theta;
-            if (tape != nullptr) {
-                *reinterpret_cast<f32x4*>(tape + R * R + i * R + j) = theta;
-            }
-            f32x4 factor;
+    for (int t = 0; t < SL::kTilesPerWave; ++t) {
+        const int tile = wave + 4 * t;
+        if (tile < SL::kTiles) {
+            const int i0 = 16 * (tile / (R / 16));
+            const int j = 16 * (tile % (R / 16)) + r16;
+            float diagonal = 0.0f;
+            float theta[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                factor[e] = j + e < i ? theta[e] : 0.0f;
+            for (int m = 0; m < 4; ++m) {
+                const int i = i0 + 4 * q4 + m;
+                theta[m] = base_pre[t][m] + theta_acc[t][m] / root;
+                s_theta[i * LD + j] = theta[m];
+                if (tape != nullptr) {
+                    tape[R * R + i * R + j] = theta[m];
+                }
+                diagonal = j == i ? theta[m] : diagonal;
             }
-            if (j <= i && i < j + 4) {
-                factor[i - j] = softplus_one(theta[i - j]);
+            // At most one of a lane's four elements is on the diagonal: one
+            // softplus per lane, and none in off-diagonal tiles.
+            if (i0 == 16 * (tile % (R / 16))) {
+                diagonal = softplus_one(diagonal);
             }
-            *reinterpret_cast<f32x4*>(s_work + i * LD + j) = factor;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int i = i0 + 4 * q4 + m;
+                s_work[i * LD + j] = j < i ? theta[m] : (j == i ? diagonal : 0.0f);
+            }
         }
     }
     __syncthreads();
 
-    // ---- I + K = I + F F^T + Omega, IEEE FP32 products (reference.py:491-497);
-    // all R products summed (F is lower triangular, the rest add exact zeros).
+    // ---- I + K = I + F F^T + Omega in FP32 (reference.py:491-497); all R
+    // products summed (F is lower triangular, the rest add exact zeros).
 #pragma unroll
-    for (int t = 0; t < SL::kThetaQuads; ++t) {
-        const int q = tid + t * kSolveThreads;
-        if (q < R * R / 4) {
-            const int i = q / (R / 4);
-            const int j = 4 * (q - i * (R / 4));
-            f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-            for (int k = 0; k < R; k += 4) {
-                const f32x4 fi = *reinterpret_cast<const f32x4*>(s_work + i * LD + k);
+    for (int t = 0; t < SL::kTilesPerWave; ++t) {
+        const int tile = wave + 4 * t;
+        if (tile < SL::kTiles) {
+            const int i0 = 16 * (tile / (R / 16));
+            const int j0 = 16 * (tile % (R / 16));
+            const f32x4 sum = mfma_tile_f32(
+                (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, R, [&](int k) { return s_work[(i0 + r16) * LD + k + q4]; },
+                [&](int k) { return s_work[(j0 + r16) * LD + k + q4]; });
+            const int c = j0 + r16;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const f32x4 fj = *reinterpret_cast<const f32x4*>(s_work + (j + e) * LD + k);
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        sum[e] = fmaf(fi[m], fj[m], sum[e]);
-                    }
-                }
+            for (int m = 0; m < 4; ++m) {
+                const int i = i0 + 4 * q4 + m;
+                const float skew = c > i ? s_theta[i * LD + c] : (c < i ? -s_theta[c * LD + i] : 0.0f);
+                s_sys[i * LD + c] = sum[m] + skew + (c == i ? 1.0f : 0.0f);
             }
-            f32x4 value;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int c = j + e;
-                float skew = 0.0f;
-                if (c > i) {
-                    skew = s_theta[i * LD + c];
-                } else if (c < i) {
-                    skew = -s_theta[c * LD + i];
-                }
-                value[e] = sum[e] + skew + (c == i ? 1.0f : 0.0f);
-            }
-            *reinterpret_cast<f32x4*>(s_sys + i * LD + j) = value;
         }
     }
     __syncthreads();
@@ -713,50 +821,34 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
             }
             __syncthreads();
         }
-        {
-            float zcol[R];
+        const int ncols = (width + 15) / 16;
+        for (int tile = wave; tile < (R / 16) * ncols; tile += 4) {
+            const int i0 = 16 * (tile / ncols);
+            const int j0 = 16 * (tile - (tile / ncols) * ncols);
+            const f32x4 u = mfma_tile_f32(
+                (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, R, [&](int k) { return s_sys[(i0 + r16) * LD + k + q4]; },
+                [&](int k) { return s_pb[(k + q4) * PLD + j0 + r16]; });
+            const int c = j0 + r16;
 #pragma unroll
-            for (int k = 0; k < R; ++k) {
-                zcol[k] = s_pb[k * PLD + lane];
-            }
-#pragma unroll 1
-            for (int i = wave; i < R; i += 4) {
-                const float* irow = s_sys + i * LD;
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < R; k += 4) {
-                    const f32x4 v4 = *reinterpret_cast<const f32x4*>(irow + k);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        acc = fmaf(v4[e], zcol[k + e], acc);
-                    }
+            for (int m = 0; m < 4; ++m) {
+                const int i = i0 + 4 * q4 + m;
+                if (tape != nullptr && c < width) {
+                    tape[4 * R * R + R * d + i * d + c0 + c] = u[m];
                 }
-                if (tape != nullptr && lane < width) {
-                    tape[4 * R * R + R * d + i * d + c0 + lane] = acc;
-                }
-                s_pa[i * PLD + lane] = 2.0f * acc - (1.0f + eta) * s_pb[i * PLD + lane];
+                s_pa[i * PLD + c] = 2.0f * u[m] - (1.0f + eta) * s_pb[i * PLD + c];
             }
         }
         __syncthreads();
-        {
-            float xcol[R];
+        for (int tile = wave; tile < (R / 16) * ncols; tile += 4) {
+            const int i0 = 16 * (tile / ncols);
+            const int j0 = 16 * (tile - (tile / ncols) * ncols);
+            const f32x4 m_acc = mfma_tile_f32(
+                (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, R, [&](int k) { return s_linvt[(i0 + r16) * LD + k + q4]; },
+                [&](int k) { return s_pa[(k + q4) * PLD + j0 + r16]; });
+            const int c = j0 + r16;
 #pragma unroll
-            for (int k = 0; k < R; ++k) {
-                xcol[k] = s_pa[k * PLD + lane];
-            }
-#pragma unroll 1
-            for (int i = wave; i < R; i += 4) {
-                const float* trow = s_linvt + i * LD;
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < R; k += 4) {
-                    const f32x4 v4 = *reinterpret_cast<const f32x4*>(trow + k);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        acc = fmaf(v4[e], xcol[k + e], acc);
-                    }
-                }
-                s_pb[i * PLD + lane] = lane < width ? acc / root : 0.0f;
+            for (int m = 0; m < 4; ++m) {
+                s_pb[(i0 + 4 * q4 + m) * PLD + c] = c < width ? m_acc[m] / root : 0.0f;
             }
         }
         __syncthreads();
