@@ -214,11 +214,16 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
             ? 2u * static_cast<uint32_t>(store_row * static_cast<int>(a.width) + store_col) : kOutOfRange;
         const uint32_t store_step = 2u * static_cast<uint32_t>(kPieceRows * a.width);
         const int store_lds = store_row * YP + store_c8;
-        auto store_piece = [&](const BufferRsrc& obuf, const uint16_t* yprev, int i) {
+        auto read_piece = [&](const uint16_t* yprev, int i) {
             const u32x2 lo = *reinterpret_cast<const u32x2*>(&yprev[store_lds + i * kPieceRows * YP]);
             const u32x2 hi = *reinterpret_cast<const u32x2*>(&yprev[store_lds + i * kPieceRows * YP + 4]);
-            const u32x4 v = {lo.x, lo.y, hi.x, hi.y};
+            return (u32x4){lo.x, lo.y, hi.x, hi.y};
+        };
+        auto write_piece = [&](const BufferRsrc& obuf, const u32x4& v, int i) {
             buffer_store16(v, obuf, store_base + static_cast<uint32_t>(i) * store_step);
+        };
+        auto store_piece = [&](const BufferRsrc& obuf, const uint16_t* yprev, int i) {
+            write_piece(obuf, read_piece(yprev, i), i);
         };
         auto store_buffer = [&](const Cursor& prev) {
             return make_buffer(a.packed + (a.packed != nullptr ? tile_row0(prev) * a.width : 0),
@@ -242,6 +247,23 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
                 const int row_k = lane_o & 31;
                 const int half_k = lane_o >> 5;
                 const uint16_t* xrow = xt + (mb * 32 + row_k) * KP + 8 * half_k;
+                // Everything this half reads from LDS besides the x fragments
+                // is issued before its MFMAs, so no read waits inside the
+                // loop: the epilogue's bias and row flag, and each packed
+                // piece one store interval before its store.
+                const int mr = mb * 32 + row_k;
+                const bool keep = all_keep || s_keep[k2][mr] != 0;
+                f32x4 bias[2][4];
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                    for (int qd = 0; qd < 4; ++qd) {
+                        bias[nb][qd] = *reinterpret_cast<const f32x4*>(&s_bias[wave * 64 + nb * 32 + 8 * qd + 4 * half_k]);
+                    }
+                }
+                constexpr int kHalfStores = kProjStores / 2;
+                constexpr int kEvery = KSTEPS / kHalfStores;
+                u32x4 piece = read_piece(yprev, mb * kHalfStores);
                 f32x16 acc[2];
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
@@ -250,36 +272,42 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
                         acc[nb][i] = 0.0f;
                     }
                 }
-                u32x4 xf[2];
-                xf[0] = *reinterpret_cast<const u32x4*>(xrow);
+                // x fragments kXAhead K steps ahead of their MFMAs.
+                constexpr int kXAhead = 3;
+                u32x4 xf[kXAhead + 1];
+#pragma unroll
+                for (int ks = 0; ks < kXAhead; ++ks) {
+                    xf[ks] = *reinterpret_cast<const u32x4*>(xrow + 16 * ks);
+                }
 #pragma unroll
                 for (int ks = 0; ks < KSTEPS; ++ks) {
-                    if (ks + 1 < KSTEPS) {
-                        xf[(ks + 1) & 1] = *reinterpret_cast<const u32x4*>(xrow + 16 * (ks + 1));
+                    if (ks + kXAhead < KSTEPS) {
+                        xf[(ks + kXAhead) % (kXAhead + 1)] =
+                            *reinterpret_cast<const u32x4*>(xrow + 16 * (ks + kXAhead));
                     }
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb) {
-                        acc[nb] = mfma32x32x16(wreg[nb][ks], xf[ks & 1], acc[nb]);
+                        acc[nb] = mfma32x32x16(wreg[nb][ks], xf[ks % (kXAhead + 1)], acc[nb]);
                     }
-                    constexpr int kEvery = KSTEPS / (kProjStores / 2);
                     if (ks % kEvery == kEvery - 1) {
-                        store_piece(obuf, yprev, mb * (kProjStores / 2) + ks / kEvery);
+                        const int i = mb * kHalfStores + ks / kEvery;
+                        write_piece(obuf, piece, i);
+                        if (ks / kEvery + 1 < kHalfStores) {
+                            piece = read_piece(yprev, i + 1);
+                        }
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 // Bias, row mask and BF16 rounding into the packed tile.
-                const int mr = mb * 32 + row_k;
-                const bool keep = all_keep || s_keep[k2][mr] != 0;
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
                     for (int qd = 0; qd < 4; ++qd) {
                         const int c = wave * 64 + nb * 32 + 8 * qd + 4 * half_k;
-                        const f32x4 bias = *reinterpret_cast<const f32x4*>(&s_bias[c]);
-                        const float v0 = keep ? acc[nb][4 * qd + 0] + bias[0] : 0.0f;
-                        const float v1 = keep ? acc[nb][4 * qd + 1] + bias[1] : 0.0f;
-                        const float v2 = keep ? acc[nb][4 * qd + 2] + bias[2] : 0.0f;
-                        const float v3 = keep ? acc[nb][4 * qd + 3] + bias[3] : 0.0f;
+                        const float v0 = keep ? acc[nb][4 * qd + 0] + bias[nb][qd][0] : 0.0f;
+                        const float v1 = keep ? acc[nb][4 * qd + 1] + bias[nb][qd][1] : 0.0f;
+                        const float v2 = keep ? acc[nb][4 * qd + 2] + bias[nb][qd][2] : 0.0f;
+                        const float v3 = keep ? acc[nb][4 * qd + 3] + bias[nb][qd][3] : 0.0f;
                         u32x2 packed;
                         packed.x = pack_bf16(v0, v1);
                         packed.y = pack_bf16(v2, v3);
@@ -491,14 +519,29 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
             const uint16_t* yt = s_y[k2 ^ 1];
             const uint32_t* pt = s_ph[k3 == 0 ? 2 : k3 - 1];
             if (unit_active) {
-                // One half at a time: the operands of one 32-token half are
-                // live at once.
+                if constexpr (R <= 32) {
+                    // Both halves' operands are read before either is
+                    // reduced, so the second half's LDS reads are in flight
+                    // during the first half's math (rows past a partial tile
+                    // read stale LDS and are not reduced).
+                    ReduceTile<R, CPW> t0;
+                    ReduceTile<R, CPW> t1;
+                    lds_tile(t0, yt, pt, 0);
+                    lds_tile(t1, yt, pt, 1);
+                    reduce_compute<R, CPW>(t0, true, acc_g, acc_s);
+                    if (prev.t0 + 32 < prev.end) {
+                        reduce_compute<R, CPW>(t1, true, acc_g, acc_s);
+                    }
+                } else {
+                    // One half at a time: the operands of one 32-token half
+                    // are live at once.
 #pragma unroll 1
-                for (int st = 0; st < 2; ++st) {
-                    if (prev.t0 + 32 * st < prev.end) {
-                        ReduceTile<R, CPW> t;
-                        lds_tile(t, yt, pt, st);
-                        reduce_compute<R, CPW>(t, true, acc_g, acc_s);
+                    for (int st = 0; st < 2; ++st) {
+                        if (prev.t0 + 32 * st < prev.end) {
+                            ReduceTile<R, CPW> t;
+                            lds_tile(t, yt, pt, st);
+                            reduce_compute<R, CPW>(t, true, acc_g, acc_s);
+                        }
                     }
                 }
             }
