@@ -475,7 +475,9 @@ __device__ __forceinline__ f32x4 mfma_tile_f32(f32x4 acc, int k_end, LoadA a, Lo
 }
 
 template <int R>
-__global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
+// Two workgroups per CU (512 systems on 256 CUs in one round): the register
+// budget is held to 256 per lane, which costs rank 48 a few spills.
+__global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     using SL = SolveLayout<R>;
     using AL = ApplyLayout<R>;
     constexpr int Q = SL::kChunks;
@@ -511,17 +513,27 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
     const float* drive = a.drive + h * d * R;
 
     // Theta0 entries of this wave's Theta tiles and the first drive panel
-    // (rows 0 .. 63 of W, zero past d), loaded now so that their latency
-    // overlaps the factorization.
-    f32x4 base_pre[SL::kTilesPerWave];
-#pragma unroll
-    for (int t = 0; t < SL::kTilesPerWave; ++t) {
+    // (rows 0 .. 63 of W, zero past d).  Up to rank 32 they are loaded now,
+    // so that their latency overlaps the factorization; at larger ranks the
+    // registers they would hold through it cost occupancy, and they are
+    // loaded where they are used.
+    constexpr bool kPrefetch = R <= 32;
+    auto base_tile = [&](int t) {
         const int tile = wave + 4 * t < SL::kTiles ? wave + 4 * t : 0;
         const int i0 = 16 * (tile / (R / 16)) + 4 * q4;
         const int j = 16 * (tile % (R / 16)) + r16;
+        f32x4 v;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            base_pre[t][m] = a.base[(h * R + i0 + m) * R + j];
+            v[m] = a.base[(h * R + i0 + m) * R + j];
+        }
+        return v;
+    };
+    f32x4 base_pre[SL::kTilesPerWave];
+    if constexpr (kPrefetch) {
+#pragma unroll
+        for (int t = 0; t < SL::kTilesPerWave; ++t) {
+            base_pre[t] = base_tile(t);
         }
     }
     auto drive_quad = [&](int c0, int width, int e) {
@@ -534,9 +546,11 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
     };
     constexpr int kDriveQuads = kSolvePanel * R / 4 / kSolveThreads;
     f32x4 drive_pre[kDriveQuads];
+    if constexpr (kPrefetch) {
 #pragma unroll
-    for (int u = 0; u < kDriveQuads; ++u) {
-        drive_pre[u] = drive_quad(0, first_width, tid + u * kSolveThreads);
+        for (int u = 0; u < kDriveQuads; ++u) {
+            drive_pre[u] = drive_quad(0, first_width, tid + u * kSolveThreads);
+        }
     }
 
     // ---- A = G / n + I; chunk partials summed in ascending order, each
@@ -680,7 +694,7 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
 #pragma unroll
         for (int u = 0; u < kDriveQuads; ++u) {
             const int e = tid + u * kSolveThreads;
-            *reinterpret_cast<f32x4*>(s_pa + 4 * e) = c0 == 0 ? drive_pre[u] : drive_quad(c0, width, e);
+            *reinterpret_cast<f32x4*>(s_pa + 4 * e) = kPrefetch && c0 == 0 ? drive_pre[u] : drive_quad(c0, width, e);
         }
         __syncthreads();
 #pragma unroll
@@ -704,6 +718,9 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(SolveArgs a) {
         if (tile < SL::kTiles) {
             const int i0 = 16 * (tile / (R / 16));
             const int j = 16 * (tile % (R / 16)) + r16;
+            if constexpr (!kPrefetch) {
+                base_pre[t] = base_tile(t);
+            }
             float diagonal = 0.0f;
             float theta[4];
 #pragma unroll
