@@ -85,26 +85,61 @@ __device__ __forceinline__ void write_records(uint16_t* out, int rows, int cols,
     }
 }
 
-// C[i][j] = sum_k A(i, k) B(k, j) over an M x N output, all threads.
-template <typename FA, typename FB, typename Store>
+// C[i][j] = sum_k A(i, k) B(k, j) over an M x N output on FP32 MFMA
+// (v_mfma_f32_16x16x4_f32, 16 x 16 tiles, wave w of the workgroup takes
+// tiles w, w + 4, ...): lane (r, q) = (lane % 16, lane / 16) supplies
+// A(i0 + r, k + q) and B(k + q, j0 + r) per step of 4 and holds rows
+// i0 + 4 q .. + 3 of column j0 + r of the tile.  Each operand element is
+// read once per tile; a per-element dot product would read every A row and
+// B column once per output and is bound by the LDS return path.  Elements
+// past M, N or K read as zero.  K <= KMAX; the K loop is unrolled to KMAX
+// so that a tile's operand reads are all issued before its MFMAs.
+template <int KMAX, typename FA, typename FB, typename Store>
 __device__ __forceinline__ void block_product(int M, int N, int K, FA a, FB b, Store store) {
-    for (int idx = threadIdx.x; idx < M * N; idx += blockDim.x) {
-        const int i = idx / N;
-        const int j = idx - i * N;
-        float acc = 0.0f;
-        for (int k = 0; k < K; ++k) {
-            acc = fmaf(a(i, k), b(k, j), acc);
+    const int wave = threadIdx.x >> 6;
+    const int waves = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    const int ncols = (N + 15) / 16;
+    const int tiles = ((M + 15) / 16) * ncols;
+    for (int tile = wave; tile < tiles; tile += waves) {
+        const int i0 = 16 * (tile / ncols);
+        const int j0 = 16 * (tile - (tile / ncols) * ncols);
+        const int i = i0 + r;
+        const int j = j0 + r;
+        float av[KMAX / 4];
+        float bv[KMAX / 4];
+#pragma unroll
+        for (int s = 0; s < KMAX / 4; ++s) {
+            const int kk = 4 * s + q;
+            av[s] = (i < M && kk < K) ? a(i, kk) : 0.0f;
+            bv[s] = (j < N && kk < K) ? b(kk, j) : 0.0f;
         }
-        store(i, j, acc);
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KMAX / 4; ++s) {
+            if (4 * s < K) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = i0 + 4 * q + m;
+            if (row < M && j < N) {
+                store(row, j, acc[m]);
+            }
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Compact backward of one system.
-template <int R>
+// Compact backward of one system.  DMAX: the bound of head_dim (32 or 64)
+// that sizes the d-length products.
+template <int R, int DMAX>
 __global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) {
     constexpr int PR = R + 1;                         // r x r pitch
-    constexpr int PD = kBwdMaxHeadDim + 1;            // r x d pitch
+    constexpr int PD = DMAX + 1;                      // r x d pitch (two workgroups per CU at d <= 32)
     __shared__ float s_linv[R * PR];
     __shared__ float s_k[R * PR];    // (I+K)^-1 -> dK -> L -> Mbar
     __shared__ float s_f[R * PR];    // Theta -> F -> Lbar -> P Linv
@@ -129,60 +164,99 @@ __global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) 
     const float* part = a.partials + system * a.chunks * a.partial_stride + R * R;
     const float* drive = a.drive + h * d * R;
 
-    // ---- loads ------------------------------------------------------------
-    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
-        const int i = idx / R;
-        const int j = idx - i * R;
-        s_linv[i * PR + j] = tape[3 * R * R + idx];
-        s_k[i * PR + j] = tape[2 * R * R + idx];
-        s_f[i * PR + j] = tape[R * R + idx];
-    }
-    for (int idx = tid; idx < R * d; idx += kBwdThreads) {
-        const int i = idx / d;
-        const int f = idx - i * d;
-        const float z = tape[4 * R * R + idx];
-        const float u = tape[4 * R * R + R * d + idx];
-        s_z[i * PD + f] = z;
-        s_u[i * PD + f] = u;
-        s_x[i * PD + f] = 2.0f * u - (1.0f + eta) * z;
-        float dm = 0.0f;
-        for (int ch = 0; ch < a.chunks; ++ch) {
-            dm += part[ch * a.partial_stride + idx];
+    // ---- loads: every load of a thread is issued before its first LDS store
+    // (the loads are latency-bound; a rolled loop would wait for each); L is
+    // held in registers until its phase.
+    constexpr int kSquare = (R * R + kBwdThreads - 1) / kBwdThreads;
+    float l_pre[kSquare];
+    {
+        float linv[kSquare];
+        float inv[kSquare];
+        float theta[kSquare];
+#pragma unroll
+        for (int t = 0; t < kSquare; ++t) {
+            const int idx = tid + t * kBwdThreads < R * R ? tid + t * kBwdThreads : 0;
+            linv[t] = tape[3 * R * R + idx];
+            inv[t] = tape[2 * R * R + idx];
+            theta[t] = tape[R * R + idx];
+            l_pre[t] = tape[idx];
         }
-        s_v[i * PD + f] = dm / root;
+        constexpr int kRect = (R * kBwdMaxHeadDim + kBwdThreads - 1) / kBwdThreads;
+        float zv[kRect];
+        float uv[kRect];
+        float dmv[kRect];
+#pragma unroll
+        for (int t = 0; t < kRect; ++t) {
+            const int idx = tid + t * kBwdThreads < R * d ? tid + t * kBwdThreads : 0;
+            zv[t] = tape[4 * R * R + idx];
+            uv[t] = tape[4 * R * R + R * d + idx];
+            dmv[t] = 0.0f;
+        }
+        for (int ch = 0; ch < a.chunks; ++ch) {
+#pragma unroll
+            for (int t = 0; t < kRect; ++t) {
+                const int idx = tid + t * kBwdThreads < R * d ? tid + t * kBwdThreads : 0;
+                dmv[t] += part[ch * a.partial_stride + idx];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kSquare; ++t) {
+            const int idx = tid + t * kBwdThreads;
+            if (idx < R * R) {
+                const int i = idx / R;
+                const int j = idx - i * R;
+                s_linv[i * PR + j] = linv[t];
+                s_k[i * PR + j] = inv[t];
+                s_f[i * PR + j] = theta[t];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kRect; ++t) {
+            const int idx = tid + t * kBwdThreads;
+            if (idx < R * d) {
+                const int i = idx / d;
+                const int f = idx - i * d;
+                s_z[i * PD + f] = zv[t];
+                s_u[i * PD + f] = uv[t];
+                s_x[i * PD + f] = 2.0f * uv[t] - (1.0f + eta) * zv[t];
+                s_v[i * PD + f] = dmv[t] / root;
+            }
+        }
     }
     __syncthreads();
 
     // ---- m = L^-T x;  dx = L^-1 dm ------------------------------------------
-    block_product(R, d, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+    block_product<R>(R, d, R, [&](int i, int k) { return s_linv[k * PR + i]; },
                   [&](int k, int j) { return s_x[k * PD + j]; },
                   [&](int i, int j, float v) { s_m[i * PD + j] = v; });
     __syncthreads();
-    block_product(R, d, R, [&](int i, int k) { return s_linv[i * PR + k]; },
+    block_product<R>(R, d, R, [&](int i, int k) { return s_linv[i * PR + k]; },
                   [&](int k, int j) { return s_v[k * PD + j]; },
                   [&](int i, int j, float v) { s_x[i * PD + j] = v; });
     __syncthreads();
     // ---- v = (I + K)^-T (2 dx) ----------------------------------------------
-    block_product(R, d, R, [&](int i, int k) { return s_k[k * PR + i]; },
+    block_product<R>(R, d, R, [&](int i, int k) { return s_k[k * PR + i]; },
                   [&](int k, int j) { return 2.0f * s_x[k * PD + j]; },
                   [&](int i, int j, float v) { s_v[i * PD + j] = v; });
     __syncthreads();
     // ---- dK = -v u^T;  F and diag(Theta) -------------------------------------
-    block_product(R, R, d, [&](int i, int k) { return s_v[i * PD + k]; },
+    block_product<DMAX>(R, R, d, [&](int i, int k) { return s_v[i * PD + k]; },
                   [&](int k, int j) { return s_u[j * PD + k]; },
                   [&](int i, int j, float v) { s_k[i * PR + j] = -v; });
     for (int idx = tid; idx < R * R; idx += kBwdThreads) {
         const int i = idx / R;
         const int j = idx - i * R;
         const float theta = s_f[i * PR + j];
+        float value = j < i ? theta : 0.0f;
         if (i == j) {
             s_diag[i] = theta;
+            value = softplus_one(theta);
         }
-        s_f[i * PR + j] = j < i ? theta : (j == i ? softplus_one(theta) : 0.0f);
+        s_f[i * PR + j] = value;
     }
     __syncthreads();
     // ---- dF = (dK + dK^T) F;  dTheta -----------------------------------------
-    block_product(R, R, R, [&](int i, int k) { return s_k[i * PR + k] + s_k[k * PR + i]; },
+    block_product<R>(R, R, R, [&](int i, int k) { return s_k[i * PR + k] + s_k[k * PR + i]; },
                   [&](int k, int j) { return s_f[k * PR + j]; },
                   [&](int i, int j, float v) { s_d[i * PR + j] = v; });
     __syncthreads();
@@ -210,23 +284,19 @@ __global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) 
             dtheta[idx] = s_d[i * PR + j];
         }
         float* ddrive = a.ddrive_part + system * d * R;
-        block_product(d, R, R, [&](int f, int k) { return s_z[k * PD + f]; },
+        block_product<R>(d, R, R, [&](int f, int k) { return s_z[k * PD + f]; },
                       [&](int k, int j) { return s_d[k * PR + j]; },
                       [&](int f, int j, float v) { ddrive[f * R + j] = v / root; });
     }
     // ---- dz = -(1 + eta) dx + v + dTheta W^T / sqrt(n) (in place in s_v) ---
-    for (int idx = tid; idx < R * d; idx += kBwdThreads) {
-        const int i = idx / d;
-        const int f = idx - i * d;
-        float acc = 0.0f;
-        for (int k = 0; k < R; ++k) {
-            acc = fmaf(s_d[i * PR + k], drive[f * R + k], acc);
-        }
-        s_v[i * PD + f] = -(1.0f + eta) * s_x[i * PD + f] + s_v[i * PD + f] + acc / root;
-    }
+    block_product<R>(R, d, R, [&](int i, int k) { return s_d[i * PR + k]; },
+                  [&](int k, int f) { return drive[f * R + k]; },
+                  [&](int i, int f, float v) {
+                      s_v[i * PD + f] = -(1.0f + eta) * s_x[i * PD + f] + s_v[i * PD + f] + v / root;
+                  });
     __syncthreads();
     // ---- ds = L^-T dz -> s_u;  -<dx, z> --------------------------------------
-    block_product(R, d, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+    block_product<R>(R, d, R, [&](int i, int k) { return s_linv[k * PR + i]; },
                   [&](int k, int j) { return s_v[k * PD + j]; },
                   [&](int i, int j, float v) { s_u[i * PD + j] = v; });
     {
@@ -252,37 +322,38 @@ __global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) 
         a.deta_part[system] = -total;
     }
     // ---- Lbar = tril(-m dx^T - ds z^T) -> s_f;  L -> s_k ---------------------
-    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
-        const int i = idx / R;
-        const int j = idx - i * R;
-        float acc = 0.0f;
-        if (j <= i) {
-            for (int f = 0; f < d; ++f) {
-                acc = fmaf(s_m[i * PD + f], s_x[j * PD + f], acc);
-                acc = fmaf(s_u[i * PD + f], s_z[j * PD + f], acc);
-            }
+    // m dx^T, then + ds z^T, negated below the diagonal.
+    block_product<DMAX>(R, R, d, [&](int i, int f) { return s_m[i * PD + f]; },
+                        [&](int f, int j) { return s_x[j * PD + f]; },
+                        [&](int i, int j, float v) { s_f[i * PR + j] = v; });
+    // Each element is stored by the lane that stored it above (same tiles,
+    // same lane mapping), so no barrier is needed between the two products.
+    block_product<DMAX>(R, R, d, [&](int i, int f) { return s_u[i * PD + f]; },
+                        [&](int f, int j) { return s_z[j * PD + f]; },
+                        [&](int i, int j, float v) { s_f[i * PR + j] = j <= i ? -(s_f[i * PR + j] + v) : 0.0f; });
+#pragma unroll
+    for (int t = 0; t < kSquare; ++t) {
+        const int idx = tid + t * kBwdThreads;
+        if (idx < R * R) {
+            const int i = idx / R;
+            const int j = idx - i * R;
+            s_k[i * PR + j] = l_pre[t];
         }
-        s_f[i * PR + j] = -acc;
-    }
-    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
-        const int i = idx / R;
-        const int j = idx - i * R;
-        s_k[i * PR + j] = tape[idx];
     }
     __syncthreads();
     // ---- P = Phi(L^T Lbar) -> s_d --------------------------------------------
-    block_product(R, R, R, [&](int i, int k) { return s_k[k * PR + i]; },
+    block_product<R>(R, R, R, [&](int i, int k) { return s_k[k * PR + i]; },
                   [&](int k, int j) { return s_f[k * PR + j]; },
                   [&](int i, int j, float v) {
                       s_d[i * PR + j] = j < i ? v : (j == i ? 0.5f * v : 0.0f);
                   });
     __syncthreads();
     // ---- Mbar = L^-T P L^-1 --------------------------------------------------
-    block_product(R, R, R, [&](int i, int k) { return s_d[i * PR + k]; },
+    block_product<R>(R, R, R, [&](int i, int k) { return s_d[i * PR + k]; },
                   [&](int k, int j) { return s_linv[k * PR + j]; },
                   [&](int i, int j, float v) { s_f[i * PR + j] = v; });
     __syncthreads();
-    block_product(R, R, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+    block_product<R>(R, R, R, [&](int i, int k) { return s_linv[k * PR + i]; },
                   [&](int k, int j) { return s_f[k * PR + j]; },
                   [&](int i, int j, float v) { s_k[i * PR + j] = v; });
     __syncthreads();
@@ -609,11 +680,16 @@ int64_t bwd_record_layout(int64_t rank, int64_t head_dim, int64_t* off_m, int64_
 
 hipError_t launch_bwd_solve(int rank, const BwdSolveArgs& a, int64_t systems, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(systems));
+    const bool small = a.head_dim <= 32;
     switch (rank) {
-        case 16: bwd_solve_kernel<16><<<grid, kBwdThreads, 0, stream>>>(a); break;
-        case 32: bwd_solve_kernel<32><<<grid, kBwdThreads, 0, stream>>>(a); break;
-        case 48: bwd_solve_kernel<48><<<grid, kBwdThreads, 0, stream>>>(a); break;
-        default: bwd_solve_kernel<64><<<grid, kBwdThreads, 0, stream>>>(a); break;
+        case 16: small ? bwd_solve_kernel<16, 32><<<grid, kBwdThreads, 0, stream>>>(a)
+                       : bwd_solve_kernel<16, kBwdMaxHeadDim><<<grid, kBwdThreads, 0, stream>>>(a); break;
+        case 32: small ? bwd_solve_kernel<32, 32><<<grid, kBwdThreads, 0, stream>>>(a)
+                       : bwd_solve_kernel<32, kBwdMaxHeadDim><<<grid, kBwdThreads, 0, stream>>>(a); break;
+        case 48: small ? bwd_solve_kernel<48, 32><<<grid, kBwdThreads, 0, stream>>>(a)
+                       : bwd_solve_kernel<48, kBwdMaxHeadDim><<<grid, kBwdThreads, 0, stream>>>(a); break;
+        default: small ? bwd_solve_kernel<64, 32><<<grid, kBwdThreads, 0, stream>>>(a)
+                       : bwd_solve_kernel<64, kBwdMaxHeadDim><<<grid, kBwdThreads, 0, stream>>>(a); break;
     }
     return hipGetLastError();
 }
