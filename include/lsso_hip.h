@@ -284,6 +284,26 @@ int lsso_hip_linear(const void* x, int x_dtype, int64_t rows,
                     void* y, int y_dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Device scratch bytes needed by lsso_hip_linear_grad_columns. */
+int lsso_hip_linear_grad_columns_workspace_bytes(int64_t rows, int64_t cols, size_t* bytes);
+
+/* Upstream-gradient pass of the biased projection's backward, one read of g:
+ * g: [rows, cols] of g_dtype (LSSO_HIP_F16 or LSSO_HIP_BF16) with row stride
+ * g_row_stride elements (unit column stride); row_mask: optional device uint8
+ * [rows], rows whose byte is 0 count as zero.  When g_bf16 is not NULL it
+ * receives g rounded to BF16 (round to nearest even), contiguous [rows, cols],
+ * excluded rows zero: the BF16 operand of the weight-gradient GEMM.  When
+ * column_sums is not NULL it receives the FP32 sum of each column over the
+ * kept rows (the bias gradient), added in a fixed order.  Either output may be
+ * NULL; with both NULL the call does nothing.
+ * Replaces: grad_output.to(torch.bfloat16) and grad_output.sum(dim=rows,
+ * dtype=torch.float32) in _TensorCoreLinear.backward
+ * (lsso/ball/reference.py:205-247). */
+int lsso_hip_linear_grad_columns(const void* g, int g_dtype, int64_t rows, int64_t cols,
+                                 int64_t g_row_stride, const uint8_t* row_mask,
+                                 void* g_bf16, float* column_sums,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

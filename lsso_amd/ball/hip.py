@@ -48,6 +48,8 @@ _SYMBOLS = (
     "lsso_hip_mixer_backward",
     "lsso_hip_linear_workspace_bytes",
     "lsso_hip_linear",
+    "lsso_hip_linear_grad_columns_workspace_bytes",
+    "lsso_hip_linear_grad_columns",
     "lsso_hip_layer_supported",
     "lsso_hip_layer_workspace_bytes",
     "lsso_hip_layer_forward",
@@ -110,6 +112,12 @@ def _declare(library: ctypes.CDLL) -> None:
     library.lsso_hip_linear.argtypes = [
         vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, i64, vp, ctypes.c_int, vp, ctypes.c_size_t, vp,
     ]  # x, x_dtype, rows, in, stride, weight, bias, row_mask, out, y, y_dtype, ws, ws_bytes, stream
+    library.lsso_hip_linear_grad_columns_workspace_bytes.restype = ctypes.c_int
+    library.lsso_hip_linear_grad_columns_workspace_bytes.argtypes = [i64, i64, size_p]
+    library.lsso_hip_linear_grad_columns.restype = ctypes.c_int
+    library.lsso_hip_linear_grad_columns.argtypes = [
+        vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, ctypes.c_size_t, vp,
+    ]  # g, g_dtype, rows, cols, stride, row_mask, g_bf16, column_sums, ws, ws_bytes, stream
     library.lsso_hip_layer_supported.restype = ctypes.c_int
     library.lsso_hip_layer_supported.argtypes = [shape_p]
     library.lsso_hip_layer_workspace_bytes.restype = ctypes.c_int
@@ -912,6 +920,45 @@ def _linear_forward(
 
 
 
+def _grad_columns(
+    flat: torch.Tensor,
+    row_mask: torch.Tensor | None,
+    want_copy: bool,
+    want_sums: bool,
+) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """One native pass over a [rows, cols] float16/bfloat16 gradient (or
+    activation): its BF16 copy with ``row_mask``-excluded rows zeroed, and its
+    FP32 column sums over the kept rows (the bias gradient)."""
+
+    library = _library()
+    rows, cols = flat.shape
+    dtype_codes = {torch.float16: _F16, torch.bfloat16: _BF16}
+    copy = torch.empty((rows, cols), dtype=torch.bfloat16, device=flat.device) if want_copy else None
+    sums = torch.empty(cols, dtype=torch.float32, device=flat.device) if want_sums else None
+    workspace = None
+    size = ctypes.c_size_t(0)
+    if want_sums:
+        _check(library.lsso_hip_linear_grad_columns_workspace_bytes(rows, cols, ctypes.byref(size)), library)
+        workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=flat.device)
+    mask = None if row_mask is None else row_mask.reshape(-1).contiguous()
+    with torch.cuda.device(flat.device):
+        status = library.lsso_hip_linear_grad_columns(
+            flat.data_ptr(),
+            dtype_codes[flat.dtype],
+            rows,
+            cols,
+            flat.stride(0) if rows > 0 else cols,
+            None if mask is None else mask.data_ptr(),
+            None if copy is None else copy.data_ptr(),
+            None if sums is None else sums.data_ptr(),
+            None if workspace is None else workspace.data_ptr(),
+            size.value,
+            _stream(flat.device),
+        )
+    _check(status, library)
+    return copy, sums
+
+
 def _mm_fp32(left: torch.Tensor, right: torch.Tensor) -> torch.Tensor:
     """FP32 result of BF16 operands with FP32 accumulation (hipBLASLt)."""
 
@@ -949,8 +996,9 @@ class _Linear(torch.autograd.Function):
     (lsso/ball/reference.py:205-247): BF16 operands with FP32 accumulation
     for the value and weight gradients, an FP32 sum of the upstream gradient
     for the bias.  The value gradient runs on the native projection kernel
-    (dX = bf16(dY) bf16(W), stored once in the value's dtype); the weight
-    gradient, a reduction over all rows, is a library GEMM.  Rows excluded
+    (dX = bf16(dY) bf16(W), stored once in the value's dtype).  One native
+    pass over dY writes its BF16 copy for the weight gradient (a library GEMM
+    over all rows) and its column sums for the bias gradient.  Rows excluded
     by ``row_mask`` carry no gradient."""
 
     @staticmethod
@@ -965,24 +1013,42 @@ class _Linear(torch.autograd.Function):
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad_output):
         value, weight, row_mask = ctx.saved_tensors
-        if row_mask is not None:
-            grad_output = torch.where(row_mask[..., None], grad_output, torch.zeros_like(grad_output))
+        out_features, in_features = weight.shape
+        flat_grad = grad_output.reshape(-1, out_features)
+        if flat_grad.stride(-1) != 1 or flat_grad.dtype not in (torch.float16, torch.bfloat16):
+            flat_grad = flat_grad.to(dtype=torch.bfloat16).contiguous()
+        native_value = value.dtype in (torch.float16, torch.bfloat16) and out_features <= 512
+        need_value = ctx.needs_input_grad[0]
+        need_weight = ctx.needs_input_grad[1]
+        need_bias = ctx.has_bias and ctx.needs_input_grad[2]
+        need_bf16 = need_weight or (need_value and not native_value)
+        copy_grad = need_bf16 and (flat_grad.dtype != torch.bfloat16 or row_mask is not None)
+        grad_bf16, grad_sums = None, None
+        if copy_grad or need_bias:
+            grad_bf16, grad_sums = _grad_columns(flat_grad, row_mask, copy_grad, need_bias)
+        if need_bf16 and grad_bf16 is None:
+            grad_bf16 = flat_grad
         grad_value = grad_weight = grad_bias = None
-        flat_gradient = grad_output.to(dtype=torch.bfloat16).reshape(-1, weight.shape[0])
-        if ctx.needs_input_grad[0]:
-            if value.dtype in (torch.float16, torch.bfloat16) and weight.shape[0] <= 512:
+        if need_value:
+            if native_value:
                 grad_value = _linear_forward(
-                    flat_gradient, weight.mT.contiguous(), None, value.dtype
+                    flat_grad, weight.mT.contiguous(), None, value.dtype,
+                    None if row_mask is None else row_mask.reshape(-1),
                 ).reshape(value.shape)
             else:
-                grad_value = _mm_fp32(flat_gradient, weight.to(dtype=torch.bfloat16))
+                grad_value = _mm_fp32(grad_bf16, weight.to(dtype=torch.bfloat16))
                 grad_value = grad_value.to(dtype=value.dtype).reshape(value.shape)
-        if ctx.needs_input_grad[1]:
-            flat_value = value.to(dtype=torch.bfloat16).reshape(-1, value.shape[-1])
-            grad_weight = _weight_gradient(flat_gradient, flat_value).to(dtype=weight.dtype)
-        if ctx.has_bias and ctx.needs_input_grad[2]:
-            dimensions = tuple(range(grad_output.ndim - 1))
-            grad_bias = grad_output.sum(dim=dimensions, dtype=torch.float32).to(dtype=ctx.bias_dtype)
+        if need_weight:
+            flat_value = value.reshape(-1, in_features)
+            if flat_value.dtype in (torch.float16, torch.bfloat16) and flat_value.stride(-1) == 1 and (
+                flat_value.dtype != torch.bfloat16 or row_mask is not None
+            ):
+                flat_value, _ = _grad_columns(flat_value, row_mask, True, False)
+            else:
+                flat_value = flat_value.to(dtype=torch.bfloat16)
+            grad_weight = _weight_gradient(grad_bf16, flat_value).to(dtype=weight.dtype)
+        if need_bias:
+            grad_bias = grad_sums.to(dtype=ctx.bias_dtype)
         return grad_value, grad_weight, grad_bias, None, None
 
 

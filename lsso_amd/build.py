@@ -26,6 +26,7 @@ SOURCES = (
     "lsso_capi.hip",
     "lsso_mixer.hip",
     "lsso_linear.hip",
+    "lsso_linear_grad.hip",
     "lsso_fused.hip",
     "lsso_backward.hip",
     "lsso_project_reduce.hip",

@@ -603,61 +603,324 @@ __global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// Parameter gradients: sums over the batch in ascending order.
-__global__ __launch_bounds__(256) void param_reduce_kernel(ParamReduceArgs a) {
-    const int64_t per_head = a.rank * a.rank + a.head_dim * a.rank + 1;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= a.heads * per_head) {
+// Token map with the system's records held in registers for the whole chunk
+// (head_dim = 16 D16 and records of at most 112 VGPRs, (3 R d + R^2) / 64):
+// the loop streams only token rows, and each step reads the next 16 tokens'
+// inputs before it computes.  The MFMA chains and the <dY, C> order are those
+// of bwd_apply_kernel, so the two kernels agree bitwise.
+template <int R, int D16>
+struct BwdTokenInputs {
+    static constexpr bool kRK32 = (R % 32) == 0;
+    static constexpr bool kDK32 = (D16 % 2) == 0;
+    using RR = RecordShape<kRK32>;
+    using RD = RecordShape<kDK32>;
+    static constexpr int kRankSteps = R / RR::kWidth;
+    static constexpr int kFeatSteps = kDK32 ? D16 / 2 : D16;
+    using RankOp = typename std::conditional<kRK32, u32x4, u32x2>::type;
+    using FeatOp = typename std::conditional<kDK32, u32x4, u32x2>::type;
+    RankOp rel[kRankSteps];
+    RankOp ph[kRankSteps];
+    FeatOp y[kFeatSteps];
+    FeatOp c[kFeatSteps];
+
+    // Lane (g, q) reads the runs of its token that the MFMA B operand takes;
+    // a token past the chunk reads a valid row and keeps zeros.
+    __device__ __forceinline__ void load(const uint16_t* rel_row, const uint16_t* content_row,
+                                         const uint16_t* grad_row, const uint32_t* phase_row,
+                                         int g, bool live) {
+#pragma unroll
+        for (int s = 0; s < kRankSteps; ++s) {
+            const int first = RR::kWidth * s + RR::kPerLane * g;
+            const RankOp r = *reinterpret_cast<const RankOp*>(rel_row + first);
+            ph[s] = *reinterpret_cast<const RankOp*>(phase_row + first / 2);
+            rel[s] = live ? r : RankOp{};
+        }
+#pragma unroll
+        for (int s = 0; s < kFeatSteps; ++s) {
+            const int first = RD::kWidth * s + RD::kPerLane * g;
+            const FeatOp yv = *reinterpret_cast<const FeatOp*>(grad_row + first);
+            const FeatOp cv = *reinterpret_cast<const FeatOp*>(content_row + first);
+            y[s] = live ? yv : FeatOp{};
+            c[s] = live ? cv : FeatOp{};
+        }
+    }
+};
+
+template <int R, int D16>
+__global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a) {
+    using In = BwdTokenInputs<R, D16>;
+    using RR = typename In::RR;
+    using RD = typename In::RD;
+    using RankOp = typename In::RankOp;
+    using FeatOp = typename In::FeatOp;
+    constexpr int RBLK = R / 16;
+    constexpr int RSTEPS = In::kRankSteps;
+    constexpr int DSTEPS = In::kFeatSteps;
+    constexpr int D = 16 * D16;
+    constexpr int PAIRS = R / 2;
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wave >= a.total_waves) {
         return;
     }
-    const int64_t h = idx / per_head;
-    const int64_t e = idx - h * per_head;
+    int64_t rest = wave;
+    const int64_t h = rest % a.heads;
+    rest /= a.heads;
+    const int64_t chunk = rest % a.chunks;
+    const int64_t b = rest / a.chunks;
+    const int q = lane & 15;
+    const int g = lane >> 4;
+    const int64_t system = b * a.heads + h;
+    const float eta = bounded_complement(a.eta_raw[h]);
+    const uint16_t* rec = a.records + system * a.record_stride;
+
+    // Records: dA^T = M dY + E C + G A (rank row blocks), dC^T = F A.
+    FeatOp m_hi[RBLK][DSTEPS], m_lo[RBLK][DSTEPS], e_hi[RBLK][DSTEPS], e_lo[RBLK][DSTEPS];
+    RankOp g_hi[RBLK][RSTEPS], g_lo[RBLK][RSTEPS], f_hi[D16][RSTEPS], f_lo[D16][RSTEPS];
+#pragma unroll
+    for (int rb = 0; rb < RBLK; ++rb) {
+#pragma unroll
+        for (int s = 0; s < DSTEPS; ++s) {
+            const int64_t o = ((rb * DSTEPS + s) * 64 + lane) * RD::kLaneHalfs;
+            m_hi[rb][s] = *reinterpret_cast<const FeatOp*>(rec + a.off_m + o);
+            m_lo[rb][s] = *reinterpret_cast<const FeatOp*>(rec + a.off_m + o + RD::kPerLane);
+            e_hi[rb][s] = *reinterpret_cast<const FeatOp*>(rec + a.off_e + o);
+            e_lo[rb][s] = *reinterpret_cast<const FeatOp*>(rec + a.off_e + o + RD::kPerLane);
+        }
+#pragma unroll
+        for (int s = 0; s < RSTEPS; ++s) {
+            const int64_t o = ((rb * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
+            g_hi[rb][s] = *reinterpret_cast<const RankOp*>(rec + a.off_g + o);
+            g_lo[rb][s] = *reinterpret_cast<const RankOp*>(rec + a.off_g + o + RR::kPerLane);
+        }
+    }
+#pragma unroll
+    for (int fb = 0; fb < D16; ++fb) {
+#pragma unroll
+        for (int s = 0; s < RSTEPS; ++s) {
+            const int64_t o = ((fb * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
+            f_hi[fb][s] = *reinterpret_cast<const RankOp*>(rec + a.off_f + o);
+            f_lo[fb][s] = *reinterpret_cast<const RankOp*>(rec + a.off_f + o + RR::kPerLane);
+        }
+    }
+
+    const int64_t begin = chunk * a.chunk_tokens;
+    const int64_t end = begin + a.chunk_tokens < a.length ? begin + a.chunk_tokens : a.length;
+    const uint16_t* proj = a.projected + b * a.length * a.width;
+    const uint16_t* grad = a.grad_output + b * a.length * a.grad_stride + h * D;
+    const uint32_t* phase = a.phases + b * a.phase_batch_stride;
+    uint16_t* gout = a.grad_projected + b * a.length * a.width;
+    const int64_t rel_off = h * R;
+    const int64_t content_off = a.heads * R + h * D;
+    auto fetch = [&](In& in, int64_t t0) {
+        const int64_t token = t0 + q;
+        const bool live = token < end;
+        const int64_t safe = live ? token : begin;
+        const uint16_t* prow = proj + safe * a.width;
+        in.load(prow + rel_off, prow + content_off, grad + safe * a.grad_stride, phase + safe * PAIRS,
+                g, live);
+    };
+
+    float dot = 0.0f;
+    In cur;
+    fetch(cur, begin);
+    for (int64_t t0 = begin; t0 < end; t0 += 16) {
+        In nxt;
+        fetch(nxt, t0 + 16);
+        const int64_t token = t0 + q;
+        const bool live = token < end;
+        const int64_t safe = live ? token : begin;
+
+        RankOp a_hi[RSTEPS];
+        RankOp a_lo[RSTEPS];
+#pragma unroll
+        for (int s = 0; s < RSTEPS; ++s) {
+#pragma unroll
+            for (int p = 0; p < RR::kPerLane / 2; ++p) {
+                float e, o;
+                rotate_pair(cur.rel[s][p], cur.ph[s][p], e, o);
+                uint32_t hi, lo;
+                split_bf16(e, o, hi, lo);
+                a_hi[s][p] = hi;
+                a_lo[s][p] = lo;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < DSTEPS; ++s) {
+#pragma unroll
+            for (int p = 0; p < RD::kPerLane / 2; ++p) {
+                dot = fmaf(bf16_lo(cur.y[s][p]), bf16_lo(cur.c[s][p]), dot);
+                dot = fmaf(bf16_hi(cur.y[s][p]), bf16_hi(cur.c[s][p]), dot);
+            }
+        }
+
+        uint16_t* out_row = gout + safe * a.width;
+        // dA^T blocks: feature-K chain (dY, C) and rank-K chain (A) kept apart.
+#pragma unroll
+        for (int rb = 0; rb < RBLK; ++rb) {
+            f32x4 acc_d = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 acc_r = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < DSTEPS; ++s) {
+                if constexpr (In::kDK32) {
+                    acc_d = mfma16x16x32(m_hi[rb][s], cur.y[s], acc_d);
+                    acc_d = mfma16x16x32(m_lo[rb][s], cur.y[s], acc_d);
+                    acc_d = mfma16x16x32(e_hi[rb][s], cur.c[s], acc_d);
+                    acc_d = mfma16x16x32(e_lo[rb][s], cur.c[s], acc_d);
+                } else {
+                    acc_d = mfma16x16x16(m_hi[rb][s], cur.y[s], acc_d);
+                    acc_d = mfma16x16x16(m_lo[rb][s], cur.y[s], acc_d);
+                    acc_d = mfma16x16x16(e_hi[rb][s], cur.c[s], acc_d);
+                    acc_d = mfma16x16x16(e_lo[rb][s], cur.c[s], acc_d);
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < RSTEPS; ++s) {
+                if constexpr (In::kRK32) {
+                    acc_r = mfma16x16x32(g_hi[rb][s], a_hi[s], acc_r);
+                    acc_r = mfma16x16x32(g_hi[rb][s], a_lo[s], acc_r);
+                    acc_r = mfma16x16x32(g_lo[rb][s], a_hi[s], acc_r);
+                } else {
+                    acc_r = mfma16x16x16(g_hi[rb][s], a_hi[s], acc_r);
+                    acc_r = mfma16x16x16(g_hi[rb][s], a_lo[s], acc_r);
+                    acc_r = mfma16x16x16(g_lo[rb][s], a_hi[s], acc_r);
+                }
+            }
+            // Lane holds dA[token q][ranks 16 rb + 4 g .. +3]: rotate back.
+            if (live) {
+                const int rank0 = 16 * rb + 4 * g;
+                u32x2 ph;
+                if constexpr (In::kRK32) {
+                    ph = *reinterpret_cast<const u32x2*>(phase + safe * PAIRS + rank0 / 2);
+                } else {
+                    ph = cur.ph[rb];  // the K16 run of step rb is ranks 16 rb + 4 g .. +3
+                }
+                float gradv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    gradv[i] = acc_d[i] + acc_r[i];
+                }
+                u32x2 packed;
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const float cosine = f16_lo(ph[p]);
+                    const float sine = f16_hi(ph[p]);
+                    const float even = gradv[2 * p] * cosine + gradv[2 * p + 1] * sine;
+                    const float odd = gradv[2 * p + 1] * cosine - gradv[2 * p] * sine;
+                    packed[p] = pack_bf16(even, odd);
+                }
+                *reinterpret_cast<u32x2*>(out_row + rel_off + rank0) = packed;
+            }
+        }
+        // dC^T blocks: eta dY + (ds / sqrt(n))^T A^T.
+#pragma unroll
+        for (int fb = 0; fb < D16; ++fb) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < RSTEPS; ++s) {
+                if constexpr (In::kRK32) {
+                    acc = mfma16x16x32(f_hi[fb][s], a_hi[s], acc);
+                    acc = mfma16x16x32(f_hi[fb][s], a_lo[s], acc);
+                    acc = mfma16x16x32(f_lo[fb][s], a_hi[s], acc);
+                } else {
+                    acc = mfma16x16x16(f_hi[fb][s], a_hi[s], acc);
+                    acc = mfma16x16x16(f_hi[fb][s], a_lo[s], acc);
+                    acc = mfma16x16x16(f_lo[fb][s], a_hi[s], acc);
+                }
+            }
+            if (live) {
+                const int f0 = 16 * fb + 4 * g;
+                u32x2 dy;
+                if constexpr (In::kDK32) {
+                    dy = *reinterpret_cast<const u32x2*>(grad + safe * a.grad_stride + f0);
+                } else {
+                    dy = cur.y[fb];  // the K16 run of step fb is features 16 fb + 4 g .. +3
+                }
+                u32x2 packed;
+                packed.x = pack_bf16(fmaf(eta, bf16_lo(dy.x), acc[0]), fmaf(eta, bf16_hi(dy.x), acc[1]));
+                packed.y = pack_bf16(fmaf(eta, bf16_lo(dy.y), acc[2]), fmaf(eta, bf16_hi(dy.y), acc[3]));
+                *reinterpret_cast<u32x2*>(out_row + content_off + f0) = packed;
+            }
+        }
+        cur = nxt;
+    }
+    // <dY, C> of this wave's tokens.
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        dot += __shfl_xor(dot, offset);
+    }
+    if (lane == 0) {
+        a.dot_part[system * a.chunks + chunk] = dot;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Parameter gradients.  One thread per element of dTheta0 and dW sums the
+// batch in ascending order (sixteen samples' loads issued together); one wave
+// per head sums deta and <dY, C> over every (sample, chunk), lane-strided and
+// then by a fixed butterfly.
+__global__ __launch_bounds__(256) void param_reduce_kernel(ParamReduceArgs a) {
     const int64_t rr = a.rank * a.rank;
     const int64_t dr = a.head_dim * a.rank;
-    // Eight samples' loads are issued together, then summed in order.
+    const int64_t elements = a.heads * (rr + dr);
+    const int64_t element_blocks = (elements + 255) / 256;
+    if (blockIdx.x >= element_blocks) {
+        const int64_t h = blockIdx.x - element_blocks;
+        const int lane = threadIdx.x;
+        if (lane >= 64) {
+            return;
+        }
+        float acc = 0.0f;
+        for (int64_t b = lane; b < a.batch; b += 64) {
+            acc += a.deta_part[b * a.heads + h];
+        }
+        const int64_t dots = a.batch * a.chunks;
+        for (int64_t i = lane; i < dots; i += 64) {
+            const int64_t b = i / a.chunks;
+            acc += a.dot_part[(b * a.heads + h) * a.chunks + (i - b * a.chunks)];
+        }
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            acc += __shfl_xor(acc, offset);
+        }
+        if (lane == 0) {
+            a.grad_eta[h] = acc * bounded_complement_derivative(a.eta_raw[h]);
+        }
+        return;
+    }
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= elements) {
+        return;
+    }
+    const int64_t h = idx / (rr + dr);
+    const int64_t e = idx - h * (rr + dr);
     const float* source;
     int64_t stride;
     if (e < rr) {
         source = a.dtheta_part + h * rr + e;
         stride = a.heads * rr;
-    } else if (e < rr + dr) {
+    } else {
         source = a.ddrive_part + h * dr + (e - rr);
         stride = a.heads * dr;
-    } else {
-        source = a.deta_part + h;
-        stride = a.heads;
     }
+    constexpr int kBatchLoads = 16;
     float acc = 0.0f;
-    for (int64_t b0 = 0; b0 < a.batch; b0 += 8) {
-        float v[8];
+    for (int64_t b0 = 0; b0 < a.batch; b0 += kBatchLoads) {
+        float v[kBatchLoads];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kBatchLoads; ++u) {
             const int64_t b = b0 + u < a.batch ? b0 + u : a.batch - 1;
             v[u] = source[b * stride];
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kBatchLoads; ++u) {
             if (b0 + u < a.batch) {
                 acc += v[u];
             }
         }
     }
-    if (e == rr + dr) {
-        // <dY, C> partials of every sample and chunk, in sample order.
-        for (int64_t b = 0; b < a.batch; ++b) {
-            const float* dots = a.dot_part + (b * a.heads + h) * a.chunks;
-            for (int64_t ch = 0; ch < a.chunks; ++ch) {
-                acc += dots[ch];
-            }
-        }
-    }
     if (e < rr) {
         a.grad_base[h * rr + e] = acc;
-    } else if (e < rr + dr) {
-        a.grad_drive[h * dr + (e - rr)] = acc;
     } else {
-        a.grad_eta[h] = acc * bounded_complement_derivative(a.eta_raw[h]);
+        a.grad_drive[h * dr + (e - rr)] = acc;
     }
 }
 
@@ -713,7 +976,35 @@ static hipError_t launch_bwd_apply_r(const BwdApplyArgs& a, bool dk32, bool vec,
     return hipGetLastError();
 }
 
+template <int R, int D16>
+static hipError_t launch_bwd_apply_resident(const BwdApplyArgs& a, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((a.total_waves + 3) / 4));
+    bwd_apply_resident_kernel<R, D16><<<grid, 256, 0, stream>>>(a);
+    return hipGetLastError();
+}
+
+// Largest head_dim / 16 whose records stay resident ((3 R d + R^2) / 64 <= 112 VGPRs).
+static int resident_max_d16(int rank) {
+    return rank <= 32 ? 4 : (rank == 48 ? 2 : 1);
+}
+
 hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, bool vec, hipStream_t stream) {
+    const int d16 = static_cast<int>(a.head_dim / 16);
+    if (vec && a.head_dim % 16 == 0 && d16 >= 1 && d16 <= resident_max_d16(rank)) {
+        switch (rank * 8 + d16) {
+            case 16 * 8 + 1: return launch_bwd_apply_resident<16, 1>(a, stream);
+            case 16 * 8 + 2: return launch_bwd_apply_resident<16, 2>(a, stream);
+            case 16 * 8 + 3: return launch_bwd_apply_resident<16, 3>(a, stream);
+            case 16 * 8 + 4: return launch_bwd_apply_resident<16, 4>(a, stream);
+            case 32 * 8 + 1: return launch_bwd_apply_resident<32, 1>(a, stream);
+            case 32 * 8 + 2: return launch_bwd_apply_resident<32, 2>(a, stream);
+            case 32 * 8 + 3: return launch_bwd_apply_resident<32, 3>(a, stream);
+            case 32 * 8 + 4: return launch_bwd_apply_resident<32, 4>(a, stream);
+            case 48 * 8 + 1: return launch_bwd_apply_resident<48, 1>(a, stream);
+            case 48 * 8 + 2: return launch_bwd_apply_resident<48, 2>(a, stream);
+            default: return launch_bwd_apply_resident<64, 1>(a, stream);
+        }
+    }
     switch (rank) {
         case 16: return launch_bwd_apply_r<16>(a, dk32, vec, stream);
         case 32: return launch_bwd_apply_r<32>(a, dk32, vec, stream);
@@ -723,8 +1014,8 @@ hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, bool vec
 }
 
 hipError_t launch_param_reduce(const ParamReduceArgs& a, hipStream_t stream) {
-    const int64_t total = a.heads * (a.rank * a.rank + a.head_dim * a.rank + 1);
-    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+    const int64_t elements = a.heads * (a.rank * a.rank + a.head_dim * a.rank);
+    const dim3 grid(static_cast<unsigned>((elements + 255) / 256 + a.heads));
     param_reduce_kernel<<<grid, 256, 0, stream>>>(a);
     return hipGetLastError();
 }

@@ -724,6 +724,108 @@ int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape, const void* grad_
     return LSSO_HIP_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+constexpr int64_t kGradTargetGroups = 512;
+
+struct GradColumnsPlan {
+    int chunks_per_slab;
+    int64_t slabs, splits, rows_per_split;
+};
+
+// Chunks of 8 columns are dealt to slabs of a power-of-two width (the largest
+// that divides the chunk count, up to 64; else the smallest covering it), and
+// rows to about 512 / slabs splits of at least eight passes each.
+void plan_grad_columns(int64_t rows, int64_t cols, GradColumnsPlan* p) {
+    const int64_t chunks = ceil_div(cols, 8);
+    int cw = 1;
+    while (cw < 64 && chunks % (2 * cw) == 0) {
+        cw *= 2;
+    }
+    if (cw < 8) {
+        cw = 1;
+        while (cw < 64 && cw < chunks) {
+            cw *= 2;
+        }
+    }
+    p->chunks_per_slab = cw;
+    p->slabs = ceil_div(chunks, cw);
+    const int64_t row_lanes = 256 / cw;
+    int64_t splits = ceil_div(kGradTargetGroups, p->slabs);
+    const int64_t most = std::max<int64_t>(1, ceil_div(rows, row_lanes * 8));
+    splits = std::min(splits, most);
+    p->rows_per_split = std::max<int64_t>(1, ceil_div(rows, splits));
+    p->splits = rows == 0 ? 0 : ceil_div(rows, p->rows_per_split);
+}
+
+}  // namespace
+
+extern "C" {
+
+int lsso_hip_linear_grad_columns_workspace_bytes(int64_t rows, int64_t cols, size_t* bytes) {
+    if (bytes == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "bytes must not be NULL");
+    }
+    if (rows < 0 || cols <= 0) {
+        return fail(LSSO_HIP_EINVAL, "rows must be >= 0 and cols must be positive");
+    }
+    GradColumnsPlan plan;
+    plan_grad_columns(rows, cols, &plan);
+    *bytes = align_up(sizeof(float) * plan.splits * cols);
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_linear_grad_columns(const void* g, int g_dtype, int64_t rows, int64_t cols,
+                                 int64_t g_row_stride, const uint8_t* row_mask, void* g_bf16,
+                                 float* column_sums, void* workspace, size_t workspace_bytes,
+                                 void* stream_handle) {
+    if (rows < 0 || cols <= 0) {
+        return fail(LSSO_HIP_EINVAL, "rows must be >= 0 and cols must be positive");
+    }
+    if (g_dtype != LSSO_HIP_F16 && g_dtype != LSSO_HIP_BF16) {
+        return fail(LSSO_HIP_EUNSUPPORTED, "the gradient dtype must be float16 or bfloat16");
+    }
+    if (g_row_stride < cols) {
+        return fail(LSSO_HIP_EINVAL, "g_row_stride must be >= cols");
+    }
+    if (g_bf16 == nullptr && column_sums == nullptr) {
+        return LSSO_HIP_OK;
+    }
+    if (rows > 0 && g == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "g must not be NULL");
+    }
+    if (!aligned(g, 2) || !aligned(g_bf16, 2) || !aligned(column_sums, 4)) {
+        return fail(LSSO_HIP_EINVAL, "g, g_bf16 and column_sums must be aligned to their element size");
+    }
+    GradColumnsPlan plan;
+    plan_grad_columns(rows, cols, &plan);
+    const size_t needed = column_sums == nullptr ? 0 : align_up(sizeof(float) * plan.splits * cols);
+    if (needed > 0 && (workspace == nullptr || workspace_bytes < needed || !aligned(workspace, 16))) {
+        return fail(LSSO_HIP_EINVAL, "workspace must be 16-byte aligned and hold " +
+                                         std::to_string(needed) + " bytes");
+    }
+    lsso_hip::GradColumnsArgs args{};
+    args.g = g;
+    args.rows = rows;
+    args.cols = cols;
+    args.g_stride = g_row_stride;
+    args.row_mask = row_mask;
+    args.g_bf16 = static_cast<uint16_t*>(g_bf16);
+    args.partials = column_sums == nullptr ? nullptr : static_cast<float*>(workspace);
+    args.rows_per_split = plan.rows_per_split;
+    args.chunks_per_slab = plan.chunks_per_slab;
+    const bool vec = cols % 8 == 0 && g_row_stride % 8 == 0 && aligned(g, 16) && aligned(g_bf16, 16);
+    const hipError_t error = lsso_hip::launch_grad_columns(
+        args, g_dtype, vec, plan.splits, plan.slabs, column_sums,
+        static_cast<hipStream_t>(stream_handle));
+    if (error != hipSuccess) {
+        return hip_failure(error, "grad_columns_kernel launch");
+    }
+    return LSSO_HIP_OK;
+}
+
 int lsso_hip_linear_workspace_bytes(int64_t rows, int64_t in_features, int64_t out_features,
                                     size_t* bytes) {
     if (bytes == nullptr) {

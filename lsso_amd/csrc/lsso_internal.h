@@ -177,6 +177,20 @@ struct LinearArgs {
     int y_vector;               // 16-byte y stores are legal
 };
 
+// Upstream-gradient pass of the projection's backward: BF16 copy and FP32
+// column sums of g [rows, cols] in one read.
+struct GradColumnsArgs {
+    const void* g;              // FP16/BF16 [rows, cols], row stride g_stride
+    int64_t rows;
+    int64_t cols;
+    int64_t g_stride;
+    const uint8_t* row_mask;    // [rows] or nullptr; 0 rows count as zero
+    uint16_t* g_bf16;           // BF16 [rows, cols] contiguous, or nullptr
+    float* partials;            // [splits, cols] column sums per split, or nullptr
+    int64_t rows_per_split;
+    int chunks_per_slab;        // 8-column chunks per workgroup: divides 256
+};
+
 // Input projection fused with the L-reductions (one pass over x per head
 // group): packed = bf16(x W^T + b) per 64-token tile in LDS, contracted into
 // the G / S partials of each head of the group and optionally written out.
@@ -233,6 +247,8 @@ int project_reduce_group_heads(int64_t rank, int64_t heads, int64_t head_dim,
 int project_reduce_tile_rows();
 hipError_t launch_project_reduce(int rank, const ProjectReduceArgs& a, int x_dtype, int grid,
                                  hipStream_t stream);
+hipError_t launch_grad_columns(const GradColumnsArgs& a, int g_dtype, bool vec, int64_t splits,
+                               int64_t slabs, float* column_sums, hipStream_t stream);
 int linear_tile_rows();
 int linear_columns_per_group(int k_steps);
 int linear_k_tier(int64_t in_features);

@@ -147,6 +147,28 @@ def test_linear_validation(library) -> None:
     assert "in_features <= 512" in _message(library)
 
 
+def test_grad_columns_validation(library) -> None:
+    size = ctypes.c_size_t()
+    assert library.lsso_hip_linear_grad_columns_workspace_bytes(0, 256, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert library.lsso_hip_linear_grad_columns_workspace_bytes(131072, 640, ctypes.byref(size)) == 0
+    assert size.value >= 640 * 4 and size.value % 256 == 0
+    assert library.lsso_hip_linear_grad_columns_workspace_bytes(4, 0, ctypes.byref(size)) == -1
+    status = library.lsso_hip_linear_grad_columns(None, 3, 4, 8, 8, None, None, None, None, 0, None)
+    assert status == -2
+    assert "float16 or bfloat16" in _message(library)
+    status = library.lsso_hip_linear_grad_columns(None, 1, 4, 8, 4, None, None, None, None, 0, None)
+    assert status == -1
+    assert "g_row_stride" in _message(library)
+    # Nothing asked for: no launch, no error.
+    assert library.lsso_hip_linear_grad_columns(None, 1, 4, 8, 8, None, None, None, None, 0, None) == 0
+    sums = ctypes.c_void_p(256)
+    status = library.lsso_hip_linear_grad_columns(ctypes.c_void_p(512), 1, 4, 8, 8, None, None,
+                                                  sums, None, 0, None)
+    assert status == -1
+    assert "workspace" in _message(library)
+
+
 def test_errors_are_thread_local(library) -> None:
     import threading
 
