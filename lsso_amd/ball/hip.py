@@ -1017,7 +1017,7 @@ class _Linear(torch.autograd.Function):
         flat_grad = grad_output.reshape(-1, out_features)
         if flat_grad.stride(-1) != 1 or flat_grad.dtype not in (torch.float16, torch.bfloat16):
             flat_grad = flat_grad.to(dtype=torch.bfloat16).contiguous()
-        native_value = value.dtype in (torch.float16, torch.bfloat16) and out_features <= 512
+        native_value = value.dtype in (torch.float16, torch.bfloat16) and out_features <= 640
         need_value = ctx.needs_input_grad[0]
         need_weight = ctx.needs_input_grad[1]
         need_bias = ctx.has_bias and ctx.needs_input_grad[2]

@@ -391,7 +391,7 @@ int run_linear(const void* x, int x_dtype, int64_t rows, int64_t in_features,
     args.row_mask = row_mask;
     args.out_features = out_features;
     args.y = y;
-    args.tiles = ceil_div(rows, lsso_hip::linear_tile_rows());
+    args.tiles = ceil_div(rows, lsso_hip::linear_tile_rows(tier));
     args.column_groups = ceil_div(out_features, lsso_hip::linear_columns_per_group(tier));
     args.x_vector = (in_features % 8 == 0 && x_row_stride % 8 == 0 && aligned(x, 16)) ? 1 : 0;
     args.y_vector = (out_features % 8 == 0 && aligned(y, 16)) ? 1 : 0;
@@ -857,7 +857,7 @@ int lsso_hip_linear(const void* x, int x_dtype, int64_t rows, int64_t in_feature
     const int tier = lsso_hip::linear_k_tier(in_features);
     if (tier == 0) {
         return fail(LSSO_HIP_EUNSUPPORTED,
-                    "the HIP projection supports in_features <= 512, got " +
+                    "the HIP projection supports in_features <= 640, got " +
                         std::to_string(in_features));
     }
     if (rows == 0) {

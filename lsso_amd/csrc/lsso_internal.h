@@ -249,7 +249,7 @@ hipError_t launch_project_reduce(int rank, const ProjectReduceArgs& a, int x_dty
                                  hipStream_t stream);
 hipError_t launch_grad_columns(const GradColumnsArgs& a, int g_dtype, bool vec, int64_t splits,
                                int64_t slabs, float* column_sums, hipStream_t stream);
-int linear_tile_rows();
+int linear_tile_rows(int k_steps);
 int linear_columns_per_group(int k_steps);
 int linear_k_tier(int64_t in_features);
 

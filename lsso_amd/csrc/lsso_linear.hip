@@ -5,11 +5,12 @@
 // FP32 accumulation, FP32 bias added to the accumulator, one final FP16 or
 // BF16 store; FP16 output never rounds through BF16.
 //
-// Schedule: persistent workgroups of 8 waves (4 when K > 256).  Each wave
-// keeps a 32-column slice of W (BF16, K padded to 16) in registers for the
-// whole launch, so the weights are read once per workgroup.  64-row x tiles
-// are staged through a double-buffered LDS tile (converted to BF16 once) and
-// shared by the workgroup's waves.
+// Schedule: persistent workgroups of 8 waves (4 when K > 256).  Each
+// wave keeps a 32-column slice of W (BF16, K padded to 16) in registers for
+// the whole launch, so the weights are read once per workgroup.  64-row x
+// tiles (32-row once K > 512, so that two of them fit LDS) are staged through
+// a double-buffered LDS tile (converted to BF16 once) and shared by the
+// workgroup's waves.
 // The MFMA computes y^T = W x^T on v_mfma_f32_32x32x16_bf16; in that form a
 // lane's accumulators are 4 runs of 4 consecutive output features of one
 // row.  The rounded tile is staged in LDS and written back in 16-byte pieces
@@ -21,15 +22,18 @@
 
 namespace lsso_hip {
 
-constexpr int kLinearTileRows = 64;
 constexpr int kXcds = 8;   // accelerator complex dies of an MI355X
+
+// Rows per x tile: 64, or 32 once K exceeds 512.
+template <int KSTEPS>
+constexpr int linear_tile_rows_k() { return KSTEPS <= 32 ? 64 : 32; }
 
 // Waves per workgroup: eight (two per SIMD, 256 registers each) while the
 // resident W slice fits; four once K exceeds 256.
 template <int KSTEPS>
 constexpr int linear_waves() { return KSTEPS <= 16 ? 8 : 4; }
 
-int linear_tile_rows() { return kLinearTileRows; }
+int linear_tile_rows(int k_steps) { return k_steps <= 32 ? 64 : 32; }
 int linear_columns_per_group(int k_steps) { return (k_steps <= 16 ? 8 : 4) * 32; }
 
 int linear_k_tier(int64_t in_features) {
@@ -39,6 +43,7 @@ int linear_k_tier(int64_t in_features) {
     if (in_features <= 256) return 16;
     if (in_features <= 384) return 24;
     if (in_features <= 512) return 32;
+    if (in_features <= 640) return 40;
     return 0;
 }
 
@@ -122,18 +127,20 @@ __device__ __forceinline__ uint16_t to_output_bits(float value) {
 template <int KSTEPS, int XT, int YT, bool XVEC>
 __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(LinearArgs a) {
     constexpr int kWaves = linear_waves<KSTEPS>();
+    constexpr int kTileRows = linear_tile_rows_k<KSTEPS>();
+    constexpr int MB = kTileRows / 32;                  // 32-row MFMA blocks per tile
     constexpr int kGroupColumns = kWaves * 32;
     constexpr int KP = 16 * KSTEPS + 8;                  // LDS row pitch (bf16)
     constexpr int kChunksPerRow = 2 * KSTEPS;           // 8-element chunks
     constexpr int kThreads = kWaves * 64;
-    constexpr int kChunksPerThread = kLinearTileRows * kChunksPerRow / kThreads;
-    static_assert(kLinearTileRows * kChunksPerRow % kThreads == 0, "tile split");
-    __shared__ __attribute__((aligned(16))) uint16_t s_x[2][kLinearTileRows * KP];
+    constexpr int kChunksPerThread = kTileRows * kChunksPerRow / kThreads;
+    static_assert(kTileRows * kChunksPerRow % kThreads == 0, "tile split");
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[2][kTileRows * KP];
     __shared__ __attribute__((aligned(16))) float s_bias[kGroupColumns];
     constexpr int YP = kGroupColumns + 8;                 // staged output row pitch
-    constexpr int kStoreChunks = kLinearTileRows * kGroupColumns / 8 / kThreads;
-    static_assert(kLinearTileRows * kGroupColumns / 8 % kThreads == 0, "store split");
-    __shared__ __attribute__((aligned(16))) uint16_t s_y[kLinearTileRows * YP];
+    constexpr int kStoreChunks = kTileRows * kGroupColumns / 8 / kThreads;
+    static_assert(kTileRows * kGroupColumns / 8 % kThreads == 0, "store split");
+    __shared__ __attribute__((aligned(16))) uint16_t s_y[kTileRows * YP];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -171,7 +178,7 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
             const int chunk = tid + c * kThreads;
             const int rr = chunk / kChunksPerRow;
             const int cc = chunk - rr * kChunksPerRow;
-            stage[c] = fetch_x_chunk<XT, XVEC>(a, tile * kLinearTileRows + rr, 8 * cc);
+            stage[c] = fetch_x_chunk<XT, XVEC>(a, tile * kTileRows + rr, 8 * cc);
         }
     };
     auto write_stage = [&](int buf) {
@@ -197,18 +204,18 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         // counter is concerned, so the order below matters: the row mask
         // bytes (needed first) are requested before the next tile's x, and the
         // next tile's x is consumed before this tile's y stores are issued.
-        bool keep[2];
+        bool keep[MB];
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-            const int64_t m = tile * kLinearTileRows + mb * 32 + (lane & 31);
+        for (int mb = 0; mb < MB; ++mb) {
+            const int64_t m = tile * kTileRows + mb * 32 + (lane & 31);
             keep[mb] = m < a.rows && (a.row_mask == nullptr || a.row_mask[m < a.rows ? m : 0] != 0);
         }
         if (next < a.tiles) {
             load_stage(next);
         }
-        f32x16 acc[2];
+        f32x16 acc[MB];
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 acc[mb][i] = 0.0f;
@@ -217,12 +224,12 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         // Operand reads run one group of two K steps ahead of the MFMAs, so
         // at most eight x fragments are live next to the resident W slice.
         constexpr int kGroup = 2;
-        u32x4 xb[2][kGroup][2];
+        u32x4 xb[2][kGroup][MB];
         auto read_group = [&](int slot, int k_base) {
 #pragma unroll
             for (int ks = 0; ks < kGroup; ++ks) {
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
+                for (int mb = 0; mb < MB; ++mb) {
                     xb[slot][ks][mb] = *reinterpret_cast<const u32x4*>(
                         &s_x[buf][(mb * 32 + (lane & 31)) * KP + 16 * (k_base + ks) + 8 * half]);
                 }
@@ -238,7 +245,7 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
 #pragma unroll
             for (int ks = 0; ks < kGroup; ++ks) {
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
+                for (int mb = 0; mb < MB; ++mb) {
                     acc[mb] = mfma32x32x16(wreg[k2 + ks], xb[slot][ks][mb], acc[mb]);
                 }
             }
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         // rounded and staged in LDS, then written back row by row so that
         // each store instruction covers whole contiguous row segments.
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < MB; ++mb) {
             const int mr = mb * 32 + (lane & 31);
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
                 const int chunk = tid + i * kThreads;
                 const int mr = chunk / (kGroupColumns / 8);
                 const int c8 = 8 * (chunk - mr * (kGroupColumns / 8));
-                const int64_t m = tile * kLinearTileRows + mr;
+                const int64_t m = tile * kTileRows + mr;
                 const int64_t n = col0 + c8;
                 if (m < a.rows && n < N) {
                     const u32x4 v = *reinterpret_cast<const u32x4*>(&s_y[mr * YP + c8]);
@@ -341,6 +348,7 @@ hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dt
         case 16: return launch_linear_k<16>(a, x_dtype, y_dtype, grid, stream);
         case 24: return launch_linear_k<24>(a, x_dtype, y_dtype, grid, stream);
         case 32: return launch_linear_k<32>(a, x_dtype, y_dtype, grid, stream);
+        case 40: return launch_linear_k<40>(a, x_dtype, y_dtype, grid, stream);
         default: return hipErrorInvalidValue;
     }
 }

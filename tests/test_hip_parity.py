@@ -237,6 +237,8 @@ def test_linear_strides_and_tails(native, dtype) -> None:
         (520, 192, 240, torch.float16, torch.bfloat16),
         (77, 96, 144, torch.float16, torch.float16),
         (130, 512, 64, torch.bfloat16, torch.bfloat16),
+        (4099, 640, 256, torch.bfloat16, torch.float16),
+        (70, 600, 72, torch.float16, torch.bfloat16),
         (33, 34, 98, torch.float16, torch.bfloat16),
     ],
 )

@@ -142,9 +142,9 @@ def test_linear_validation(library) -> None:
     assert library.lsso_hip_linear_workspace_bytes(10, 256, 512, ctypes.byref(size)) == 0
     assert size.value == 0
     assert library.lsso_hip_linear_workspace_bytes(-1, 256, 512, ctypes.byref(size)) == -1
-    status = library.lsso_hip_linear(None, 1, 4, 600, 600, None, None, None, 8, None, 1, None, 0, None)
+    status = library.lsso_hip_linear(None, 1, 4, 700, 700, None, None, None, 8, None, 1, None, 0, None)
     assert status == -2
-    assert "in_features <= 512" in _message(library)
+    assert "in_features <= 640" in _message(library)
 
 
 def test_grad_columns_validation(library) -> None:
