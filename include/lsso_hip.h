@@ -199,7 +199,9 @@ int lsso_hip_layer_workspace_bytes(const lsso_hip_mixer_shape* shape, int positi
  *   mixed  = the mixer of lsso_hip_mixer_forward on packed
  *   y      = cast(bf16(mixed) out_weight^T + out_bias)  (row_mask rows -> 0)
  * The input projection runs fused with the mixer's token reductions (one pass
- * over x per head group) and the output projection fused with the apply when
+ * over x per head group) at rank <= 32, and as its own kernel before the
+ * reductions from rank 48 on, where that is faster; the output projection
+ * runs fused with the apply when
  * lsso_hip_mixer_projected_supported() allows, so packed is read back once
  * and mixed never reaches HBM.  The result is bitwise that of lsso_hip_linear,
  * lsso_hip_mixer_forward and lsso_hip_linear in sequence.  in_weight: float32
@@ -261,6 +263,41 @@ int lsso_hip_layer_forward_timed(const lsso_hip_mixer_shape* shape,
                                  size_t workspace_bytes,
                                  void* stream,
                                  void* const* events);
+
+/* Training forward of the input projection and the mixer, one call:
+ *   packed = lsso_hip_linear(x, in_weight, in_bias, row_mask) (BF16),
+ *   mixed  = lsso_hip_mixer_forward(packed, ..., tape),
+ * with the projection fused with the token reductions at rank <= 32 (so x is
+ * read once and packed is written once, then read once more by the apply)
+ * and run as its own kernel from rank 48 on, where that is faster.  Both outputs
+ * and the tape are bitwise those of the two calls; packed and the tape are
+ * what lsso_hip_mixer_backward and the projection's backward need.  Shapes as
+ * lsso_hip_layer_supported (ask it first); x: [batch, length, H*head_dim] of
+ * x_dtype, 16-byte aligned; packed: BF16 [batch, length, H*(rank+head_dim)],
+ * 16-byte aligned; mixed: BF16 [batch, length, H*head_dim]; tape: NULL or
+ * lsso_hip_mixer_tape_floats() floats.  The workspace is that of
+ * lsso_hip_mixer_forward.
+ * Replaces: tensor_core_linear followed by fast_mix under autograd in
+ * LSSO._forward_cuda (lsso/ball/model.py:270-405; lsso/ball/cuda.py:220-255). */
+int lsso_hip_project_mix_forward(const lsso_hip_mixer_shape* shape,
+                                 const void* x,
+                                 int x_dtype,
+                                 const float* in_weight,
+                                 const float* in_bias,
+                                 const uint8_t* row_mask,
+                                 const float* core_base_raw,
+                                 const float* core_drive_weight,
+                                 const float* eta_raw,
+                                 const float* inverse_frequency,
+                                 const float* centered_positions,
+                                 int positions_mode,
+                                 const float* valid_counts,
+                                 void* packed,
+                                 void* mixed,
+                                 float* tape,
+                                 void* workspace,
+                                 size_t workspace_bytes,
+                                 void* stream);
 
 /* Device scratch bytes needed by lsso_hip_linear. */
 int lsso_hip_linear_workspace_bytes(int64_t rows, int64_t in_features,

@@ -54,6 +54,7 @@ _SYMBOLS = (
     "lsso_hip_layer_workspace_bytes",
     "lsso_hip_layer_forward",
     "lsso_hip_layer_forward_timed",
+    "lsso_hip_project_mix_forward",
 )
 
 
@@ -132,6 +133,14 @@ def _declare(library: ctypes.CDLL) -> None:
     library.lsso_hip_layer_forward_timed.argtypes = [
         *library.lsso_hip_layer_forward.argtypes, ctypes.POINTER(ctypes.c_void_p),
     ]  # ... as lsso_hip_layer_forward, then hipEvent_t events[8]
+
+
+    library.lsso_hip_project_mix_forward.restype = ctypes.c_int
+    library.lsso_hip_project_mix_forward.argtypes = [
+        shape_p, vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp, vp,
+        ctypes.c_size_t, vp,
+    ]  # shape, x, x_dtype, in_weight, in_bias, row_mask, base, drive, eta, inv_freq, positions,
+    #    mode, counts, packed, mixed, tape, workspace, workspace_bytes, stream
 
 
 def default_library_path() -> Path:
@@ -859,6 +868,167 @@ def layer_forward(
     return output
 
 
+def _project_mix_forward(
+    x: torch.Tensor,
+    in_weight: torch.Tensor,
+    in_bias: torch.Tensor | None,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None,
+    valid_counts: torch.Tensor | None,
+    row_mask: torch.Tensor | None,
+    record_tape: bool,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """(packed, mixed, tape) of lsso_hip_project_mix_forward (no autograd)."""
+
+    library = _library()
+    shape, mode = _layer_shape(
+        x, in_weight, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+    )
+    device = x.device
+    width = in_weight.shape[0]
+    dtype_codes = {torch.float16: _F16, torch.bfloat16: _BF16}
+    if x.dtype not in dtype_codes:
+        raise TypeError("the fused projection + mixer supports float16/bfloat16 x")
+    if in_bias is not None and (in_bias.dtype != torch.float32 or tuple(in_bias.shape) != (width,)):
+        raise TypeError(f"in_bias must be float32 [{width}]")
+    _require_device_tensor(in_weight, "in_weight", device)
+    if in_bias is not None:
+        _require_device_tensor(in_bias, "in_bias", device)
+    in_weight = in_weight.contiguous()
+    in_bias = None if in_bias is None else in_bias.contiguous()
+    mask_ptr = None
+    if row_mask is not None:
+        if row_mask.dtype != torch.bool or tuple(row_mask.shape) != (shape.batch, shape.length):
+            raise ValueError("row_mask must be a bool [B, N] tensor")
+        row_mask = row_mask.contiguous()
+        mask_ptr = row_mask.data_ptr()
+    workspace_bytes = ctypes.c_size_t()
+    _check(library.lsso_hip_mixer_workspace_bytes(ctypes.byref(shape), mode, ctypes.byref(workspace_bytes)), library)
+    workspace = torch.empty(workspace_bytes.value, dtype=torch.uint8, device=device)
+    packed = torch.empty((shape.batch, shape.length, width), dtype=torch.bfloat16, device=device)
+    mixed = torch.empty(
+        (shape.batch, shape.length, shape.heads * shape.head_dim), dtype=torch.bfloat16, device=device
+    )
+    tape = None
+    if record_tape:
+        floats = ctypes.c_size_t()
+        _check(library.lsso_hip_mixer_tape_floats(ctypes.byref(shape), ctypes.byref(floats)), library)
+        tape = torch.empty(floats.value, dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        status = library.lsso_hip_project_mix_forward(
+            ctypes.byref(shape),
+            x.data_ptr(),
+            dtype_codes[x.dtype],
+            in_weight.data_ptr(),
+            None if in_bias is None else in_bias.data_ptr(),
+            mask_ptr,
+            core_base_raw.data_ptr(),
+            core_drive_weight.data_ptr(),
+            eta_raw.data_ptr(),
+            ctypes.cast(_inverse_frequency(shape.rank), ctypes.c_void_p),
+            None if centered_positions is None else centered_positions.data_ptr(),
+            mode,
+            None if valid_counts is None else valid_counts.data_ptr(),
+            packed.data_ptr(),
+            mixed.data_ptr(),
+            None if tape is None else tape.data_ptr(),
+            workspace.data_ptr(),
+            workspace_bytes.value,
+            _stream(device),
+        )
+    _check(status, library)
+    return packed, mixed, tape
+
+
+class _ProjectMix(torch.autograd.Function):
+    """Autograd of the input projection and the mixer run as one native call
+    (lsso_hip_project_mix_forward).  The backward is the mixer VJP
+    (cuda.py:256-280) followed by the projection VJP (reference.py:205-247),
+    exactly as when the two run separately."""
+
+    @staticmethod
+    def forward(ctx, x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw,
+                centered_positions, valid_counts, row_mask):
+        with torch.no_grad():
+            packed, mixed, tape = _project_mix_forward(
+                x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw,
+                centered_positions, valid_counts, row_mask, True,
+            )
+        ctx.save_for_backward(x, in_weight, packed, core_base_raw, core_drive_weight, eta_raw, tape, row_mask)
+        ctx.centered_positions = centered_positions
+        ctx.valid_counts = valid_counts
+        ctx.has_bias = in_bias is not None
+        ctx.bias_dtype = None if in_bias is None else in_bias.dtype
+        return mixed
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_mixed):
+        x, in_weight, packed, core_base_raw, core_drive_weight, eta_raw, tape, row_mask = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        grad_packed, grad_base, grad_drive, grad_eta = backward(
+            grad_mixed.to(dtype=torch.bfloat16),
+            packed,
+            core_base_raw,
+            core_drive_weight,
+            eta_raw,
+            tape,
+            ctx.centered_positions,
+            ctx.valid_counts,
+        )
+        grad_x, grad_weight, grad_bias = _linear_vjp(
+            grad_packed, x, in_weight, row_mask, needs[0], needs[1], ctx.has_bias and needs[2],
+            ctx.bias_dtype,
+        )
+        return (
+            grad_x,
+            grad_weight,
+            grad_bias,
+            grad_base if needs[3] else None,
+            grad_drive if needs[4] else None,
+            grad_eta if needs[5] else None,
+            None,
+            None,
+            None,
+        )
+
+
+def project_mix(
+    x: torch.Tensor,
+    in_weight: torch.Tensor,
+    in_bias: torch.Tensor | None,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    centered_positions: torch.Tensor | None = None,
+    valid_counts: torch.Tensor | None = None,
+    row_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """mixed = fast_mix(linear(x, in_weight, in_bias, bf16, row_mask), ...)
+    in one native call, bitwise that of the two (the input projection runs
+    fused with the token reductions).  Differentiable (first order) when
+    autograd needs it; ask ``layer_supported`` first."""
+
+    for name, value in (("centered_positions", centered_positions), ("valid_counts", valid_counts)):
+        if value is not None and value.requires_grad:
+            raise ValueError(f"the LSSO HIP fast path does not support gradients for {name}")
+    require_available()
+    if torch.is_grad_enabled() and _any_requires_grad(
+        x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw
+    ):
+        return _ProjectMix.apply(
+            x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw,
+            centered_positions, valid_counts, row_mask,
+        )
+    _packed, mixed, _tape = _project_mix_forward(
+        x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw,
+        centered_positions, valid_counts, row_mask, False,
+    )
+    return mixed
+
+
 def _linear_forward(
     value: torch.Tensor,
     weight: torch.Tensor,
@@ -1013,43 +1183,63 @@ class _Linear(torch.autograd.Function):
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad_output):
         value, weight, row_mask = ctx.saved_tensors
-        out_features, in_features = weight.shape
-        flat_grad = grad_output.reshape(-1, out_features)
-        if flat_grad.stride(-1) != 1 or flat_grad.dtype not in (torch.float16, torch.bfloat16):
-            flat_grad = flat_grad.to(dtype=torch.bfloat16).contiguous()
-        native_value = value.dtype in (torch.float16, torch.bfloat16) and out_features <= 640
-        need_value = ctx.needs_input_grad[0]
-        need_weight = ctx.needs_input_grad[1]
-        need_bias = ctx.has_bias and ctx.needs_input_grad[2]
-        need_bf16 = need_weight or (need_value and not native_value)
-        copy_grad = need_bf16 and (flat_grad.dtype != torch.bfloat16 or row_mask is not None)
-        grad_bf16, grad_sums = None, None
-        if copy_grad or need_bias:
-            grad_bf16, grad_sums = _grad_columns(flat_grad, row_mask, copy_grad, need_bias)
-        if need_bf16 and grad_bf16 is None:
-            grad_bf16 = flat_grad
-        grad_value = grad_weight = grad_bias = None
-        if need_value:
-            if native_value:
-                grad_value = _linear_forward(
-                    flat_grad, weight.mT.contiguous(), None, value.dtype,
-                    None if row_mask is None else row_mask.reshape(-1),
-                ).reshape(value.shape)
-            else:
-                grad_value = _mm_fp32(grad_bf16, weight.to(dtype=torch.bfloat16))
-                grad_value = grad_value.to(dtype=value.dtype).reshape(value.shape)
-        if need_weight:
-            flat_value = value.reshape(-1, in_features)
-            if flat_value.dtype in (torch.float16, torch.bfloat16) and flat_value.stride(-1) == 1 and (
-                flat_value.dtype != torch.bfloat16 or row_mask is not None
-            ):
-                flat_value, _ = _grad_columns(flat_value, row_mask, True, False)
-            else:
-                flat_value = flat_value.to(dtype=torch.bfloat16)
-            grad_weight = _weight_gradient(grad_bf16, flat_value).to(dtype=weight.dtype)
-        if need_bias:
-            grad_bias = grad_sums.to(dtype=ctx.bias_dtype)
+        grad_value, grad_weight, grad_bias = _linear_vjp(
+            grad_output, value, weight, row_mask, ctx.needs_input_grad[0],
+            ctx.needs_input_grad[1], ctx.has_bias and ctx.needs_input_grad[2], ctx.bias_dtype,
+        )
         return grad_value, grad_weight, grad_bias, None, None
+
+
+def _linear_vjp(
+    grad_output: torch.Tensor,
+    value: torch.Tensor,
+    weight: torch.Tensor,
+    row_mask: torch.Tensor | None,
+    need_value: bool,
+    need_weight: bool,
+    need_bias: bool,
+    bias_dtype: torch.dtype | None,
+):
+    """(dX, dW, db) of y = cast(bf16(x) bf16(W)^T + b) (reference.py:205-247).
+
+    One native pass over dY writes its BF16 copy (excluded rows zero) for
+    the weight gradient and its FP32 column sums for the bias gradient; dX
+    runs on the native projection kernel from dY in its own dtype."""
+
+    out_features, in_features = weight.shape
+    flat_grad = grad_output.reshape(-1, out_features)
+    if flat_grad.stride(-1) != 1 or flat_grad.dtype not in (torch.float16, torch.bfloat16):
+        flat_grad = flat_grad.to(dtype=torch.bfloat16).contiguous()
+    native_value = value.dtype in (torch.float16, torch.bfloat16) and out_features <= 640
+    need_bf16 = need_weight or (need_value and not native_value)
+    copy_grad = need_bf16 and (flat_grad.dtype != torch.bfloat16 or row_mask is not None)
+    grad_bf16, grad_sums = None, None
+    if copy_grad or need_bias:
+        grad_bf16, grad_sums = _grad_columns(flat_grad, row_mask, copy_grad, need_bias)
+    if need_bf16 and grad_bf16 is None:
+        grad_bf16 = flat_grad
+    grad_value = grad_weight = grad_bias = None
+    if need_value:
+        if native_value:
+            grad_value = _linear_forward(
+                flat_grad, weight.mT.contiguous(), None, value.dtype,
+                None if row_mask is None else row_mask.reshape(-1),
+            ).reshape(value.shape)
+        else:
+            grad_value = _mm_fp32(grad_bf16, weight.to(dtype=torch.bfloat16))
+            grad_value = grad_value.to(dtype=value.dtype).reshape(value.shape)
+    if need_weight:
+        flat_value = value.reshape(-1, in_features)
+        if flat_value.dtype in (torch.float16, torch.bfloat16) and flat_value.stride(-1) == 1 and (
+            flat_value.dtype != torch.bfloat16 or row_mask is not None
+        ):
+            flat_value, _ = _grad_columns(flat_value, row_mask, True, False)
+        else:
+            flat_value = flat_value.to(dtype=torch.bfloat16)
+        grad_weight = _weight_gradient(grad_bf16, flat_value).to(dtype=weight.dtype)
+    if need_bias:
+        grad_bias = grad_sums.to(dtype=bias_dtype)
+    return grad_value, grad_weight, grad_bias
 
 
 def linear(
@@ -1084,5 +1274,6 @@ __all__ = [
     "load",
     "mix_project",
     "mix_project_supported",
+    "project_mix",
     "require_available",
 ]

@@ -303,6 +303,27 @@ class LSSO(nn.Module):
                 self.w_o.bias,
                 row_mask=mask,
             )
+        if needs_grad and x.is_contiguous() and hip.layer_supported(
+            x, self.w_bc.weight, self.core_base_raw, self.core_drive_weight, self.eta_raw
+        ):
+            # Training: the input projection runs fused with the token
+            # reductions (one read of x, one write of the packed projection),
+            # bitwise equal to the separate linear + fast_mix below.
+            centered_positions, valid_counts, mask = self._native_geometry(
+                x, valid_mask, position_ids
+            )
+            mixed = hip.project_mix(
+                x,
+                self.w_bc.weight,
+                self.w_bc.bias,
+                self.core_base_raw,
+                self.core_drive_weight,
+                self.eta_raw,
+                centered_positions,
+                valid_counts,
+                row_mask=mask,
+            )
+            return hip.linear(mixed, self.w_o.weight, self.w_o.bias, x.dtype, row_mask=mask)
         projected, centered_positions, valid_counts, mask = self._native_inputs(
             x, valid_mask, position_ids
         )

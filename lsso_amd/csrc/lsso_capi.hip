@@ -252,6 +252,9 @@ int run_solve(const MixerPlan& plan, const MixerBuffers& buf, const float* core_
 
 // Phase table, L-reductions and the compact solve: everything up to the
 // apply operand records.
+int run_reduce(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
+               int positions_mode, bool vec, hipStream_t stream);
+
 int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
                 const float* core_base_raw, const float* core_drive_weight, const float* eta_raw,
                 const float* inverse_frequency, const float* centered_positions,
@@ -261,6 +264,17 @@ int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* proj
     if (status != LSSO_HIP_OK) {
         return status;
     }
+    status = run_reduce(plan, buf, projected, positions_mode, vec, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    return run_solve(plan, buf, core_base_raw, core_drive_weight, eta_raw, valid_counts, tape,
+                     stream);
+}
+
+// The token reductions of packed (G and S partials per chunk).
+int run_reduce(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
+               int positions_mode, bool vec, hipStream_t stream) {
     lsso_hip::ReduceArgs reduce{};
     reduce.projected = static_cast<const uint16_t*>(projected);
     reduce.content = static_cast<const uint16_t*>(projected) + plan.heads * plan.rank;
@@ -281,11 +295,7 @@ int run_compact(const MixerPlan& plan, const MixerBuffers& buf, const void* proj
     reduce.total_waves = plan.batch * plan.heads * plan.reduce_chunks * plan.column_groups;
     const hipError_t error =
         lsso_hip::launch_reduce(static_cast<int>(plan.rank), reduce, plan.cpw, vec, stream);
-    if (error != hipSuccess) {
-        return hip_failure(error, "reduce_kernel launch");
-    }
-    return run_solve(plan, buf, core_base_raw, core_drive_weight, eta_raw, valid_counts, tape,
-                     stream);
+    return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "reduce_kernel launch");
 }
 
 int run_apply(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
@@ -907,6 +917,9 @@ int layer_forward_impl(const lsso_hip_mixer_shape* shape, const void* x, int x_d
                        const float* valid_counts, const float* out_weight, const float* out_bias,
                        void* y, int y_dtype, void* workspace, size_t workspace_bytes,
                        void* stream_handle, void* const* events);
+int run_project_reduce(const MixerPlan& plan, const MixerBuffers& buf, const void* x, int x_dtype,
+                       const float* in_weight, const float* in_bias, const uint8_t* row_mask,
+                       void* packed, int positions_mode, int group_heads, hipStream_t stream);
 
 }  // namespace
 
@@ -969,9 +982,124 @@ int lsso_hip_layer_forward_timed(const lsso_hip_mixer_shape* shape, const void* 
                               workspace, workspace_bytes, stream_handle, events);
 }
 
+int lsso_hip_project_mix_forward(const lsso_hip_mixer_shape* shape, const void* x, int x_dtype,
+                                 const float* in_weight, const float* in_bias,
+                                 const uint8_t* row_mask, const float* core_base_raw,
+                                 const float* core_drive_weight, const float* eta_raw,
+                                 const float* inverse_frequency, const float* centered_positions,
+                                 int positions_mode, const float* valid_counts, void* packed,
+                                 void* mixed, float* tape, void* workspace, size_t workspace_bytes,
+                                 void* stream_handle) {
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    const int group_heads = layer_group_heads(plan);
+    if (group_heads == 0) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "the fused projection + mixer supports head_dim a multiple of 16 up to 64 and "
+                    "H*head_dim <= 384; use lsso_hip_linear and lsso_hip_mixer_forward");
+    }
+    if (x_dtype != LSSO_HIP_F16 && x_dtype != LSSO_HIP_BF16) {
+        return fail(LSSO_HIP_EINVAL, "x_dtype must be LSSO_HIP_F16 or LSSO_HIP_BF16");
+    }
+    if (x == nullptr || in_weight == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "x and in_weight must not be NULL");
+    }
+    if (!aligned(x, 16) || !aligned(packed, 16)) {
+        return fail(LSSO_HIP_EINVAL, "x and packed must be 16-byte aligned");
+    }
+    MixerBuffers buf{};
+    status = check_mixer_call(plan, packed, core_base_raw, core_drive_weight, eta_raw, mixed,
+                              centered_positions, positions_mode, workspace, workspace_bytes, &buf);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    status = run_phase(plan, buf, inverse_frequency, centered_positions, positions_mode, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    status = run_project_reduce(plan, buf, x, x_dtype, in_weight, in_bias, row_mask, packed,
+                                positions_mode, group_heads, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    status = run_solve(plan, buf, core_base_raw, core_drive_weight, eta_raw, valid_counts, tape,
+                       stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    return run_apply(plan, buf, packed, eta_raw, positions_mode, mixed,
+                     vector_rows(plan, packed, mixed), stream);
+}
+
 }  // extern "C"
 
 namespace {
+
+// The fused projection + reduce reads x once per head group.  From rank 48
+// on (three or more groups at H*d = 256, and register spills in those
+// instantiations) the separate projection and reduce are faster: at B = 64,
+// N = 2048, H = 8, d = 32 the projection, phase table, reduce and solve took
+// 125 / 154 / 349 / 463 us fused against 143 / 172 / 272 / 397 us separate for
+// rank 16 / 32 / 48 / 64.
+bool fused_projection_pays(const MixerPlan& plan) { return plan.rank <= 32; }
+
+// The input projection and the token reductions: writes `packed` (bitwise
+// lsso_hip_linear's output) and the reduce partials of buf (bitwise
+// reduce_kernel's), fused in one kernel where that pays.
+int run_project_reduce(const MixerPlan& plan, const MixerBuffers& buf, const void* x, int x_dtype,
+                       const float* in_weight, const float* in_bias, const uint8_t* row_mask,
+                       void* packed, int positions_mode, int group_heads, hipStream_t stream) {
+    if (!fused_projection_pays(plan)) {
+        const int status = run_linear(x, x_dtype, plan.batch * plan.length, plan.out_width,
+                                      plan.out_width, in_weight, in_bias, row_mask, plan.width,
+                                      packed, LSSO_HIP_BF16, stream);
+        if (status != LSSO_HIP_OK) {
+            return status;
+        }
+        return run_reduce(plan, buf, packed, positions_mode, vector_rows(plan, packed, packed),
+                          stream);
+    }
+    int units = 0;
+    const int status = compute_units(&units);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    lsso_hip::ProjectReduceArgs pr{};
+    pr.x = x;
+    pr.weight = in_weight;
+    pr.bias = in_bias;
+    pr.row_mask = row_mask;
+    pr.phases = buf.phases;
+    pr.phase_batch_stride = phase_batch_stride(plan, positions_mode);
+    pr.packed = static_cast<uint16_t*>(packed);
+    pr.partials = buf.partials;
+    pr.batch = plan.batch;
+    pr.length = plan.length;
+    pr.heads = plan.heads;
+    pr.head_dim = plan.head_dim;
+    pr.in_features = plan.out_width;
+    pr.width = plan.width;
+    pr.chunks = plan.reduce_chunks;
+    pr.chunk_tokens = plan.reduce_chunk_tokens;
+    pr.partial_stride = plan.partial_stride;
+    pr.group_heads = group_heads;
+    pr.head_groups = ceil_div(plan.heads, group_heads);
+    // One persistent workgroup per compute unit; the blocks of the head
+    // groups of one item are dealt to the same XCD when the count allows.
+    const int64_t items = plan.batch * plan.reduce_chunks;
+    int64_t per_group = units / pr.head_groups;
+    if (per_group < 1) per_group = 1;
+    if (per_group > items) per_group = items;
+    if (per_group >= 8) per_group -= per_group % 8;
+    const hipError_t error = lsso_hip::launch_project_reduce(
+        static_cast<int>(plan.rank), pr, x_dtype, static_cast<int>(per_group * pr.head_groups),
+        stream);
+    return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "project_reduce_kernel launch");
+}
 
 int layer_forward_impl(const lsso_hip_mixer_shape* shape, const void* x, int x_dtype,
                        const float* in_weight, const float* in_bias, const uint8_t* row_mask,
@@ -1036,46 +1164,13 @@ int layer_forward_impl(const lsso_hip_mixer_shape* shape, const void* x, int x_d
         return status;
     }
 
-    int units = 0;
-    status = compute_units(&units);
-    if (status != LSSO_HIP_OK) {
-        return status;
-    }
-    lsso_hip::ProjectReduceArgs pr{};
-    pr.x = x;
-    pr.weight = in_weight;
-    pr.bias = in_bias;
-    pr.row_mask = row_mask;
-    pr.phases = buf.phases;
-    pr.phase_batch_stride = phase_batch_stride(plan, positions_mode);
-    pr.packed = static_cast<uint16_t*>(packed);
-    pr.partials = buf.partials;
-    pr.batch = plan.batch;
-    pr.length = plan.length;
-    pr.heads = plan.heads;
-    pr.head_dim = plan.head_dim;
-    pr.in_features = plan.out_width;
-    pr.width = plan.width;
-    pr.chunks = plan.reduce_chunks;
-    pr.chunk_tokens = plan.reduce_chunk_tokens;
-    pr.partial_stride = plan.partial_stride;
-    pr.group_heads = group_heads;
-    pr.head_groups = ceil_div(plan.heads, group_heads);
-    // One persistent workgroup per compute unit; the blocks of the head
-    // groups of one item are dealt to the same XCD when the count allows.
-    const int64_t items = plan.batch * plan.reduce_chunks;
-    int64_t per_group = units / pr.head_groups;
-    if (per_group < 1) per_group = 1;
-    if (per_group > items) per_group = items;
-    if (per_group >= 8) per_group -= per_group % 8;
     if ((status = mark(2)) != LSSO_HIP_OK) {
         return status;
     }
-    const hipError_t error = lsso_hip::launch_project_reduce(
-        static_cast<int>(plan.rank), pr, x_dtype, static_cast<int>(per_group * pr.head_groups),
-        stream);
-    if (error != hipSuccess) {
-        return hip_failure(error, "project_reduce_kernel launch");
+    status = run_project_reduce(plan, buf, x, x_dtype, in_weight, in_bias, row_mask, packed,
+                                positions_mode, group_heads, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
     }
     if ((status = mark(3)) != LSSO_HIP_OK || (status = mark(4)) != LSSO_HIP_OK) {
         return status;

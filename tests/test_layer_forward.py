@@ -154,3 +154,67 @@ def test_module_runs_the_layer_path_and_matches_the_oracle(native):
     got = y.detach().to(device="cpu", dtype=torch.float64)
     rel = float((got - expected).norm() / expected.norm())
     assert rel <= 5e-3, rel
+
+
+# -- training forward: projection + mixer in one call -------------------------
+@pytest.mark.parametrize(
+    ("batch", "rank", "heads", "head_dim", "length", "masked"),
+    [
+        (2, 48, 8, 32, 333, False),   # C5 geometry
+        (2, 32, 8, 32, 1000, True),
+        (1, 64, 6, 64, 300, True),    # C4 geometry
+        (3, 16, 8, 16, 65, False),
+    ],
+)
+def test_project_mix_is_bitwise_linear_then_forward_train(native, batch, rank, heads, head_dim, length, masked):
+    x, in_w, in_b, base, drive, eta_raw, _out_w, _out_b = _layer_inputs(
+        batch, rank, heads, head_dim, length, seed=5000 + rank + length
+    )
+    positions, counts, mask = None, None, None
+    if masked:
+        generator = torch.Generator().manual_seed(length)
+        valid = torch.randint(length // 4, length + 1, (batch,), generator=generator)
+        mask = (torch.arange(length)[None, :] < valid[:, None]).cuda()
+        counts = valid.float().cuda()
+        starts = torch.randint(0, 1024, (batch, 1), generator=generator).float()
+        raw = starts + torch.arange(length, dtype=torch.float32)[None, :]
+        centre = (raw * mask.cpu()).sum(dim=1, keepdim=True) / valid[:, None]
+        positions = (raw - centre).cuda()
+    with torch.no_grad():
+        assert native.layer_supported(x, in_w, base, drive, eta_raw)
+        packed, mixed, tape = native._project_mix_forward(
+            x, in_w, in_b, base, drive, eta_raw, positions, counts, mask, True
+        )
+        projected = native.linear(x, in_w, in_b, torch.bfloat16, row_mask=mask)
+        expected_mixed, expected_tape = native.forward_train(projected, base, drive, eta_raw, positions, counts)
+    torch.cuda.synchronize()
+    assert torch.equal(packed, projected)
+    assert torch.equal(mixed, expected_mixed)
+    assert torch.equal(tape, expected_tape)
+
+
+def test_project_mix_gradients_equal_the_two_call_path(native):
+    x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(2, 48, 8, 32, 300, seed=77)
+    mask = torch.ones(2, 300, dtype=torch.bool, device="cuda")
+    mask[1, 250:] = False
+    counts = mask.sum(dim=1).float()
+    positions = torch.arange(300, dtype=torch.float32, device="cuda")[None, :].repeat(2, 1)
+    positions = positions - (positions * mask).sum(dim=1, keepdim=True) / counts[:, None]
+    upstream = torch.randn(2, 300, 8 * 32, device="cuda").bfloat16()
+
+    def run(fused: bool):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (x, in_w, in_b, base, drive, eta_raw)]
+        if fused:
+            mixed = native.project_mix(*leaves, positions, counts, row_mask=mask)
+        else:
+            projected = native.linear(leaves[0], leaves[1], leaves[2], torch.bfloat16, row_mask=mask)
+            mixed = native.fast_mix(projected, leaves[3], leaves[4], leaves[5], positions, counts)
+        mixed.backward(upstream)
+        return mixed.detach(), [leaf.grad for leaf in leaves]
+
+    fused_out, fused_grads = run(True)
+    split_out, split_grads = run(False)
+    assert torch.equal(fused_out, split_out)
+    for got, want in zip(fused_grads, split_grads):
+        assert got is not None and torch.isfinite(got).all()
+        assert torch.equal(got, want)
