@@ -605,8 +605,9 @@ __global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
 
 // Token map with the system's records held in registers for the whole chunk
 // (head_dim = 16 D16 and records of at most 112 VGPRs, (3 R d + R^2) / 64):
-// the loop streams only token rows, and each step reads the next 16 tokens'
-// inputs before it computes.  The MFMA chains and the <dY, C> order are those
+// the loop streams only token rows, with each 16-token step's inputs read
+// one step before it computes.  A step's output is staged in the wave's LDS
+// tile and written as 16-byte pieces of each token's dR and dC runs.  The MFMA chains and the <dY, C> order are those
 // of bwd_apply_kernel, so the two kernels agree bitwise.
 template <int R, int D16>
 struct BwdTokenInputs {
@@ -658,7 +659,13 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
     constexpr int DSTEPS = In::kFeatSteps;
     constexpr int D = 16 * D16;
     constexpr int PAIRS = R / 2;
+    // Output tile of a step, per wave: 16 tokens x [dR (R) | dC (D)] in BF16.
+    constexpr int OP = R + D + 8;                     // row pitch (bf16)
+    constexpr int kRowChunks = (R + D) / 8;           // 16-byte pieces per token
+    constexpr int kStorePasses = (16 * kRowChunks + 63) / 64;
+    __shared__ __attribute__((aligned(16))) uint16_t s_out[4][16 * OP];
     const int lane = threadIdx.x & 63;
+    uint16_t* out_tile = s_out[threadIdx.x >> 6];
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (wave >= a.total_waves) {
         return;
@@ -722,11 +729,8 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
     };
 
     float dot = 0.0f;
-    In cur;
-    fetch(cur, begin);
-    for (int64_t t0 = begin; t0 < end; t0 += 16) {
-        In nxt;
-        fetch(nxt, t0 + 16);
+    // One 16-token step from its staged inputs.
+    auto compute = [&](const In& cur, int64_t t0) {
         const int64_t token = t0 + q;
         const bool live = token < end;
         const int64_t safe = live ? token : begin;
@@ -754,7 +758,6 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
             }
         }
 
-        uint16_t* out_row = gout + safe * a.width;
         // dA^T blocks: feature-K chain (dY, C) and rank-K chain (A) kept apart.
 #pragma unroll
         for (int rb = 0; rb < RBLK; ++rb) {
@@ -786,8 +789,9 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
                     acc_r = mfma16x16x16(g_lo[rb][s], a_hi[s], acc_r);
                 }
             }
-            // Lane holds dA[token q][ranks 16 rb + 4 g .. +3]: rotate back.
-            if (live) {
+            // Lane holds dA[token q][ranks 16 rb + 4 g .. +3]: rotate back
+            // into the output tile.
+            {
                 const int rank0 = 16 * rb + 4 * g;
                 u32x2 ph;
                 if constexpr (In::kRK32) {
@@ -809,7 +813,7 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
                     const float odd = gradv[2 * p + 1] * cosine - gradv[2 * p] * sine;
                     packed[p] = pack_bf16(even, odd);
                 }
-                *reinterpret_cast<u32x2*>(out_row + rel_off + rank0) = packed;
+                *reinterpret_cast<u32x2*>(&out_tile[q * OP + rank0]) = packed;
             }
         }
         // dC^T blocks: eta dY + (ds / sqrt(n))^T A^T.
@@ -828,7 +832,7 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
                     acc = mfma16x16x16(f_lo[fb][s], a_hi[s], acc);
                 }
             }
-            if (live) {
+            {
                 const int f0 = 16 * fb + 4 * g;
                 u32x2 dy;
                 if constexpr (In::kDK32) {
@@ -839,10 +843,35 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
                 u32x2 packed;
                 packed.x = pack_bf16(fmaf(eta, bf16_lo(dy.x), acc[0]), fmaf(eta, bf16_hi(dy.x), acc[1]));
                 packed.y = pack_bf16(fmaf(eta, bf16_lo(dy.y), acc[2]), fmaf(eta, bf16_hi(dy.y), acc[3]));
-                *reinterpret_cast<u32x2*>(out_row + content_off + f0) = packed;
+                *reinterpret_cast<u32x2*>(&out_tile[q * OP + R + f0]) = packed;
             }
         }
-        cur = nxt;
+        // The tile goes out as 16-byte pieces of each token's dR and dC runs
+        // (the wave's own LDS region: its reads follow its writes in order).
+#pragma unroll
+        for (int pass = 0; pass < kStorePasses; ++pass) {
+            const int idx = lane + 64 * pass;
+            const int row = idx / kRowChunks;
+            const int piece = idx - row * kRowChunks;
+            if (idx < 16 * kRowChunks && t0 + row < end) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(&out_tile[row * OP + 8 * piece]);
+                const int64_t column = 8 * piece < R ? rel_off + 8 * piece : content_off + 8 * piece - R;
+                *reinterpret_cast<u32x4*>(gout + (t0 + row) * a.width + column) = v;
+            }
+        }
+    };
+    // Inputs are read one step ahead, alternating between two stages.
+    In s0;
+    In s1;
+    fetch(s0, begin);
+    for (int64_t t0 = begin; t0 < end; t0 += 32) {
+        fetch(s1, t0 + 16);
+        compute(s0, t0);
+        if (t0 + 16 >= end) {
+            break;
+        }
+        fetch(s0, t0 + 32);
+        compute(s1, t0 + 16);
     }
     // <dY, C> of this wave's tokens.
     for (int offset = 32; offset > 0; offset >>= 1) {
