@@ -784,8 +784,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         bool open = live;
         int own_step = 0;
         float own_pivot = 1.0f;
-#pragma unroll 1
-        for (int k = 0; k < R; ++k) {
+        auto gj_step = [&](int k) {
             const float x = row_get(rowv, k);
             const unsigned magnitude = __float_as_uint(fabsf(x));
             const unsigned best = __builtin_amdgcn_readfirstlane(__ockl_wfred_max_u32(open ? magnitude : 0u));
@@ -803,6 +802,20 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
             }
             if (lane == 0) {
                 s_pivot[k] = p;
+            }
+        };
+        if constexpr (R <= 32) {
+            // Unrolled, the next step's pivot search overlaps the end of the
+            // current step's row updates (from rank 48 on, the unrolled
+            // chain spills registers).
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                gj_step(k);
+            }
+        } else {
+#pragma unroll 1
+            for (int k = 0; k < R; ++k) {
+                gj_step(k);
             }
         }
         if (live) {
