@@ -125,13 +125,15 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
 //   (I + K)^-1                       Gauss-Jordan with partial (row) pivoting
 //   U = (I + K)^-1 Z, X = 2U - (1 + eta) Z, M' = L^-T X / sqrt(n)   products
 //
-// The two factorizations are sequential (one step per rank) and run in wave 0
-// with one matrix row per lane held in registers.  A step's pivot row reaches
-// the other lanes by v_readlane into scalar registers, one element per
-// column, so a step is one chain of VALU instructions with no LDS round trip.
-// Step loops stay rolled (the pivot lane and column are wave-uniform
-// registers); the substitution for L^-1 has no cross-lane traffic and is
-// unrolled.  The products use all four waves.
+// The Cholesky factor is blocked in 8-column panels in wave 0 (the diagonal
+// block and the panel pass through LDS, one row per lane).  Gauss-Jordan runs
+// in wave 0 with one matrix row per lane held in registers: a step's pivot
+// row reaches the other lanes by v_readlane into scalar registers, one
+// element per column, so a step is one chain of VALU instructions with no
+// LDS round trip.  Its step loop is unrolled up to rank 32 (the next pivot
+// search then overlaps the current row updates) and rolled above, where the
+// unrolled chain spills.  The substitution for L^-1 has no cross-lane traffic
+// and is unrolled.  The products use all four waves on FP32 MFMA tiles.
 extern "C" __device__ unsigned int __ockl_wfred_max_u32(unsigned int);
 
 constexpr int kSolveThreads = 256;
