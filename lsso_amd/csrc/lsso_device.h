@@ -177,14 +177,14 @@ struct ApplyLayout {
 // read as float4 pairs when K is a multiple of 4.
 template <int KSTEPS>
 __device__ __forceinline__ void load_weight_row(u32x4 (&wreg)[KSTEPS], const float* weight,
-                                                int64_t n, int64_t K, int lane) {
+                                                int64_t n, int64_t K, int lane, int64_t k_base = 0) {
     const int half = lane >> 5;
     const bool nv = n >= 0;
     const float* wrow = weight + (nv ? n : 0) * K;
     const bool vector_rows = (K % 4) == 0;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-        const int64_t k0 = 16 * ks + 8 * half;
+        const int64_t k0 = k_base + 16 * ks + 8 * half;
         float v[8];
         if (vector_rows && nv && k0 + 8 <= K) {
             const f32x4 lo = *reinterpret_cast<const f32x4*>(wrow + k0);
@@ -238,12 +238,14 @@ __device__ __forceinline__ void load_weight_row_k8(u32x4 (&wreg)[KSTEPS], const 
     }
 }
 
-// Resident slice of rows n0 .. n0 + 31 (one row per lane % 32).
+// Resident slice of rows n0 .. n0 + 31 (one row per lane % 32), columns
+// k_base .. k_base + 16 KSTEPS.
 template <int KSTEPS>
 __device__ __forceinline__ void load_weight_slice(u32x4 (&wreg)[KSTEPS], const float* weight,
-                                                  int64_t N, int64_t K, int64_t n0, int lane) {
+                                                  int64_t N, int64_t K, int64_t n0, int lane,
+                                                  int64_t k_base = 0) {
     const int64_t n = n0 + (lane & 31);
-    load_weight_row<KSTEPS>(wreg, weight, n < N ? n : -1, K, lane);
+    load_weight_row<KSTEPS>(wreg, weight, n < N ? n : -1, K, lane, k_base);
 }
 
 }  // namespace lsso_hip

@@ -5,9 +5,10 @@
 // FP32 accumulation, FP32 bias added to the accumulator, one final FP16 or
 // BF16 store; FP16 output never rounds through BF16.
 //
-// Schedule: persistent workgroups of 8 waves (4 when K > 256).  Each
+// Schedule: persistent workgroups of 8 waves (4 when 256 < K <= 512).  Each
 // wave keeps a 32-column slice of W (BF16, K padded to 16) in registers for
-// the whole launch, so the weights are read once per workgroup.  64-row x
+// the whole launch, so the weights are read once per workgroup; past K = 512
+// two waves share a slice, one per half of K.  64-row x
 // tiles (32-row once K > 512, so that two of them fit LDS) are staged through
 // a double-buffered LDS tile (converted to BF16 once) and shared by the
 // workgroup's waves.
@@ -29,9 +30,13 @@ template <int KSTEPS>
 constexpr int linear_tile_rows_k() { return KSTEPS <= 32 ? 64 : 32; }
 
 // Waves per workgroup: eight (two per SIMD, 256 registers each) while the
-// resident W slice fits; four once K exceeds 256.
+// resident W slice fits; four for K in (256, 512]; eight again past 512,
+// where two waves share each 32-column slice, one per half of K, and add
+// their accumulators through LDS.
 template <int KSTEPS>
-constexpr int linear_waves() { return KSTEPS <= 16 ? 8 : 4; }
+constexpr int linear_waves() { return (KSTEPS <= 16 || KSTEPS > 32) ? 8 : 4; }
+template <int KSTEPS>
+constexpr int linear_ksplit() { return KSTEPS > 32 ? 2 : 1; }
 
 int linear_tile_rows(int k_steps) { return k_steps <= 32 ? 64 : 32; }
 int linear_columns_per_group(int k_steps) { return (k_steps <= 16 ? 8 : 4) * 32; }
@@ -127,9 +132,12 @@ __device__ __forceinline__ uint16_t to_output_bits(float value) {
 template <int KSTEPS, int XT, int YT, bool XVEC>
 __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(LinearArgs a) {
     constexpr int kWaves = linear_waves<KSTEPS>();
+    constexpr int KSPLIT = linear_ksplit<KSTEPS>();
+    constexpr int KW = KSTEPS / KSPLIT;                 // K steps per wave
+    constexpr int kSlices = kWaves / KSPLIT;            // 32-column slices per group
     constexpr int kTileRows = linear_tile_rows_k<KSTEPS>();
     constexpr int MB = kTileRows / 32;                  // 32-row MFMA blocks per tile
-    constexpr int kGroupColumns = kWaves * 32;
+    constexpr int kGroupColumns = kSlices * 32;
     constexpr int KP = 16 * KSTEPS + 8;                  // LDS row pitch (bf16)
     constexpr int kChunksPerRow = 2 * KSTEPS;           // 8-element chunks
     constexpr int kThreads = kWaves * 64;
@@ -141,6 +149,8 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     constexpr int kStoreChunks = kTileRows * kGroupColumns / 8 / kThreads;
     static_assert(kTileRows * kGroupColumns / 8 % kThreads == 0, "store split");
     __shared__ __attribute__((aligned(16))) uint16_t s_y[kTileRows * YP];
+    // Upper-K partial accumulators of a split tile, per slice, block, element and lane.
+    __shared__ float s_part[KSPLIT == 2 ? kSlices * MB * 16 * 64 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -160,12 +170,15 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         group_index = blockIdx.x / a.column_groups;
     }
     const int64_t group_count = gridDim.x / a.column_groups;
-    const int64_t n0 = cg * kGroupColumns + wave * 32;
+    const int slice = wave % kSlices;
+    const int khalf = wave / kSlices;
+    const int kofs = KW * khalf;                        // first K step of this wave
+    const int64_t n0 = cg * kGroupColumns + slice * 32;
     const int64_t K = a.in_features;
     const int64_t N = a.out_features;
 
-    u32x4 wreg[KSTEPS];
-    load_weight_slice<KSTEPS>(wreg, a.weight, N, K, n0, lane);
+    u32x4 wreg[KW];
+    load_weight_slice<KW>(wreg, a.weight, N, K, n0, lane, int64_t{16} * kofs);
     for (int c = tid; c < kGroupColumns; c += kThreads) {
         const int64_t n = cg * kGroupColumns + c;
         s_bias[c] = (a.bias != nullptr && n < N) ? a.bias[n] : 0.0f;
@@ -231,15 +244,15 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
                     xb[slot][ks][mb] = *reinterpret_cast<const u32x4*>(
-                        &s_x[buf][(mb * 32 + (lane & 31)) * KP + 16 * (k_base + ks) + 8 * half]);
+                        &s_x[buf][(mb * 32 + (lane & 31)) * KP + 16 * (kofs + k_base + ks) + 8 * half]);
                 }
             }
         };
         read_group(0, 0);
 #pragma unroll
-        for (int k2 = 0; k2 < KSTEPS; k2 += kGroup) {
+        for (int k2 = 0; k2 < KW; k2 += kGroup) {
             const int slot = (k2 / kGroup) & 1;
-            if (k2 + kGroup < KSTEPS) {
+            if (k2 + kGroup < KW) {
                 read_group(slot ^ 1, k2 + kGroup);
             }
 #pragma unroll
@@ -251,16 +264,42 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (KSPLIT == 2) {
+            // The upper-K waves hand their accumulators to the lower-K waves
+            // of the same slice, which add them (lower + upper) and finish.
+            if (khalf == 1) {
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        s_part[((slice * MB + mb) * 16 + i) * 64 + lane] = acc[mb][i];
+                    }
+                }
+            }
+            __syncthreads();
+            if (khalf == 0) {
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        acc[mb][i] += s_part[((slice * MB + mb) * 16 + i) * 64 + lane];
+                    }
+                }
+            }
+        }
         // y^T block: lane holds row m = lane%32 of the 32-row block and
         // features n0 + 8 q + 4 half + r for q, r in 0..3.  The tile is
         // rounded and staged in LDS, then written back row by row so that
         // each store instruction covers whole contiguous row segments.
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
+            if (khalf != 0) {
+                break;   // wave-uniform: the upper-K waves have handed over
+            }
             const int mr = mb * 32 + (lane & 31);
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
-                const int c = wave * 32 + 8 * qd + 4 * half;
+                const int c = slice * 32 + 8 * qd + 4 * half;
                 const f32x4 bias = *reinterpret_cast<const f32x4*>(&s_bias[c]);
                 const float v0 = keep[mb] ? acc[mb][4 * qd + 0] + bias[0] : 0.0f;
                 const float v1 = keep[mb] ? acc[mb][4 * qd + 1] + bias[1] : 0.0f;
