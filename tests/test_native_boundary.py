@@ -147,6 +147,36 @@ def test_linear_validation(library) -> None:
     assert "in_features <= 640" in _message(library)
 
 
+def test_project_mix_forward_validates_before_launch(library) -> None:
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    # head_dim 17 is outside the fused envelope (a multiple of 16 is needed).
+    status = library.lsso_hip_project_mix_forward(
+        ctypes.byref(_shape()), fake, 1, fake, None, None, fake, fake, fake, None, None, 0, None,
+        fake, fake, None, fake, 1 << 30, None,
+    )
+    assert status == -2
+    assert "lsso_hip_linear and lsso_hip_mixer_forward" in _message(library)
+    shape = _shape(heads=8, rank=48, head_dim=32)
+    status = library.lsso_hip_project_mix_forward(
+        ctypes.byref(shape), fake, 3, fake, None, None, fake, fake, fake, None, None, 0, None,
+        fake, fake, None, fake, 1 << 30, None,
+    )
+    assert status == -1
+    assert "x_dtype" in _message(library)
+    status = library.lsso_hip_project_mix_forward(
+        ctypes.byref(shape), None, 1, fake, None, None, fake, fake, fake, None, None, 0, None,
+        fake, fake, None, fake, 1 << 30, None,
+    )
+    assert status == -1
+    assert "must not be NULL" in _message(library)
+    status = library.lsso_hip_project_mix_forward(
+        ctypes.byref(shape), fake, 1, fake, None, None, fake, fake, fake, None, None, 0, None,
+        fake, fake, None, fake, 16, None,
+    )
+    assert status == -1
+    assert "workspace" in _message(library)
+
+
 def test_grad_columns_validation(library) -> None:
     size = ctypes.c_size_t()
     assert library.lsso_hip_linear_grad_columns_workspace_bytes(0, 256, ctypes.byref(size)) == 0
