@@ -42,6 +42,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--workload", choices=("forward", "train"), default="forward",
                         help="forward: the headline mixer forward (r=32); train: forward + "
                              "first-order backward of loss = mean(y^2) at r=48 (config C5)")
+    parser.add_argument("--rank", type=int, default=None, choices=(16, 32, 48, 64),
+                        help="--workload train only: rank (default 48, config C5; 32 is the "
+                             "shell of the reference's published fwd+bwd numbers)")
     parser.add_argument("--cpu-samples", type=int, default=64,
                         help="sequences of the workload timed on the CPU oracle (0 skips)")
     parser.add_argument("--cpu-repeats", type=int, default=7)
@@ -118,13 +121,16 @@ def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> dict
 def train_benchmark(args: argparse.Namespace) -> int:
     """Forward + analytic backward of the complete mixer (config C5: B=64,
     D=256, H=8, r=48, L=2048, FP16 x, loss = mean(y^2), gradients for x and
-    all seven parameters); tokens/s of whole training steps."""
+    all seven parameters); tokens/s of whole training steps.  --rank 32 runs
+    the shell of the reference's published fwd+bwd numbers and reports the
+    ratio to them as vs_baseline."""
 
     from lsso_amd import LSSO, LSSOConfig
 
     device = torch.device("cuda", 0)
     length = 2048 if args.length is None else args.length
-    batch, dim, heads, rank = args.batch, 256, 8, 48
+    rank = 48 if args.rank is None else args.rank
+    batch, dim, heads = args.batch, 256, 8
     torch.manual_seed(0)
     layer = LSSO(LSSOConfig(dim=dim, num_heads=heads, rank=rank, bias=True))
     with torch.no_grad():
@@ -150,9 +156,15 @@ def train_benchmark(args: argparse.Namespace) -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
     tokens = batch * length
+    # The reference publishes fwd+bwd only for the r = 32 shell at B = 64
+    # (RTX 5070 Ti, results/cuda/wall_clock.csv:5-7): B*L / (7.512, 15.260,
+    # 29.160 ms) at L = 1024, 2048, 4096.
+    published = {1024: 64 * 1024 / 7.512e-3, 2048: 64 * 2048 / 15.260e-3, 4096: 64 * 4096 / 29.160e-3}
+    value = tokens * args.steps / elapsed
+    vs_baseline = value / published[length] if rank == 32 and batch == 64 and length in published else None
     result = {
-        "metric": "mixer fwd+bwd tokens/s @B64 D256 H8 r48 L2048 fp16",
-        "value": tokens * args.steps / elapsed,
+        "metric": f"mixer fwd+bwd tokens/s @B{batch} D256 H8 r{rank} L{length} fp16",
+        "value": value,
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -160,9 +172,7 @@ def train_benchmark(args: argparse.Namespace) -> int:
         "ms_per_step": 1e3 * elapsed / args.steps,
         "higher_is_better": True,
         "scaling": "weak",
-        # The reference publishes fwd+bwd only at r=32 (15.260 ms per batch at
-        # L=2048, results/cuda/wall_clock.csv:6), not at this r=48 config.
-        "vs_baseline": None,
+        "vs_baseline": vs_baseline,
         "dtype": "bf16",
         "data": "synthetic: x ~ N(0,1) fp16, seeded random-init weights",
         "config": {"workload": "lsso_mixer_forward_backward", "batch": batch, "length": length,
