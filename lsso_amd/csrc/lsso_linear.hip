@@ -5,13 +5,13 @@
 // FP32 accumulation, FP32 bias added to the accumulator, one final FP16 or
 // BF16 store; FP16 output never rounds through BF16.
 //
-// Schedule: persistent workgroups of 8 waves (4 when 256 < K <= 512).  Each
+// Schedule: persistent workgroups of 8 waves (4 when 256 < K <= 384).  Each
 // wave keeps a 32-column slice of W (BF16, K padded to 16) in registers for
-// the whole launch, so the weights are read once per workgroup; past K = 512
-// two waves share a slice, one per half of K.  64-row x
-// tiles (32-row once K > 512, so that two of them fit LDS) are staged through
-// a double-buffered LDS tile (converted to BF16 once) and shared by the
-// workgroup's waves.
+// the whole launch, so the weights are read once per workgroup; past K = 384
+// two waves share a slice, one per half of K.  64-row x tiles (32-row once
+// K > 384, so that two of them and the split's partials fit LDS) are staged
+// through a double-buffered LDS tile (converted to BF16 once) and shared by
+// the workgroup's waves.
 // The MFMA computes y^T = W x^T on v_mfma_f32_32x32x16_bf16; in that form a
 // lane's accumulators are 4 runs of 4 consecutive output features of one
 // row.  The rounded tile is staged in LDS and written back in 16-byte pieces
@@ -25,20 +25,21 @@ namespace lsso_hip {
 
 constexpr int kXcds = 8;   // accelerator complex dies of an MI355X
 
-// Rows per x tile: 64, or 32 once K exceeds 512.
+// Rows per x tile: 64, or 32 once K exceeds 384.
 template <int KSTEPS>
-constexpr int linear_tile_rows_k() { return KSTEPS <= 32 ? 64 : 32; }
+constexpr int linear_tile_rows_k() { return KSTEPS <= 24 ? 64 : 32; }
 
 // Waves per workgroup: eight (two per SIMD, 256 registers each) while the
-// resident W slice fits; four for K in (256, 512]; eight again past 512,
+// resident W slice fits; four for K in (256, 384]; eight again past 384,
 // where two waves share each 32-column slice, one per half of K, and add
-// their accumulators through LDS.
+// their accumulators through LDS.  Up to K = 384 the K order is a single
+// chain, the one the fused projection kernels reproduce bit for bit.
 template <int KSTEPS>
-constexpr int linear_waves() { return (KSTEPS <= 16 || KSTEPS > 32) ? 8 : 4; }
+constexpr int linear_waves() { return (KSTEPS <= 16 || KSTEPS >= 32) ? 8 : 4; }
 template <int KSTEPS>
-constexpr int linear_ksplit() { return KSTEPS > 32 ? 2 : 1; }
+constexpr int linear_ksplit() { return KSTEPS >= 32 ? 2 : 1; }
 
-int linear_tile_rows(int k_steps) { return k_steps <= 32 ? 64 : 32; }
+int linear_tile_rows(int k_steps) { return k_steps <= 24 ? 64 : 32; }
 int linear_columns_per_group(int k_steps) { return (k_steps <= 16 ? 8 : 4) * 32; }
 
 int linear_k_tier(int64_t in_features) {
