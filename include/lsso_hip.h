@@ -142,6 +142,36 @@ int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape,
                             size_t workspace_bytes,
                             void* stream);
 
+/* lsso_hip_mixer_backward, and, when grad_projected_column_sums (float32
+ * [H*(rank+head_dim)]) is not NULL, the FP32 sums over all rows of each
+ * column of grad_projected: the bias gradient of the input projection
+ * (grad_output.sum(dim=rows, dtype=float32) in _TensorCoreLinear.backward).
+ * The sums are taken from the token map's output tiles, so grad_projected is
+ * not read again; they are added in a fixed order.  Same workspace as
+ * lsso_hip_mixer_backward.
+ * Replaces: torch.ops.lsso_equilibrium.backward followed by the input
+ * projection's bias reduction (csrc/ball/backward.cu:1386-1667;
+ * lsso/ball/reference.py:236-245). */
+int lsso_hip_mixer_backward_ex(const lsso_hip_mixer_shape* shape,
+                               const void* grad_output,
+                               const void* projected,
+                               const float* core_base_raw,
+                               const float* core_drive_weight,
+                               const float* eta_raw,
+                               const float* inverse_frequency,
+                               const float* centered_positions,
+                               int positions_mode,
+                               const float* valid_counts,
+                               const float* tape,
+                               void* grad_projected,
+                               float* grad_base,
+                               float* grad_drive,
+                               float* grad_eta,
+                               float* grad_projected_column_sums,
+                               void* workspace,
+                               size_t workspace_bytes,
+                               void* stream);
+
 /* 1 if lsso_hip_mixer_forward_projected handles this shape, 0 if not (use
  * lsso_hip_mixer_forward followed by lsso_hip_linear), or a negative code for
  * an invalid shape.  The fused path covers heads <= 8, head_dim a multiple of

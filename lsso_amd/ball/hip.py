@@ -46,6 +46,7 @@ _SYMBOLS = (
     "lsso_hip_mixer_forward_projected",
     "lsso_hip_mixer_backward_workspace_bytes",
     "lsso_hip_mixer_backward",
+    "lsso_hip_mixer_backward_ex",
     "lsso_hip_linear_workspace_bytes",
     "lsso_hip_linear",
     "lsso_hip_linear_grad_columns_workspace_bytes",
@@ -107,6 +108,11 @@ def _declare(library: ctypes.CDLL) -> None:
         ctypes.c_size_t, vp,
     ]  # shape, grad_output, projected, base, drive, eta, inv_freq, positions, mode, counts,
     #    tape, grad_projected, grad_base, grad_drive, grad_eta, workspace, workspace_bytes, stream
+    library.lsso_hip_mixer_backward_ex.restype = ctypes.c_int
+    library.lsso_hip_mixer_backward_ex.argtypes = [
+        shape_p, vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp,
+        ctypes.c_size_t, vp,
+    ]  # ... as lsso_hip_mixer_backward, with grad_projected_column_sums before the workspace
     library.lsso_hip_linear_workspace_bytes.restype = ctypes.c_int
     library.lsso_hip_linear_workspace_bytes.argtypes = [i64, i64, i64, size_p]
     library.lsso_hip_linear.restype = ctypes.c_int
@@ -495,10 +501,13 @@ def backward(
     tape: torch.Tensor,
     centered_positions: torch.Tensor | None = None,
     valid_counts: torch.Tensor | None = None,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    column_sums: bool = False,
+):
     """Native first-order VJP of the mixer (csrc/ball/binding.cpp:92-95):
     returns (grad_projected, grad_core_base_raw, grad_core_drive_weight,
-    grad_eta_raw)."""
+    grad_eta_raw), and with ``column_sums`` also the FP32 column sums of
+    grad_projected over all rows (the input projection's bias gradient,
+    taken inside the token map)."""
 
     library = _library()
     shape, mode = _validate_mixer(
@@ -527,8 +536,9 @@ def backward(
     grad_base = torch.empty_like(core_base_raw)
     grad_drive = torch.empty_like(core_drive_weight)
     grad_eta = torch.empty_like(eta_raw)
+    sums = torch.empty(projected.shape[-1], dtype=torch.float32, device=device) if column_sums else None
     with torch.cuda.device(device):
-        status = library.lsso_hip_mixer_backward(
+        status = library.lsso_hip_mixer_backward_ex(
             ctypes.byref(shape),
             grad_output.data_ptr(),
             projected.data_ptr(),
@@ -544,11 +554,14 @@ def backward(
             grad_base.data_ptr(),
             grad_drive.data_ptr(),
             grad_eta.data_ptr(),
+            None if sums is None else sums.data_ptr(),
             workspace.data_ptr(),
             workspace_bytes.value,
             _stream(device),
         )
     _check(status, library)
+    if column_sums:
+        return grad_projected, grad_base, grad_drive, grad_eta, sums
     return grad_projected, grad_base, grad_drive, grad_eta
 
 
@@ -968,7 +981,12 @@ class _ProjectMix(torch.autograd.Function):
     def backward(ctx, grad_mixed):
         x, in_weight, packed, core_base_raw, core_drive_weight, eta_raw, tape, row_mask = ctx.saved_tensors
         needs = ctx.needs_input_grad
-        grad_packed, grad_base, grad_drive, grad_eta = backward(
+        # Without a row mask, the column sums of grad_packed taken inside the
+        # token map are the bias gradient.  With one, rows the mask excludes
+        # must not count, and only the projection VJP's own pass knows them.
+        need_bias = ctx.has_bias and needs[2]
+        fused_sums = need_bias and row_mask is None
+        grads = backward(
             grad_mixed.to(dtype=torch.bfloat16),
             packed,
             core_base_raw,
@@ -977,10 +995,12 @@ class _ProjectMix(torch.autograd.Function):
             tape,
             ctx.centered_positions,
             ctx.valid_counts,
+            column_sums=fused_sums,
         )
+        grad_packed, grad_base, grad_drive, grad_eta = grads[:4]
         grad_x, grad_weight, grad_bias = _linear_vjp(
-            grad_packed, x, in_weight, row_mask, needs[0], needs[1], ctx.has_bias and needs[2],
-            ctx.bias_dtype,
+            grad_packed, x, in_weight, row_mask, needs[0], needs[1], need_bias, ctx.bias_dtype,
+            grads[4] if fused_sums else None,
         )
         return (
             grad_x,
@@ -1199,8 +1219,12 @@ def _linear_vjp(
     need_weight: bool,
     need_bias: bool,
     bias_dtype: torch.dtype | None,
+    grad_sums: torch.Tensor | None = None,
 ):
     """(dX, dW, db) of y = cast(bf16(x) bf16(W)^T + b) (reference.py:205-247).
+    ``grad_sums``: the FP32 column sums of dY when the caller already has
+    them (over the rows ``row_mask`` keeps), so no pass over dY is made for
+    the bias.
 
     One native pass over dY writes its BF16 copy (excluded rows zero) for
     the weight gradient and its FP32 column sums for the bias gradient; dX
@@ -1213,9 +1237,12 @@ def _linear_vjp(
     native_value = value.dtype in (torch.float16, torch.bfloat16) and out_features <= 640
     need_bf16 = need_weight or (need_value and not native_value)
     copy_grad = need_bf16 and (flat_grad.dtype != torch.bfloat16 or row_mask is not None)
-    grad_bf16, grad_sums = None, None
-    if copy_grad or need_bias:
-        grad_bf16, grad_sums = _grad_columns(flat_grad, row_mask, copy_grad, need_bias)
+    grad_bf16 = None
+    sums_needed = need_bias and grad_sums is None
+    if copy_grad or sums_needed:
+        grad_bf16, computed = _grad_columns(flat_grad, row_mask, copy_grad, sums_needed)
+        if sums_needed:
+            grad_sums = computed
     if need_bf16 and grad_bf16 is None:
         grad_bf16 = flat_grad
     grad_value = grad_weight = grad_bias = None

@@ -729,6 +729,12 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
     };
 
     float dot = 0.0f;
+    // Column sums of grad_projected over this wave's tokens, from the staged
+    // output tiles: lane j holds columns 2 j, 2 j + 1 of [dR | dC].
+    constexpr int kPairColumns = (R + D) / 2;
+    static_assert(kPairColumns <= 64, "one column pair per lane");
+    float col_even = 0.0f;
+    float col_odd = 0.0f;
     // One 16-token step from its staged inputs.
     auto compute = [&](const In& cur, int64_t t0) {
         const int64_t token = t0 + q;
@@ -859,6 +865,20 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
                 *reinterpret_cast<u32x4*>(gout + (t0 + row) * a.width + column) = v;
             }
         }
+        if (a.column_part != nullptr && lane < kPairColumns) {
+            float even = 0.0f;
+            float odd = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if (t0 + r < end) {
+                    const uint32_t v = *reinterpret_cast<const uint32_t*>(&out_tile[r * OP + 2 * lane]);
+                    even += bf16_lo(v);
+                    odd += bf16_hi(v);
+                }
+            }
+            col_even += even;
+            col_odd += odd;
+        }
     };
     // Inputs are read one step ahead, alternating between two stages.
     In s0;
@@ -872,6 +892,13 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
         }
         fetch(s0, t0 + 32);
         compute(s1, t0 + 16);
+    }
+    if (a.column_part != nullptr && lane < kPairColumns) {
+        const int c = 2 * lane;
+        const int64_t column = c < R ? rel_off + c : content_off + c - R;
+        float* row = a.column_part + (b * a.chunks + chunk) * a.width + column;
+        row[0] = col_even;
+        row[1] = col_odd;
     }
     // <dY, C> of this wave's tokens.
     for (int offset = 32; offset > 0; offset >>= 1) {
@@ -1017,9 +1044,14 @@ static int resident_max_d16(int rank) {
     return rank <= 32 ? 4 : (rank == 48 ? 2 : 1);
 }
 
+bool bwd_apply_resident(int rank, int64_t head_dim, bool vec) {
+    const int64_t d16 = head_dim / 16;
+    return vec && head_dim % 16 == 0 && d16 >= 1 && d16 <= resident_max_d16(rank);
+}
+
 hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, bool vec, hipStream_t stream) {
     const int d16 = static_cast<int>(a.head_dim / 16);
-    if (vec && a.head_dim % 16 == 0 && d16 >= 1 && d16 <= resident_max_d16(rank)) {
+    if (bwd_apply_resident(rank, a.head_dim, vec)) {
         switch (rank * 8 + d16) {
             case 16 * 8 + 1: return launch_bwd_apply_resident<16, 1>(a, stream);
             case 16 * 8 + 2: return launch_bwd_apply_resident<16, 2>(a, stream);

@@ -509,10 +509,43 @@ int lsso_hip_mixer_forward_projected(const lsso_hip_mixer_shape* shape, const vo
 
 namespace {
 
+constexpr int64_t kGradTargetGroups = 512;
+
+struct GradColumnsPlan {
+    int chunks_per_slab;
+    int64_t slabs, splits, rows_per_split;
+};
+
+// Chunks of 8 columns are dealt to slabs of a power-of-two width (the largest
+// that divides the chunk count, up to 64; else the smallest covering it), and
+// rows to about 512 / slabs splits of at least eight passes each.
+void plan_grad_columns(int64_t rows, int64_t cols, GradColumnsPlan* p) {
+    const int64_t chunks = ceil_div(cols, 8);
+    int cw = 1;
+    while (cw < 64 && chunks % (2 * cw) == 0) {
+        cw *= 2;
+    }
+    if (cw < 8) {
+        cw = 1;
+        while (cw < 64 && cw < chunks) {
+            cw *= 2;
+        }
+    }
+    p->chunks_per_slab = cw;
+    p->slabs = ceil_div(chunks, cw);
+    const int64_t row_lanes = 256 / cw;
+    int64_t splits = ceil_div(kGradTargetGroups, p->slabs);
+    const int64_t most = std::max<int64_t>(1, ceil_div(rows, row_lanes * 8));
+    splits = std::min(splits, most);
+    p->rows_per_split = std::max<int64_t>(1, ceil_div(rows, splits));
+    p->splits = rows == 0 ? 0 : ceil_div(rows, p->rows_per_split);
+}
+
 struct BackwardPlan {
     int64_t record_stride, off_m, off_e, off_g, off_f;
     int feature_k32;
-    size_t off_phases, off_partials, off_records, off_dtheta, off_ddrive, off_deta, off_dot, total;
+    size_t off_phases, off_partials, off_records, off_dtheta, off_ddrive, off_deta, off_dot;
+    size_t off_columns, total;
 };
 
 int make_backward_plan(const MixerPlan& plan, BackwardPlan* bp) {
@@ -539,6 +572,11 @@ int make_backward_plan(const MixerPlan& plan, BackwardPlan* bp) {
     offset = align_up(offset + sizeof(float) * systems);
     bp->off_dot = offset;
     offset = align_up(offset + sizeof(float) * systems * plan.apply_chunks);
+    // Column-sum partials of grad_projected: one row per (sample, chunk) from
+    // the token map, or one per split of the one-pass gradient kernel.
+    bp->off_columns = offset;
+    const int64_t column_rows = std::max<int64_t>(plan.batch * plan.apply_chunks, kGradTargetGroups);
+    offset = align_up(offset + sizeof(float) * column_rows * plan.width);
     bp->total = offset;
     return LSSO_HIP_OK;
 }
@@ -574,6 +612,21 @@ int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape, const void* grad_
                             void* grad_projected, float* grad_base, float* grad_drive,
                             float* grad_eta, void* workspace, size_t workspace_bytes,
                             void* stream_handle) {
+    return lsso_hip_mixer_backward_ex(shape, grad_output, projected, core_base_raw,
+                                      core_drive_weight, eta_raw, inverse_frequency,
+                                      centered_positions, positions_mode, valid_counts, tape,
+                                      grad_projected, grad_base, grad_drive, grad_eta, nullptr,
+                                      workspace, workspace_bytes, stream_handle);
+}
+
+int lsso_hip_mixer_backward_ex(const lsso_hip_mixer_shape* shape, const void* grad_output,
+                               const void* projected, const float* core_base_raw,
+                               const float* core_drive_weight, const float* eta_raw,
+                               const float* inverse_frequency, const float* centered_positions,
+                               int positions_mode, const float* valid_counts, const float* tape,
+                               void* grad_projected, float* grad_base, float* grad_drive,
+                               float* grad_eta, float* grad_projected_column_sums,
+                               void* workspace, size_t workspace_bytes, void* stream_handle) {
     (void)core_base_raw;  // Theta is read from the tape
     MixerPlan plan;
     int status = make_plan(shape, positions_mode, &plan);
@@ -696,6 +749,7 @@ int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape, const void* grad_
     apply.eta_raw = eta_raw;
     apply.grad_projected = static_cast<uint16_t*>(grad_projected);
     apply.dot_part = dot;
+    float* column_part = reinterpret_cast<float*>(ws + bp.off_columns);
     apply.batch = plan.batch;
     apply.length = plan.length;
     apply.heads = plan.heads;
@@ -707,10 +761,38 @@ int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape, const void* grad_
     // Whole 16-byte (K32) or 8-byte (K16) feature runs per lane.
     const bool bwd_vec = plan.head_dim % 8 == 0 && plan.width % 8 == 0 && aligned(projected, 16) &&
                          aligned(grad_output, 16) && aligned(grad_projected, 16);
+    const bool fused_sums = grad_projected_column_sums != nullptr &&
+                            lsso_hip::bwd_apply_resident(static_cast<int>(plan.rank), plan.head_dim, bwd_vec);
+    apply.column_part = fused_sums ? column_part : nullptr;
     error = lsso_hip::launch_bwd_apply(static_cast<int>(plan.rank), apply, bp.feature_k32 != 0,
                                        bwd_vec, stream);
     if (error != hipSuccess) {
         return hip_failure(error, "bwd_apply_kernel launch");
+    }
+    if (fused_sums) {
+        error = lsso_hip::launch_column_sum(column_part, plan.batch * plan.apply_chunks, plan.width,
+                                            grad_projected_column_sums, stream);
+        if (error != hipSuccess) {
+            return hip_failure(error, "column_sum_kernel launch");
+        }
+    } else if (grad_projected_column_sums != nullptr) {
+        // The general token map: one read of grad_projected for its sums.
+        GradColumnsPlan gp;
+        plan_grad_columns(plan.batch * plan.length, plan.width, &gp);
+        lsso_hip::GradColumnsArgs ga{};
+        ga.g = grad_projected;
+        ga.rows = plan.batch * plan.length;
+        ga.cols = plan.width;
+        ga.g_stride = plan.width;
+        ga.partials = column_part;
+        ga.rows_per_split = gp.rows_per_split;
+        ga.chunks_per_slab = gp.chunks_per_slab;
+        const bool vec = plan.width % 8 == 0 && aligned(grad_projected, 16);
+        error = lsso_hip::launch_grad_columns(ga, LSSO_HIP_BF16, vec, gp.splits, gp.slabs,
+                                              grad_projected_column_sums, stream);
+        if (error != hipSuccess) {
+            return hip_failure(error, "grad_columns_kernel launch (backward)");
+        }
     }
 
     lsso_hip::ParamReduceArgs params{};
@@ -737,38 +819,6 @@ int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape, const void* grad_
 }  // extern "C"
 
 namespace {
-
-constexpr int64_t kGradTargetGroups = 512;
-
-struct GradColumnsPlan {
-    int chunks_per_slab;
-    int64_t slabs, splits, rows_per_split;
-};
-
-// Chunks of 8 columns are dealt to slabs of a power-of-two width (the largest
-// that divides the chunk count, up to 64; else the smallest covering it), and
-// rows to about 512 / slabs splits of at least eight passes each.
-void plan_grad_columns(int64_t rows, int64_t cols, GradColumnsPlan* p) {
-    const int64_t chunks = ceil_div(cols, 8);
-    int cw = 1;
-    while (cw < 64 && chunks % (2 * cw) == 0) {
-        cw *= 2;
-    }
-    if (cw < 8) {
-        cw = 1;
-        while (cw < 64 && cw < chunks) {
-            cw *= 2;
-        }
-    }
-    p->chunks_per_slab = cw;
-    p->slabs = ceil_div(chunks, cw);
-    const int64_t row_lanes = 256 / cw;
-    int64_t splits = ceil_div(kGradTargetGroups, p->slabs);
-    const int64_t most = std::max<int64_t>(1, ceil_div(rows, row_lanes * 8));
-    splits = std::min(splits, most);
-    p->rows_per_split = std::max<int64_t>(1, ceil_div(rows, splits));
-    p->splits = rows == 0 ? 0 : ceil_div(rows, p->rows_per_split);
-}
 
 }  // namespace
 

@@ -135,6 +135,7 @@ struct BwdApplyArgs {
     const float* eta_raw;
     uint16_t* grad_projected;   // BF16 [B, N, width]
     float* dot_part;            // [B*H, chunks]: <dY, C> per chunk
+    float* column_part;         // [B*chunks, width]: column sums of grad_projected, or nullptr
     int64_t batch;
     int64_t length;
     int64_t heads;
@@ -236,6 +237,11 @@ int64_t bwd_record_layout(int64_t rank, int64_t head_dim, int64_t* off_m, int64_
                           int64_t* off_g, int64_t* off_f, int* feature_k32);
 hipError_t launch_bwd_solve(int rank, const BwdSolveArgs& a, int64_t systems, hipStream_t stream);
 hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, bool vec, hipStream_t stream);
+// True when launch_bwd_apply runs the resident token map, which also writes
+// column_part when it is set.
+bool bwd_apply_resident(int rank, int64_t head_dim, bool vec);
+hipError_t launch_column_sum(const float* partials, int64_t splits, int64_t cols, float* out,
+                             hipStream_t stream);
 hipError_t launch_param_reduce(const ParamReduceArgs& a, hipStream_t stream);
 
 hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,

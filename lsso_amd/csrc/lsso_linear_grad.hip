@@ -169,6 +169,13 @@ __global__ __launch_bounds__(kGradThreads) void column_sum_kernel(const float* p
     }
 }
 
+hipError_t launch_column_sum(const float* partials, int64_t splits, int64_t cols, float* out,
+                             hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((cols + 31) / 32));
+    column_sum_kernel<<<grid, kGradThreads, 0, stream>>>(partials, splits, cols, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_grad_columns(const GradColumnsArgs& a, int g_dtype, bool vec, int64_t splits,
                                int64_t slabs, float* column_sums, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(slabs));

@@ -152,3 +152,24 @@ def test_module_backward_matches_oracle_autograd_masked(native):
     assert _rel_l2(x.grad, x64.grad) <= GRAD_LIMIT
     for name, parameter in layer.named_parameters():
         assert _rel_l2(parameter.grad, params[name].grad) <= GRAD_LIMIT, (name, _rel_l2(parameter.grad, params[name].grad))
+
+
+@pytest.mark.parametrize(
+    ("batch", "rank", "heads", "head_dim", "length"),
+    [
+        (2, 48, 8, 32, 300),   # resident token map: sums from its output tiles
+        (2, 32, 2, 64, 129),   # resident, four content blocks
+        (1, 16, 3, 24, 77),    # general token map: one pass over grad_projected
+    ],
+)
+def test_backward_column_sums_match_grad_projected(native, batch, rank, heads, head_dim, length):
+    projected, base, drive, eta_raw, grad = _inputs(batch, rank, heads, head_dim, length, seed=rank + length)
+    args = [t.cuda() for t in (grad, projected, base, drive, eta_raw)]
+    with torch.no_grad():
+        _, tape = native.forward_train(args[1], args[2], args[3], args[4])
+        plain = native.backward(*args, tape)
+        *grads, sums = native.backward(*args, tape, column_sums=True)
+    for a, b in zip(plain, grads):
+        assert torch.equal(a, b)
+    expected = grads[0].double().sum(dim=(0, 1))
+    torch.testing.assert_close(sums.double(), expected, rtol=1e-5, atol=1e-4)

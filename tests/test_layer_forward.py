@@ -215,6 +215,11 @@ def test_project_mix_gradients_equal_the_two_call_path(native):
     fused_out, fused_grads = run(True)
     split_out, split_grads = run(False)
     assert torch.equal(fused_out, split_out)
-    for got, want in zip(fused_grads, split_grads):
-        assert got is not None and torch.isfinite(got).all()
-        assert torch.equal(got, want)
+    names = ("x", "in_weight", "in_bias", "base", "drive", "eta")
+    for name, got, want in zip(names, fused_grads, split_grads):
+        assert got is not None and torch.isfinite(got).all(), name
+        if name == "in_bias":
+            # Summed inside the token map: the same FP32 sums in another fixed order.
+            torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+        else:
+            assert torch.equal(got, want), name
