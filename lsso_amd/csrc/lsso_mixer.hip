@@ -132,7 +132,8 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
 // element per column, so a step is one chain of VALU instructions with no
 // LDS round trip.  Its step loop is unrolled up to rank 32 (the next pivot
 // search then overlaps the current row updates) and rolled above, where the
-// unrolled chain spills.  The substitution for L^-1 has no cross-lane traffic
+// unrolled chain spills.  At rank 32 each row is split over the two wave
+// halves instead (16 columns per lane, the pivot row through LDS).  The substitution for L^-1 has no cross-lane traffic
 // and is unrolled.  The products use all four waves on FP32 MFMA tiles.
 extern "C" __device__ unsigned int __ockl_wfred_max_u32(unsigned int);
 
@@ -476,6 +477,84 @@ __device__ __forceinline__ f32x4 mfma_tile_f32(f32x4 acc, int k_end, LoadA a, Lo
     return acc;
 }
 
+// Gauss-Jordan of a rank-32 system (the in-place form of solve_kernel, same
+// pivots, factors and updates element for element) with each matrix row split
+// over the two halves of the wave: lane l holds columns 16 (l / 32) .. + 15 of
+// row l % 32, so all 64 lanes update and each updates 16 columns.  Per step:
+// the pivot search runs over the half that holds column k; the row's column-k
+// value reaches the other half by a lane swap; the pivot row's two halves go
+// through LDS (s_rows, 64 floats per step parity; one lane per half writes,
+// each lane reads its half back as a broadcast).  Row p_k ends, scaled by
+// 1 / pivot, at row k of s_out; s_pivot[k] = p_k.
+template <int LD>
+__device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s_out, float* s_rows, int* s_pivot,
+                                                    int lane) {
+    const int half = lane >> 5;
+    const int row = lane & 31;
+    f32x16 t;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(s_sys + row * LD + 16 * half + 4 * m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            t[4 * m + e] = v[e];
+        }
+    }
+    bool open = true;
+    int own_step = 0;
+    float own_pivot = 1.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const bool owner = half == (k >> 4);
+        const float own = t[k & 15];
+        const float other = __shfl_xor(own, 32);
+        const float x = owner ? own : other;
+        const unsigned magnitude = __float_as_uint(fabsf(own));
+        const unsigned best =
+            __builtin_amdgcn_readfirstlane(__ockl_wfred_max_u32(open && owner ? magnitude : 0u));
+        const unsigned long long ties = __ballot(open && owner && magnitude == best);
+        const int source = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(ties)));
+        const int p = source & 31;
+        const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(own), source));
+        const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
+        const float f = row == p ? 0.0f : x * inv_pivot;
+        float* buf = s_rows + (k & 1) * 32 + 16 * half;
+        if (row == p) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                *reinterpret_cast<f32x4*>(buf + 4 * m) = (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
+            }
+        }
+        wave_lds_order();
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(buf + 4 * m);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                t[4 * m + e] = fmaf(-f, v[e], t[4 * m + e]);
+            }
+        }
+        if (owner) {
+            t[k & 15] = row == p ? 1.0f : -f;
+        }
+        if (row == p) {
+            open = false;
+            own_step = k;
+            own_pivot = pivot;
+        }
+        if (lane == 0) {
+            s_pivot[k] = p;
+        }
+    }
+    t = t * __builtin_amdgcn_rcpf(own_pivot);
+    wave_lds_order();
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        *reinterpret_cast<f32x4*>(s_out + own_step * LD + 16 * half + 4 * m) =
+            (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
+    }
+}
+
 template <int R>
 // Two workgroups per CU (512 systems on 256 CUs in one round): the register
 // budget is held to 256 per lane, which costs rank 48 a few spills.
@@ -777,7 +856,11 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     // k from every other row with the unscaled pivot row, and keeps column k
     // as column p_k of the growing inverse.  Row p_k ends as pi_k times row k
     // of the inverse with its columns in step order.
-    if (wave == 0) {
+    if constexpr (R == 32) {
+        if (wave == 0) {
+            gauss_jordan_halves<LD>(s_sys, s_work, s_work, s_pivot, lane);
+        }
+    } else if (wave == 0) {
         const bool live = lane < R;
         LSSO_REG_ROW(rowv);
         if (live) {
@@ -809,7 +892,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         if constexpr (R <= 32) {
             // Unrolled, the next step's pivot search overlaps the end of the
             // current step's row updates (from rank 48 on, the unrolled
-            // chain spills registers).
+            // chain spills registers).  Rank 32 takes gauss_jordan_halves.
 #pragma unroll
             for (int k = 0; k < R; ++k) {
                 gj_step(k);
