@@ -109,6 +109,33 @@ def test_mixer_masked_batched_positions_match_fp64_oracle(native, rank, head_dim
     assert _rel_l2(out, expected) <= 5e-3
 
 
+@pytest.mark.parametrize("rank", (16, 32, 48, 64))
+def test_mixer_pivoting_systems_match_fp64_oracle(native, rank: int) -> None:
+    """Systems whose LU takes pivots off the diagonal.  A large Theta0 and no
+    drive make I + K = I + F F^T + Omega independent of the tokens; its
+    partial-pivoting LU (scipy) is checked to exchange rows in every head, so
+    the Gauss-Jordan row exchanges of each rank's form (one row per lane, or
+    rows split over the wave halves at rank 32) are exercised."""
+
+    import numpy as np
+    import scipy.linalg
+
+    generator = torch.Generator().manual_seed(913)
+    length, heads, head_dim = 65, 2, 16
+    projected = torch.randn(1, length, heads * (rank + head_dim), generator=generator).bfloat16()
+    base = 3.0 * torch.randn(heads, rank, rank, generator=generator)
+    drive = torch.zeros(heads, head_dim, rank)
+    eta_raw = torch.tensor([0.3, -0.2])
+    system = oracle.accretive_generator(base.double()) + torch.eye(rank, dtype=torch.float64)
+    for h in range(heads):
+        _, pivots = scipy.linalg.lu_factor(system[h].numpy())
+        assert (pivots != np.arange(rank)).sum() >= rank // 4
+    out = _run_mixer(native, projected, base, drive, eta_raw)
+    expected = oracle.fast_mix_fp64(projected, base, drive, eta_raw)
+    assert torch.isfinite(out).all()
+    assert _rel_l2(out, expected) <= 5e-3
+
+
 @pytest.mark.parametrize("scale", (0.001, 64.0))
 def test_mixer_relation_scale_extremes(native, scale: float) -> None:
     """Reference tests/cuda/test_fast_path.py:1482-1509 (forward part)."""
