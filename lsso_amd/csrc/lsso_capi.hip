@@ -28,7 +28,15 @@ int hip_failure(hipError_t error, const char* where) {
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 size_t align_up(size_t value) { return (value + 255) & ~static_cast<size_t>(255); }
 
-constexpr int64_t kReduceTargetWaves = 2048;
+// Token chunk of the L-reductions.  It depends on nothing but itself, so a
+// sequence is cut into the same chunks (and its G / S partials are summed in
+// the same order) whatever the batch holds: a sample's outputs and input
+// gradients are bitwise the same alone or in any batch.  The reference gets
+// the same property from its fixed 32-token tile partials
+// (csrc/ball/forward.cu:510-628).  512 tokens keeps the partial traffic small
+// (2 partial sets per 1,024 tokens) while B = 64 sequences of 1,024 tokens
+// still give 128 chunks, about one per compute unit and head group.
+constexpr int64_t kReduceChunkTokens = 512;
 constexpr int64_t kApplyTargetWaves = 4096;
 
 struct MixerPlan {
@@ -88,8 +96,12 @@ int make_plan(const lsso_hip_mixer_shape* shape, int positions_mode, MixerPlan* 
     p->column_groups = ceil_div(p->head_dim, 32 * p->cpw);
     // Chunks are whole 64-token tiles, so the fused projection + reduce and
     // the standalone reduce share one chunking (and their partials agree).
-    plan_chunks(p->length, p->batch * p->heads * p->column_groups, kReduceTargetWaves,
-                lsso_hip::project_reduce_tile_rows(), &p->reduce_chunks, &p->reduce_chunk_tokens);
+    static_assert(kReduceChunkTokens % 64 == 0, "reduce chunks are whole projection tiles");
+    p->reduce_chunk_tokens = kReduceChunkTokens;
+    p->reduce_chunks = ceil_div(p->length, kReduceChunkTokens);
+    if (lsso_hip::project_reduce_tile_rows() != 64) {
+        return fail(LSSO_HIP_ERUNTIME, "internal: the projection tile is not 64 rows");
+    }
 
     p->feature_blocks = ceil_div(p->head_dim, 16);
     p->nfbw = p->feature_blocks >= 4 ? 4 : (p->feature_blocks == 3 ? 4 : static_cast<int>(p->feature_blocks));
