@@ -5,7 +5,9 @@
  * biased projections as hand-written CDNA4 kernels.  Every entry point takes
  * plain device pointers, sizes and a hipStream_t; the library never allocates
  * device memory.  Callers size the scratch buffers with the *_workspace_bytes
- * queries and own every allocation.  All launches are asynchronous and
+ * queries and own every allocation; the one exception,
+ * lsso_hip_mixer_forward_static, uses a device array that is part of the
+ * library's code object instead.  All launches are asynchronous and
  * stream-ordered; no entry point synchronizes the host.
  *
  * Return values: 0 on success, a negative LSSO_HIP_E* code on failure.  The
@@ -108,6 +110,35 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape,
                            void* workspace,
                            size_t workspace_bytes,
                            void* stream);
+
+/* Size of the device array that lsso_hip_mixer_forward_static uses as its
+ * workspace (64 MiB; each GPU the library runs on holds one). */
+#define LSSO_HIP_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* lsso_hip_mixer_forward without a caller workspace, and without any device
+ * allocation: the workspace is a device array of the library's own, of
+ * LSSO_HIP_STATIC_SCRATCH_BYTES per GPU, held from the library's first use on
+ * a GPU until the process ends.  Geometries whose
+ * lsso_hip_mixer_workspace_bytes() exceeds that size are rejected with
+ * LSSO_HIP_EUNSUPPORTED (B = 64, N = 4096, H = 8, r = 32, d = 32 needs about
+ * 38 MB).  All calls on one GPU share its array: calls in flight at the same
+ * time on one GPU (on different streams) race, calls ordered on one stream do
+ * not.  Arguments and results are those of lsso_hip_mixer_forward.
+ * No counterpart in the reference: this entry point is for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). */
+int lsso_hip_mixer_forward_static(const lsso_hip_mixer_shape* shape,
+                                  const void* projected,
+                                  const float* core_base_raw,
+                                  const float* core_drive_weight,
+                                  const float* eta_raw,
+                                  const float* inverse_frequency,
+                                  const float* centered_positions,
+                                  int positions_mode,
+                                  const float* valid_counts,
+                                  void* output,
+                                  float* tape,
+                                  void* stream);
 
 /* Device scratch bytes needed by lsso_hip_mixer_backward.
  * Replaces: the at::empty allocations of backward_cuda

@@ -42,6 +42,7 @@ _SYMBOLS = (
     "lsso_hip_mixer_workspace_bytes",
     "lsso_hip_mixer_tape_floats",
     "lsso_hip_mixer_forward",
+    "lsso_hip_mixer_forward_static",
     "lsso_hip_mixer_projected_supported",
     "lsso_hip_mixer_forward_projected",
     "lsso_hip_mixer_backward_workspace_bytes",
@@ -92,6 +93,10 @@ def _declare(library: ctypes.CDLL) -> None:
     library.lsso_hip_mixer_forward.argtypes = [
         shape_p, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp, ctypes.c_size_t, vp,
     ]
+    library.lsso_hip_mixer_forward_static.restype = ctypes.c_int
+    library.lsso_hip_mixer_forward_static.argtypes = [
+        shape_p, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp,
+    ]  # shape, projected, base, drive, eta, inv_freq, positions, mode, counts, output, tape, stream
     library.lsso_hip_mixer_projected_supported.restype = ctypes.c_int
     library.lsso_hip_mixer_projected_supported.argtypes = [shape_p]
     library.lsso_hip_mixer_forward_projected.restype = ctypes.c_int

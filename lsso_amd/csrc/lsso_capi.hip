@@ -6,6 +6,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "lsso_hip.h"
@@ -460,6 +461,103 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape, const void* projec
     }
 
     return run_apply(plan, buf, projected, eta_raw, positions_mode, output, vec, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free mixer forward.
+//
+// lsso_hip_mixer_forward_static runs lsso_hip_mixer_forward with the
+// workspace in `scratch`, a device array of the library's own, so that a
+// caller that cannot allocate device memory (code under HIP graph capture, a
+// serving loop, a harness that forbids hipMalloc) passes only its inputs and
+// outputs.  Each GPU holds its own copy of the array from the library's
+// first use on it until the process ends.  In host code the name `scratch`
+// is a host-side stand-in, not a device address: the array's address on a
+// device comes from hipGetSymbolAddress, looked up once per device with that
+// device current and kept in g_static_scratch, and only that address is
+// handed to kernels.
+//
+// Every call on one GPU uses that GPU's single array, so two calls in flight
+// at the same time on one GPU (on different streams) race; calls ordered on
+// one stream do not.  Nothing in the array has to start at zero: every byte
+// a call reads (phase table, G / S partials, Z, apply records) was written
+// earlier in the same call.
+namespace {
+
+constexpr size_t kStaticScratchBytes = LSSO_HIP_STATIC_SCRATCH_BYTES;
+constexpr int kStaticScratchDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+std::mutex g_static_scratch_lock;
+void* g_static_scratch[kStaticScratchDevices];
+
+// Device address of `scratch` on the current device.
+int static_scratch(void** address) {
+    int device = 0;
+    hipError_t error = hipGetDevice(&device);
+    if (error != hipSuccess) {
+        return hip_failure(error, "hipGetDevice");
+    }
+    if (device < 0 || device >= kStaticScratchDevices) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "the static scratch serves devices 0.." +
+                        std::to_string(kStaticScratchDevices - 1) + ", got device " +
+                        std::to_string(device));
+    }
+    std::lock_guard<std::mutex> lock(g_static_scratch_lock);
+    if (g_static_scratch[device] == nullptr) {
+        void* pointer = nullptr;
+        error = hipGetSymbolAddress(&pointer, HIP_SYMBOL(scratch));
+        if (error != hipSuccess) {
+            return hip_failure(error, "hipGetSymbolAddress(scratch)");
+        }
+        if (pointer == nullptr || !aligned(pointer, 256)) {
+            return fail(LSSO_HIP_ERUNTIME, "the static scratch has no 256-byte aligned device address");
+        }
+        g_static_scratch[device] = pointer;
+    }
+    *address = g_static_scratch[device];
+    return LSSO_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lsso_hip_mixer_forward_static(const lsso_hip_mixer_shape* shape, const void* projected,
+                                  const float* core_base_raw, const float* core_drive_weight,
+                                  const float* eta_raw, const float* inverse_frequency,
+                                  const float* centered_positions, int positions_mode,
+                                  const float* valid_counts, void* output, float* tape,
+                                  void* stream_handle) {
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    if (plan.total > kStaticScratchBytes) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "this geometry needs " + std::to_string(plan.total) +
+                        " workspace bytes, more than the static scratch's " +
+                        std::to_string(kStaticScratchBytes) +
+                        "; use lsso_hip_mixer_forward with a caller workspace");
+    }
+    void* workspace = nullptr;
+    status = static_scratch(&workspace);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    return lsso_hip_mixer_forward(shape, projected, core_base_raw, core_drive_weight, eta_raw,
+                                  inverse_frequency, centered_positions, positions_mode,
+                                  valid_counts, output, tape, workspace, kStaticScratchBytes,
+                                  stream_handle);
 }
 
 int lsso_hip_mixer_projected_supported(const lsso_hip_mixer_shape* shape) {
