@@ -48,6 +48,8 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--cpu-samples", type=int, default=64,
                         help="sequences of the workload timed on the CPU oracle (0 skips)")
     parser.add_argument("--cpu-repeats", type=int, default=7)
+    parser.add_argument("--no-parity", action="store_true",
+                        help="skip the error figures against the CPU oracle")
     parser.add_argument("--copy-mib", type=int, default=0,
                         help="after the timed region, run one device copy of this many MiB "
                              "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -59,26 +61,42 @@ TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profile
                             "mixer_forward_c3_l4096_hbm_traffic.md")
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` at the headline workload, from the
-    calibrated rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under
-    profiles/ (None when the summary has no line for it)."""
+def measured_traffic(kernel_prefix: str):
+    """(kernel name, HBM bytes per launch) of the first kernel whose name
+    starts with `kernel_prefix` in the calibrated rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary committed under profiles/ for the headline
+    workload, or (None, None) when the summary has no such line."""
 
     try:
         with open(TRAFFIC_FILE) as handle:
             for line in handle:
                 if line.startswith("traffic_bytes_per_launch:"):
                     name, _, value = line.split(":", 1)[1].rpartition("=")
-                    if name.strip() == kernel:
-                        return float(value)
+                    if name.strip().startswith(kernel_prefix):
+                        return name.strip(), float(value)
     except OSError:
-        return None
-    return None
+        return None, None
+    return None, None
 
 
-def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> dict:
+def error_figures(actual: torch.Tensor, expected: torch.Tensor) -> dict:
+    """max_abs = max |a - e|, max_rel = max |a - e| / max |e|, rel_l2 =
+    ||a - e|| / ||e||, in FP64."""
+
+    a = actual.detach().to(device="cpu", dtype=torch.float64)
+    e = expected.detach().to(device="cpu", dtype=torch.float64)
+    diff = (a - e).abs()
+    return {
+        "max_abs": float(diff.max()),
+        "max_rel": float(diff.max() / e.abs().max()),
+        "rel_l2": float((a - e).norm() / e.norm()),
+    }
+
+
+def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> tuple[dict, torch.Tensor]:
     """Time the CPU oracle (reference CPU path restated, FP32) on `samples`
-    sequences of the workload; tokens/s is scaled by the sample size."""
+    sequences of the workload; tokens/s is scaled by the sample size.
+    Returns the record and the oracle's FP32 output for those sequences."""
 
     from oracle import lsso_reference as oracle
 
@@ -89,7 +107,7 @@ def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> dict
               "rank": layer.config.rank, "bias": layer.config.bias}
     x = x_cpu[:samples].contiguous()
     with torch.no_grad():
-        oracle.lsso_forward(params, config, x)  # warmup
+        output = oracle.lsso_forward(params, config, x)  # warmup
         times = []
         for _ in range(repeats):
             start = time.perf_counter()
@@ -115,7 +133,34 @@ def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> dict
                   f"(oracle/lsso_reference.py), median of {repeats} after 1 warmup, "
                   f"{seconds * 1e3:.1f} ms per sample batch",
         "cpu": model,
-    }
+    }, output
+
+
+def parity(layer, x_cpu: torch.Tensor, y: torch.Tensor, fp32_output: torch.Tensor | None,
+           fp32_samples: int) -> dict:
+    """Error figures of the GPU output y against the FP32 CPU oracle (on the
+    sequences the CPU baseline ran, or on 3 when it did not run) and its
+    rel-L2 error against the FP64 oracle on sequences 0, B/2 and B-1."""
+
+    from oracle import lsso_reference as oracle
+
+    config = {"dim": layer.config.dim, "num_heads": layer.config.num_heads,
+              "rank": layer.config.rank, "bias": layer.config.bias}
+    if fp32_output is None:
+        fp32_samples = min(3, x_cpu.shape[0])
+        params = {name: p.detach().float().cpu() for name, p in layer.named_parameters()}
+        with torch.no_grad():
+            fp32_output = oracle.lsso_forward(params, config, x_cpu[:fp32_samples].contiguous())
+    figures = error_figures(y[:fp32_samples], fp32_output)
+    picks = sorted({0, x_cpu.shape[0] // 2, x_cpu.shape[0] - 1})
+    params64 = {name: p.detach().double().cpu() for name, p in layer.named_parameters()}
+    with torch.no_grad():
+        fp64_output = oracle.lsso_forward(params64, config, x_cpu[picks].double())
+    figures["rel_l2_fp64"] = error_figures(y[picks], fp64_output)["rel_l2"]
+    figures["reference"] = (f"FP32 CPU oracle on sequences 0..{fp32_samples - 1} (max_rel = max|a-e| / "
+                            f"max|e|); FP64 oracle on sequences {picks}")
+    figures["limit_rel_l2_fp64"] = 5e-3
+    return figures
 
 
 def train_benchmark(args: argparse.Namespace) -> int:
@@ -155,6 +200,10 @@ def train_benchmark(args: argparse.Namespace) -> int:
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
+    grads = [x.grad] + [parameter.grad for parameter in layer.parameters()]
+    if any(g is None or not torch.isfinite(g).all() for g in grads):
+        print("a gradient of the last timed step is missing or not finite", file=sys.stderr)
+        return 1
     tokens = batch * length
     # The reference publishes fwd+bwd only for the r = 32 shell at B = 64
     # (RTX 5070 Ti, results/cuda/wall_clock.csv:5-7): B*L / (7.512, 15.260,
@@ -177,7 +226,7 @@ def train_benchmark(args: argparse.Namespace) -> int:
         "data": "synthetic: x ~ N(0,1) fp16, seeded random-init weights",
         "config": {"workload": "lsso_mixer_forward_backward", "batch": batch, "length": length,
                    "dim": dim, "heads": heads, "rank": rank, "bias": True, "io_dtype": "fp16",
-                   "loss": "mean(y^2)"},
+                   "grad_dtype": "fp32 parameters, fp16 x", "loss": "mean(y^2)"},
     }
     print(json.dumps(result), flush=True)
     return 0
@@ -228,16 +277,15 @@ def main() -> int:
     # on the launch stream (lsso_hip_layer_forward_timed).
     stage_names = ("phase_table", "project_reduce", "solve", "mix_project")
     width = heads * rank + dim
-    k_tier = next(t for t in (8, 12, 16, 24) if dim <= 16 * t)
     # Algorithmic bytes per launch, counting the ABI tensors once (the FP32
     # partials and apply records in the workspace are left out):
     #   project_reduce: x read (FP16) + packed write (BF16) + W_in, b_in (FP32)
     #   mix_project:    packed read (BF16) + y write (FP16) + W_o, b_o (FP32)
     stage_kernels = {
-        "project_reduce": (f"lsso_hip::project_reduce_kernel<{k_tier}, {rank}, 1, 1>",
+        "project_reduce": ("lsso_hip::project_reduce_kernel<",
                            tokens * (dim * 2 + width * 2) + width * dim * 4 + width * 4,
                            "fused input projection + token reductions (x -> packed, G, S)"),
-        "mix_project": (f"lsso_hip::mix_project_kernel<{rank}, 2, 1, 2>",
+        "mix_project": ("lsso_hip::mix_project_kernel<",
                         tokens * (width * 2 + dim * 2) + dim * dim * 4 + dim * 4,
                         "fused apply + output projection (packed -> y)"),
     }
@@ -304,11 +352,16 @@ def main() -> int:
     ms_per_step = 1e3 * elapsed / args.steps
     value = tokens * args.steps / elapsed
     kernel_ms = statistics.mean(start_event.elapsed_time(end_event) for start_event, end_event in timed_pairs)
-    kernel_name, kernel_bytes, kernel_role = stage_kernels[dominant]
+    kernel_prefix, kernel_bytes, kernel_role = stage_kernels[dominant]
     achieved = kernel_bytes / (kernel_ms * 1e-3) / 1e9
-    chain_bytes = tokens * 5120
+    # HBM bytes per token the chain moves by design: x read (FP16), packed
+    # written and read back (BF16), y written (FP16).
+    chain_bytes_per_token = dim * 2 + 2 * width * 2 + dim * 2
+    chain_bytes = tokens * chain_bytes_per_token
     headline = (batch, length) == (64, 4096)
-    traffic = measured_traffic(kernel_name) if headline else None
+    kernel_name, traffic = measured_traffic(kernel_prefix) if headline else (None, None)
+    if kernel_name is None:
+        kernel_name = kernel_prefix.rstrip("<")
     result = {
         "metric": "mixer fwd tokens/s @B64 D256 H8 r32 L4096 fp16; % HBM roofline",
         "value": value,
@@ -333,6 +386,8 @@ def main() -> int:
             "io_dtype": "fp16",
             "positions": "default",
             "mask": False,
+            "accumulate_dtype": "fp32",
+            "chain_bytes_per_token": chain_bytes_per_token,
             "chain_hbm_fraction": chain_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         },
         "roofline": {
@@ -350,8 +405,12 @@ def main() -> int:
             "stage_ms_source": f"{STAGE_PROBE_STEPS} untimed steps with events around every stage",
         },
     }
+    fp32_output = None
+    samples = min(args.cpu_samples, batch)
     if args.cpu_samples > 0:
-        result["cpu_baseline"] = cpu_baseline(layer, x_cpu, min(args.cpu_samples, batch), args.cpu_repeats)
+        result["cpu_baseline"], fp32_output = cpu_baseline(layer, x_cpu, samples, args.cpu_repeats)
+    if not args.no_parity:
+        result["parity"] = parity(layer, x_cpu, check, fp32_output, samples)
     print(json.dumps(result), flush=True)
     return 0
 

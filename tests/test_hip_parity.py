@@ -302,6 +302,10 @@ def _oracle_params(layer: LSSO) -> dict[str, torch.Tensor]:
     return {name: p.detach().double().cpu() for name, p in layer.named_parameters()}
 
 
+def _oracle_params_fp32(layer: LSSO) -> dict[str, torch.Tensor]:
+    return {name: p.detach().float().cpu() for name, p in layer.named_parameters()}
+
+
 def _config_dict(config: LSSOConfig) -> dict:
     return {"dim": config.dim, "num_heads": config.num_heads, "rank": config.rank, "bias": config.bias}
 
@@ -377,11 +381,13 @@ def test_module_c1_config_matches_reference_golden(native) -> None:
     assert _rel_l2(out, y64) <= 5e-3
 
 
-@pytest.mark.parametrize("length", (1024, 4096))
-def test_headline_shell_slice_matches_oracle(native, length: int) -> None:
-    """B=64, D=256, H=8, r=32, FP16 (the L=1024 and L=4096 benchmark shells): the full batch
-    runs on the GPU; samples 0, 17 and 63 are checked against the FP64
-    oracle, and the full batch is checked for determinism."""
+@pytest.mark.parametrize("length", (1024, 2048, 4096))
+def test_headline_shell_slice_matches_oracle(native, parity_report, length: int) -> None:
+    """B=64, D=256, H=8, r=32, FP16 (configs C2 and C3: the L=1024, 2048 and
+    4096 benchmark shells): the full batch runs on the GPU; samples 0, 17
+    and 63 are checked against the FP64 oracle (and their error figures
+    against the FP32 CPU oracle are reported), and the full batch is checked
+    for determinism."""
 
     torch.manual_seed(0)
     layer = LSSO(LSSOConfig(dim=256, num_heads=8, rank=32, bias=True)).cuda().eval()
@@ -397,10 +403,14 @@ def test_headline_shell_slice_matches_oracle(native, length: int) -> None:
     assert torch.isfinite(out).all()
     picks = [0, 17, 63]
     expected = oracle.lsso_forward(_oracle_params(layer), _config_dict(layer.config), x[picks].double())
+    fp32 = oracle.lsso_forward(_oracle_params_fp32(layer), _config_dict(layer.config), x[picks].float())
+    name = "C2" if length == 1024 else "C3"
+    parity_report.record(f"{name} B64 D256 H8 r32 L{length} fp16 (samples 0,17,63)", out[picks], fp32,
+                         expected)
     assert _rel_l2(out[picks], expected) <= 5e-3
 
 
-def test_masked_bf16_config_c4_slice(native) -> None:
+def test_masked_bf16_config_c4_slice(native, parity_report) -> None:
     """C4: B=32, D=384, H=6 (d=64), r=64, BF16, trailing-padding masks with
     valid lengths in [L/4, L], per-sample positions start ~ U[0, 1024)."""
 
@@ -422,4 +432,7 @@ def test_masked_bf16_config_c4_slice(native) -> None:
     picks = [int(lengths.argmin()), int(lengths.argmax()), 5]
     expected = oracle.lsso_forward(_oracle_params(layer), _config_dict(layer.config), x[picks].double(),
                                    mask[picks], position_ids[picks])
+    fp32 = oracle.lsso_forward(_oracle_params_fp32(layer), _config_dict(layer.config), x[picks].float(),
+                               mask[picks], position_ids[picks])
+    parity_report.record("C4 B32 D384 H6 r64 L4096 bf16 masked (3 samples)", out[picks], fp32, expected)
     assert _rel_l2(out[picks], expected) <= 5e-3
