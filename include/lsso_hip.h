@@ -151,7 +151,8 @@ int lsso_hip_mixer_backward_workspace_bytes(const lsso_hip_mixer_shape* shape,
  * heads*head_dim] (masked rows zero); outputs grad_projected bfloat16 like
  * projected, and float32 grad_base [H, r, r], grad_drive [H, d, r] and
  * grad_eta [H] (sums over the batch in a fixed order: deterministic).
- * head_dim <= 64.  Positions, counts and inverse_frequency as in the forward.
+ * Any head_dim (heads wider than 64 take the compact VJP in 32-column
+ * panels).  Positions, counts and inverse_frequency as in the forward.
  * Replaces: torch.ops.lsso_equilibrium.backward (csrc/ball/binding.cpp:92-95,
  * csrc/ball/backward.cu:1386-1667, lsso/ball/cuda.py:256-280). */
 int lsso_hip_mixer_backward(const lsso_hip_mixer_shape* shape,

@@ -35,8 +35,7 @@ constexpr int kBwdThreads = 256;
 constexpr int kBwdMaxHeadDim = 64;
 
 bool backward_supported(int64_t rank, int64_t head_dim) {
-    return (rank == 16 || rank == 32 || rank == 48 || rank == 64) && head_dim >= 1 &&
-           head_dim <= kBwdMaxHeadDim;
+    return (rank == 16 || rank == 32 || rank == 48 || rank == 64) && head_dim >= 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -376,6 +375,270 @@ __global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) 
     write_records<kRank32>(rec + a.off_f, d, R, [&](int f, int k) { return s_u[k * PD + f] * inv_root; });
 }
 
+// Records of rows [rb0, rb1) x K steps [s0, s1) of an M x K matrix whose
+// full record has `steps` K steps (the layout of write_records).
+template <bool K32, typename Value>
+__device__ __forceinline__ void write_record_block(uint16_t* out, int rows, int cols, int rb0, int rb1,
+                                                   int s0, int s1, Value value) {
+    using RS = RecordShape<K32>;
+    const int steps = (cols + RS::kWidth - 1) / RS::kWidth;
+    const int width = s1 - s0;
+    const int lanes = (rb1 - rb0) * width * 64;
+    for (int idx = threadIdx.x; idx < lanes; idx += blockDim.x) {
+        const int lane = idx & 63;
+        const int step = s0 + (idx >> 6) % width;
+        const int rb = rb0 + (idx >> 6) / width;
+        const int row = 16 * rb + (lane & 15);
+        const int k0 = RS::kWidth * step + RS::kPerLane * (lane >> 4);
+        uint16_t* rec = out + ((static_cast<int64_t>(rb) * steps + step) * 64 + lane) * RS::kLaneHalfs;
+#pragma unroll
+        for (int i = 0; i < RS::kPerLane; i += 2) {
+            const float v0 = (row < rows && k0 + i < cols) ? value(row, k0 + i) : 0.0f;
+            const float v1 = (row < rows && k0 + i + 1 < cols) ? value(row, k0 + i + 1) : 0.0f;
+            uint32_t hi, lo;
+            split_bf16(v0, v1, hi, lo);
+            *reinterpret_cast<uint32_t*>(rec + i) = hi;
+            *reinterpret_cast<uint32_t*>(rec + RS::kPerLane + i) = lo;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Compact backward of one system for head_dim > 64: the algebra of
+// bwd_solve_kernel with the r x d quantities taken in panels of kWidePanel
+// columns, so that LDS holds only r x r matrices and one panel of each r x d
+// one.  The columns of every r x d product are independent, except for the
+// sums over d: dK = -v u^T (needed before dTheta, which every panel's dz
+// needs) and Lbar = -(m dx^T + ds z^T).  Pass 1 accumulates dK over the
+// panels; pass 2 recomputes each panel's m, dx and v from the tape and the dm
+// partials, then forms dz, ds, the Lbar sum, the <dx, z> sum, the drive
+// gradient rows and the panel's token-map records.
+constexpr int kWidePanel = 32;
+
+template <int R>
+__global__ __launch_bounds__(kBwdThreads) void bwd_solve_wide_kernel(BwdSolveArgs a) {
+    constexpr int PR = R + 1;
+    constexpr int PP = kWidePanel + 1;
+    __shared__ float s_linv[R * PR];
+    __shared__ float s_kinv[R * PR];   // (I+K)^-1 -> L (after pass 2)
+    __shared__ float s_f[R * PR];      // Theta -> F -> Lbar -> Mbar
+    __shared__ float s_dk[R * PR];     // dK -> L^-T P -> Mbar sym
+    __shared__ float s_d[R * PR];      // dF -> dTheta -> P
+    __shared__ float s_z[R * PP];
+    __shared__ float s_u[R * PP];      // u -> ds
+    __shared__ float s_dx[R * PP];
+    __shared__ float s_m[R * PP];
+    __shared__ float s_v[R * PP];      // dm -> v -> dz
+    __shared__ float s_diag[R];
+    __shared__ float s_red[kBwdThreads / 64];
+
+    const int tid = threadIdx.x;
+    const int64_t system = blockIdx.x;
+    const int64_t b = system / a.heads;
+    const int64_t h = system - b * a.heads;
+    const int d = static_cast<int>(a.head_dim);
+    const float count = a.valid_counts != nullptr ? a.valid_counts[b] : static_cast<float>(a.length);
+    const float root = sqrtf(count);
+    const float inv_root = 1.0f / root;
+    const float eta = bounded_complement(a.eta_raw[h]);
+    const float* tape = a.tape + system * a.tape_stride;
+    const float* tape_z = tape + 4 * R * R;
+    const float* tape_u = tape_z + R * d;
+    const float* part = a.partials + system * a.chunks * a.partial_stride + R * R;
+    const float* drive = a.drive + h * d * R;
+    const int chunks = static_cast<int>(a.chunks);
+    const int stride = static_cast<int>(a.partial_stride);
+
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        s_linv[i * PR + j] = tape[3 * R * R + idx];
+        s_kinv[i * PR + j] = tape[2 * R * R + idx];
+        s_f[i * PR + j] = tape[R * R + idx];
+        s_dk[i * PR + j] = 0.0f;
+    }
+
+    // A panel's z, u and dm / sqrt(n) (chunk partials summed in order) into LDS.
+    auto load_panel = [&](int c0, int w) {
+        for (int idx = tid; idx < R * w; idx += kBwdThreads) {
+            const int i = idx / w;
+            const int f = c0 + (idx - i * w);
+            float dm = 0.0f;
+            for (int ch = 0; ch < chunks; ++ch) {
+                dm += part[ch * stride + i * d + f];
+            }
+            s_z[i * PP + f - c0] = tape_z[i * d + f];
+            s_u[i * PP + f - c0] = tape_u[i * d + f];
+            s_v[i * PP + f - c0] = dm / root;
+        }
+    };
+    // dx = L^-1 dm (s_v -> s_dx), then v = (I + K)^-T (2 dx) (-> s_v).
+    auto panel_dx_v = [&](int w) {
+        block_product<R>(R, w, R, [&](int i, int k) { return s_linv[i * PR + k]; },
+                         [&](int k, int j) { return s_v[k * PP + j]; },
+                         [&](int i, int j, float v) { s_dx[i * PP + j] = v; });
+        __syncthreads();
+        block_product<R>(R, w, R, [&](int i, int k) { return s_kinv[k * PR + i]; },
+                         [&](int k, int j) { return 2.0f * s_dx[k * PP + j]; },
+                         [&](int i, int j, float v) { s_v[i * PP + j] = v; });
+        __syncthreads();
+    };
+    __syncthreads();
+
+    // ---- pass 1: dK = -sum over panels of v u^T ------------------------------
+    for (int c0 = 0; c0 < d; c0 += kWidePanel) {
+        const int w = d - c0 < kWidePanel ? d - c0 : kWidePanel;
+        load_panel(c0, w);
+        __syncthreads();
+        panel_dx_v(w);
+        block_product<kWidePanel>(R, R, w, [&](int i, int k) { return s_v[i * PP + k]; },
+                                  [&](int k, int j) { return s_u[j * PP + k]; },
+                                  [&](int i, int j, float v) { s_dk[i * PR + j] -= v; });
+        __syncthreads();
+    }
+
+    // ---- F, dF = (dK + dK^T) F, dTheta ---------------------------------------
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        const float theta = s_f[i * PR + j];
+        float value = j < i ? theta : 0.0f;
+        if (i == j) {
+            s_diag[i] = theta;
+            value = softplus_one(theta);
+        }
+        s_f[i * PR + j] = value;
+    }
+    __syncthreads();
+    block_product<R>(R, R, R, [&](int i, int k) { return s_dk[i * PR + k] + s_dk[k * PR + i]; },
+                     [&](int k, int j) { return s_f[k * PR + j]; },
+                     [&](int i, int j, float v) { s_d[i * PR + j] = v; });
+    __syncthreads();
+    float* dtheta = a.dtheta_part + system * R * R;
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        float g;
+        if (j < i) {
+            g = s_d[i * PR + j];
+        } else if (j == i) {
+            const float shifted = s_diag[i] + kSoftplusOneOffset;
+            g = s_d[i * PR + j] / (1.0f + expf(-shifted));
+        } else {
+            g = s_dk[i * PR + j] - s_dk[j * PR + i];
+        }
+        s_d[i * PR + j] = g;
+        dtheta[idx] = g;
+        s_f[i * PR + j] = 0.0f;   // Lbar accumulator
+    }
+    __syncthreads();
+
+    // ---- pass 2 ---------------------------------------------------------------
+    uint16_t* rec = a.records + system * a.record_stride;
+    float* ddrive = a.ddrive_part + system * d * R;
+    float dot = 0.0f;
+    for (int c0 = 0; c0 < d; c0 += kWidePanel) {
+        const int w = d - c0 < kWidePanel ? d - c0 : kWidePanel;
+        load_panel(c0, w);
+        __syncthreads();
+        // m = L^-T x with x = 2 u - (1 + eta) z.
+        block_product<R>(R, w, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+                         [&](int k, int j) { return 2.0f * s_u[k * PP + j] - (1.0f + eta) * s_z[k * PP + j]; },
+                         [&](int i, int j, float v) { s_m[i * PP + j] = v; });
+        panel_dx_v(w);
+        // Drive gradient rows c0 .. c0 + w: z^T dTheta / sqrt(n).
+        block_product<R>(w, R, R, [&](int f, int k) { return s_z[k * PP + f]; },
+                         [&](int k, int j) { return s_d[k * PR + j]; },
+                         [&](int f, int j, float v) { ddrive[(c0 + f) * R + j] = v / root; });
+        // dz = -(1 + eta) dx + v + dTheta W^T / sqrt(n), in place in s_v.
+        block_product<R>(R, w, R, [&](int i, int k) { return s_d[i * PR + k]; },
+                         [&](int k, int f) { return drive[(c0 + f) * R + k]; },
+                         [&](int i, int f, float v) {
+                             s_v[i * PP + f] = -(1.0f + eta) * s_dx[i * PP + f] + s_v[i * PP + f] + v / root;
+                         });
+        for (int idx = tid; idx < R * w; idx += kBwdThreads) {
+            const int i = idx / w;
+            const int f = idx - i * w;
+            dot = fmaf(s_dx[i * PP + f], s_z[i * PP + f], dot);
+        }
+        __syncthreads();
+        // ds = L^-T dz -> s_u (u is spent: m holds what it fed).
+        block_product<R>(R, w, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+                         [&](int k, int j) { return s_v[k * PP + j]; },
+                         [&](int i, int j, float v) { s_u[i * PP + j] = v; });
+        __syncthreads();
+        // Lbar sum: + m dx^T + ds z^T (each element stays with one lane).
+        block_product<kWidePanel>(R, R, w, [&](int i, int f) { return s_m[i * PP + f]; },
+                                  [&](int f, int j) { return s_dx[j * PP + f]; },
+                                  [&](int i, int j, float v) { s_f[i * PR + j] += v; });
+        block_product<kWidePanel>(R, R, w, [&](int i, int f) { return s_u[i * PP + f]; },
+                                  [&](int f, int j) { return s_z[j * PP + f]; },
+                                  [&](int i, int j, float v) { s_f[i * PR + j] += v; });
+        // Token-map records of this panel's columns (M' = m / sqrt(n) and
+        // ds / sqrt(n)) and rows (ds^T / sqrt(n)).
+        if (a.feature_k32) {
+            write_record_block<true>(rec + a.off_m, R, d, 0, R / 16, c0 / 32, (c0 + w + 31) / 32,
+                                     [&](int i, int f) { return s_m[i * PP + f - c0] * inv_root; });
+            write_record_block<true>(rec + a.off_e, R, d, 0, R / 16, c0 / 32, (c0 + w + 31) / 32,
+                                     [&](int i, int f) { return s_u[i * PP + f - c0] * inv_root; });
+        } else {
+            write_record_block<false>(rec + a.off_m, R, d, 0, R / 16, c0 / 16, (c0 + w + 15) / 16,
+                                      [&](int i, int f) { return s_m[i * PP + f - c0] * inv_root; });
+            write_record_block<false>(rec + a.off_e, R, d, 0, R / 16, c0 / 16, (c0 + w + 15) / 16,
+                                      [&](int i, int f) { return s_u[i * PP + f - c0] * inv_root; });
+        }
+        constexpr bool kRank32 = (R % 32) == 0;
+        write_record_block<kRank32>(rec + a.off_f, d, R, c0 / 16, (c0 + w + 15) / 16, 0,
+                                    R / RecordShape<kRank32>::kWidth,
+                                    [&](int f, int k) { return s_u[k * PP + f - c0] * inv_root; });
+        __syncthreads();
+    }
+
+    // ---- -<dx, z> --------------------------------------------------------------
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        dot += __shfl_xor(dot, offset);
+    }
+    if ((tid & 63) == 0) {
+        s_red[tid >> 6] = dot;
+    }
+    // ---- Lbar = tril(-(m dx^T + ds z^T)); L -> s_kinv --------------------------
+    for (int idx = tid; idx < R * R; idx += kBwdThreads) {
+        const int i = idx / R;
+        const int j = idx - i * R;
+        s_f[i * PR + j] = j <= i ? -s_f[i * PR + j] : 0.0f;
+        s_kinv[i * PR + j] = tape[idx];
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float total = 0.0f;
+        for (int w = 0; w < kBwdThreads / 64; ++w) {
+            total += s_red[w];
+        }
+        a.deta_part[system] = -total;
+    }
+    // ---- P = Phi(L^T Lbar) -> s_d ---------------------------------------------
+    block_product<R>(R, R, R, [&](int i, int k) { return s_kinv[k * PR + i]; },
+                     [&](int k, int j) { return s_f[k * PR + j]; },
+                     [&](int i, int j, float v) {
+                         s_d[i * PR + j] = j < i ? v : (j == i ? 0.5f * v : 0.0f);
+                     });
+    __syncthreads();
+    // ---- Mbar = L^-T P L^-1 ----------------------------------------------------
+    block_product<R>(R, R, R, [&](int i, int k) { return s_d[i * PR + k]; },
+                     [&](int k, int j) { return s_linv[k * PR + j]; },
+                     [&](int i, int j, float v) { s_f[i * PR + j] = v; });
+    __syncthreads();
+    block_product<R>(R, R, R, [&](int i, int k) { return s_linv[k * PR + i]; },
+                     [&](int k, int j) { return s_f[k * PR + j]; },
+                     [&](int i, int j, float v) { s_dk[i * PR + j] = v; });
+    __syncthreads();
+    const float inv_count = 1.0f / count;
+    constexpr bool kRank32 = (R % 32) == 0;
+    write_records<kRank32>(rec + a.off_g, R, R, [&](int i, int k) {
+        return (s_dk[i * PR + k] + s_dk[k * PR + i]) * inv_count;
+    });
+}
+
 // ---------------------------------------------------------------------------
 // Token map: one wave per (b, chunk, h), 16 tokens per step.
 template <int R, bool DK32, bool VEC>
@@ -441,78 +704,146 @@ __global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
                 a_lo[s][p] = lo;
             }
         }
-        // dY and C as B operands (feature K; exact in BF16), plus <dY, C>.
+        // Features are taken in panels of kBwdMaxHeadDim: dY and C of one
+        // panel are the B operands of its feature-K steps (exact in BF16);
+        // the dA^T accumulators of every rank block run across all panels,
+        // and the panel's dC blocks are finished inside it.  With one panel
+        // (head_dim <= 64) the MFMA chains and the <dY, C> order are those of
+        // the resident token map.
         typedef typename std::conditional<DK32, u32x4, u32x2>::type FeatOp;
-        FeatOp y_op[kBwdMaxHeadDim / 16];
-        FeatOp c_op[kBwdMaxHeadDim / 16];
+        constexpr int kPanelSteps = kBwdMaxHeadDim / RD::kWidth;
+        constexpr int kPanelBlocks = kBwdMaxHeadDim / 16;
+        f32x4 acc_d[RBLK];
 #pragma unroll
-        for (int s = 0; s < kBwdMaxHeadDim / RD::kWidth; ++s) {
-            if (s < dsteps) {
-                const int first = RD::kWidth * s + RD::kPerLane * g;
-                if constexpr (VEC) {
-                    // d is a multiple of the per-lane run: whole runs or none.
-                    const bool run = live && first < d;
-                    y_op[s] = run ? *reinterpret_cast<const FeatOp*>(grow + (run ? first : 0))
-                                  : FeatOp{};
-                    c_op[s] = run ? *reinterpret_cast<const FeatOp*>(crow + (run ? first : 0))
-                                  : FeatOp{};
+        for (int rb = 0; rb < RBLK; ++rb) {
+            acc_d[rb] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        for (int panel = 0; panel * kPanelSteps < dsteps; ++panel) {
+            const int s0 = panel * kPanelSteps;
+            FeatOp y_op[kPanelSteps];
+            FeatOp c_op[kPanelSteps];
 #pragma unroll
-                    for (int p = 0; p < RD::kPerLane / 2; ++p) {
-                        dot = fmaf(bf16_lo(y_op[s][p]), bf16_lo(c_op[s][p]), dot);
-                        dot = fmaf(bf16_hi(y_op[s][p]), bf16_hi(c_op[s][p]), dot);
-                    }
-                } else {
+            for (int ps = 0; ps < kPanelSteps; ++ps) {
+                const int s = s0 + ps;
+                y_op[ps] = FeatOp{};
+                c_op[ps] = FeatOp{};
+                if (s < dsteps) {
+                    const int first = RD::kWidth * s + RD::kPerLane * g;
+                    if constexpr (VEC) {
+                        // d is a multiple of the per-lane run: whole runs or none.
+                        const bool run = live && first < d;
+                        y_op[ps] = run ? *reinterpret_cast<const FeatOp*>(grow + (run ? first : 0))
+                                       : FeatOp{};
+                        c_op[ps] = run ? *reinterpret_cast<const FeatOp*>(crow + (run ? first : 0))
+                                       : FeatOp{};
 #pragma unroll
-                    for (int p = 0; p < RD::kPerLane / 2; ++p) {
-                        const int f = first + 2 * p;
-                        uint32_t yv = 0u, cv = 0u;
-                        if (live && f < d) {
-                            const uint32_t y_lo = grow[f];
-                            const uint32_t c_lo = crow[f];
-                            const uint32_t y_hi = f + 1 < d ? grow[f + 1] : 0u;
-                            const uint32_t c_hi = f + 1 < d ? crow[f + 1] : 0u;
-                            yv = y_lo | (y_hi << 16);
-                            cv = c_lo | (c_hi << 16);
+                        for (int p = 0; p < RD::kPerLane / 2; ++p) {
+                            dot = fmaf(bf16_lo(y_op[ps][p]), bf16_lo(c_op[ps][p]), dot);
+                            dot = fmaf(bf16_hi(y_op[ps][p]), bf16_hi(c_op[ps][p]), dot);
                         }
-                        y_op[s][p] = yv;
-                        c_op[s][p] = cv;
-                        dot = fmaf(bf16_lo(yv), bf16_lo(cv), dot);
-                        dot = fmaf(bf16_hi(yv), bf16_hi(cv), dot);
+                    } else {
+#pragma unroll
+                        for (int p = 0; p < RD::kPerLane / 2; ++p) {
+                            const int f = first + 2 * p;
+                            uint32_t yv = 0u, cv = 0u;
+                            if (live && f < d) {
+                                const uint32_t y_lo = grow[f];
+                                const uint32_t c_lo = crow[f];
+                                const uint32_t y_hi = f + 1 < d ? grow[f + 1] : 0u;
+                                const uint32_t c_hi = f + 1 < d ? crow[f + 1] : 0u;
+                                yv = y_lo | (y_hi << 16);
+                                cv = c_lo | (c_hi << 16);
+                            }
+                            y_op[ps][p] = yv;
+                            c_op[ps][p] = cv;
+                            dot = fmaf(bf16_lo(yv), bf16_lo(cv), dot);
+                            dot = fmaf(bf16_hi(yv), bf16_hi(cv), dot);
+                        }
+                    }
+                }
+            }
+
+            // dA^T blocks, feature-K chain (dY, C): this panel's steps.
+#pragma unroll
+            for (int rb = 0; rb < RBLK; ++rb) {
+#pragma unroll
+                for (int ps = 0; ps < kPanelSteps; ++ps) {
+                    const int s = s0 + ps;
+                    if (s < dsteps) {
+                        const int64_t o = ((static_cast<int64_t>(rb) * dsteps + s) * 64 + lane) * RD::kLaneHalfs;
+                        if constexpr (DK32) {
+                            const u32x4 mh = *reinterpret_cast<const u32x4*>(rec_m + o);
+                            const u32x4 ml = *reinterpret_cast<const u32x4*>(rec_m + o + 8);
+                            const u32x4 eh = *reinterpret_cast<const u32x4*>(rec_e + o);
+                            const u32x4 el = *reinterpret_cast<const u32x4*>(rec_e + o + 8);
+                            acc_d[rb] = mfma16x16x32(mh, y_op[ps], acc_d[rb]);
+                            acc_d[rb] = mfma16x16x32(ml, y_op[ps], acc_d[rb]);
+                            acc_d[rb] = mfma16x16x32(eh, c_op[ps], acc_d[rb]);
+                            acc_d[rb] = mfma16x16x32(el, c_op[ps], acc_d[rb]);
+                        } else {
+                            const u32x2 mh = *reinterpret_cast<const u32x2*>(rec_m + o);
+                            const u32x2 ml = *reinterpret_cast<const u32x2*>(rec_m + o + 4);
+                            const u32x2 eh = *reinterpret_cast<const u32x2*>(rec_e + o);
+                            const u32x2 el = *reinterpret_cast<const u32x2*>(rec_e + o + 4);
+                            acc_d[rb] = mfma16x16x16(mh, y_op[ps], acc_d[rb]);
+                            acc_d[rb] = mfma16x16x16(ml, y_op[ps], acc_d[rb]);
+                            acc_d[rb] = mfma16x16x16(eh, c_op[ps], acc_d[rb]);
+                            acc_d[rb] = mfma16x16x16(el, c_op[ps], acc_d[rb]);
+                        }
+                    }
+                }
+            }
+
+            // dC^T blocks of this panel: eta dY + (ds / sqrt(n))^T A^T.
+#pragma unroll
+            for (int pb = 0; pb < kPanelBlocks; ++pb) {
+                const int fb = panel * kPanelBlocks + pb;
+                if (fb < fblocks) {
+                    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int s = 0; s < RSTEPS; ++s) {
+                        const int64_t o = ((static_cast<int64_t>(fb) * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
+                        if constexpr (RK32) {
+                            const u32x4 fh = *reinterpret_cast<const u32x4*>(rec_f + o);
+                            const u32x4 fl = *reinterpret_cast<const u32x4*>(rec_f + o + 8);
+                            acc = mfma16x16x32(fh, a_hi[s], acc);
+                            acc = mfma16x16x32(fh, a_lo[s], acc);
+                            acc = mfma16x16x32(fl, a_hi[s], acc);
+                        } else {
+                            const u32x2 fh = *reinterpret_cast<const u32x2*>(rec_f + o);
+                            const u32x2 fl = *reinterpret_cast<const u32x2*>(rec_f + o + 4);
+                            acc = mfma16x16x16(fh, a_hi[s], acc);
+                            acc = mfma16x16x16(fh, a_lo[s], acc);
+                            acc = mfma16x16x16(fl, a_hi[s], acc);
+                        }
+                    }
+                    if (live) {
+                        const int f0 = 16 * fb + 4 * g;
+                        if (VEC && f0 + 4 <= d) {
+                            const u32x2 dy = *reinterpret_cast<const u32x2*>(grow + f0);
+                            u32x2 packed;
+                            packed.x = pack_bf16(fmaf(eta, bf16_lo(dy.x), acc[0]), fmaf(eta, bf16_hi(dy.x), acc[1]));
+                            packed.y = pack_bf16(fmaf(eta, bf16_lo(dy.y), acc[2]), fmaf(eta, bf16_hi(dy.y), acc[3]));
+                            *reinterpret_cast<u32x2*>(out_row + a.heads * R + h * d + f0) = packed;
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                if (f0 + i < d) {
+                                    const float dy = bf16_bits_to_float(grow[f0 + i]);
+                                    out_row[a.heads * R + h * d + f0 + i] = to_bf16_bits(fmaf(eta, dy, acc[i]));
+                                }
+                            }
+                        }
                     }
                 }
             }
         }
 
-        // dA^T blocks: feature-K chain (dY, C) and rank-K chain (A) kept apart.
+        // dA^T blocks, rank-K chain (A, kept apart from the feature chain),
+        // then the rotation back to dR.
 #pragma unroll
         for (int rb = 0; rb < RBLK; ++rb) {
-            f32x4 acc_d = {0.0f, 0.0f, 0.0f, 0.0f};
             f32x4 acc_r = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < kBwdMaxHeadDim / RD::kWidth; ++s) {
-                if (s < dsteps) {
-                    const int64_t o = ((static_cast<int64_t>(rb) * dsteps + s) * 64 + lane) * RD::kLaneHalfs;
-                    if constexpr (DK32) {
-                        const u32x4 mh = *reinterpret_cast<const u32x4*>(rec_m + o);
-                        const u32x4 ml = *reinterpret_cast<const u32x4*>(rec_m + o + 8);
-                        const u32x4 eh = *reinterpret_cast<const u32x4*>(rec_e + o);
-                        const u32x4 el = *reinterpret_cast<const u32x4*>(rec_e + o + 8);
-                        acc_d = mfma16x16x32(mh, y_op[s], acc_d);
-                        acc_d = mfma16x16x32(ml, y_op[s], acc_d);
-                        acc_d = mfma16x16x32(eh, c_op[s], acc_d);
-                        acc_d = mfma16x16x32(el, c_op[s], acc_d);
-                    } else {
-                        const u32x2 mh = *reinterpret_cast<const u32x2*>(rec_m + o);
-                        const u32x2 ml = *reinterpret_cast<const u32x2*>(rec_m + o + 4);
-                        const u32x2 eh = *reinterpret_cast<const u32x2*>(rec_e + o);
-                        const u32x2 el = *reinterpret_cast<const u32x2*>(rec_e + o + 4);
-                        acc_d = mfma16x16x16(mh, y_op[s], acc_d);
-                        acc_d = mfma16x16x16(ml, y_op[s], acc_d);
-                        acc_d = mfma16x16x16(eh, c_op[s], acc_d);
-                        acc_d = mfma16x16x16(el, c_op[s], acc_d);
-                    }
-                }
-            }
 #pragma unroll
             for (int s = 0; s < RSTEPS; ++s) {
                 const int64_t o = ((static_cast<int64_t>(rb) * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
@@ -537,7 +868,7 @@ __global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
                 float grad[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    grad[i] = acc_d[i] + acc_r[i];
+                    grad[i] = acc_d[rb][i] + acc_r[i];
                 }
                 u32x2 packed;
 #pragma unroll
@@ -549,48 +880,6 @@ __global__ __launch_bounds__(256) void bwd_apply_kernel(BwdApplyArgs a) {
                     packed[p] = pack_bf16(even, odd);
                 }
                 *reinterpret_cast<u32x2*>(out_row + h * R + rank0) = packed;
-            }
-        }
-        // dC^T blocks: eta dY + (ds / sqrt(n))^T A^T.
-#pragma unroll
-        for (int fb = 0; fb < kBwdMaxHeadDim / 16; ++fb) {
-            if (fb < fblocks) {
-                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int s = 0; s < RSTEPS; ++s) {
-                    const int64_t o = ((static_cast<int64_t>(fb) * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
-                    if constexpr (RK32) {
-                        const u32x4 fh = *reinterpret_cast<const u32x4*>(rec_f + o);
-                        const u32x4 fl = *reinterpret_cast<const u32x4*>(rec_f + o + 8);
-                        acc = mfma16x16x32(fh, a_hi[s], acc);
-                        acc = mfma16x16x32(fh, a_lo[s], acc);
-                        acc = mfma16x16x32(fl, a_hi[s], acc);
-                    } else {
-                        const u32x2 fh = *reinterpret_cast<const u32x2*>(rec_f + o);
-                        const u32x2 fl = *reinterpret_cast<const u32x2*>(rec_f + o + 4);
-                        acc = mfma16x16x16(fh, a_hi[s], acc);
-                        acc = mfma16x16x16(fh, a_lo[s], acc);
-                        acc = mfma16x16x16(fl, a_hi[s], acc);
-                    }
-                }
-                if (live) {
-                    const int f0 = 16 * fb + 4 * g;
-                    if (VEC && f0 + 4 <= d) {
-                        const u32x2 dy = *reinterpret_cast<const u32x2*>(grow + f0);
-                        u32x2 packed;
-                        packed.x = pack_bf16(fmaf(eta, bf16_lo(dy.x), acc[0]), fmaf(eta, bf16_hi(dy.x), acc[1]));
-                        packed.y = pack_bf16(fmaf(eta, bf16_lo(dy.y), acc[2]), fmaf(eta, bf16_hi(dy.y), acc[3]));
-                        *reinterpret_cast<u32x2*>(out_row + a.heads * R + h * d + f0) = packed;
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            if (f0 + i < d) {
-                                const float dy = bf16_bits_to_float(grow[f0 + i]);
-                                out_row[a.heads * R + h * d + f0 + i] = to_bf16_bits(fmaf(eta, dy, acc[i]));
-                            }
-                        }
-                    }
-                }
             }
         }
     }
@@ -999,6 +1288,15 @@ int64_t bwd_record_layout(int64_t rank, int64_t head_dim, int64_t* off_m, int64_
 
 hipError_t launch_bwd_solve(int rank, const BwdSolveArgs& a, int64_t systems, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(systems));
+    if (a.head_dim > kBwdMaxHeadDim) {
+        switch (rank) {
+            case 16: bwd_solve_wide_kernel<16><<<grid, kBwdThreads, 0, stream>>>(a); break;
+            case 32: bwd_solve_wide_kernel<32><<<grid, kBwdThreads, 0, stream>>>(a); break;
+            case 48: bwd_solve_wide_kernel<48><<<grid, kBwdThreads, 0, stream>>>(a); break;
+            default: bwd_solve_wide_kernel<64><<<grid, kBwdThreads, 0, stream>>>(a); break;
+        }
+        return hipGetLastError();
+    }
     const bool small = a.head_dim <= 32;
     switch (rank) {
         case 16: small ? bwd_solve_kernel<16, 32><<<grid, kBwdThreads, 0, stream>>>(a)

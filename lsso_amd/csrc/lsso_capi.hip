@@ -661,8 +661,8 @@ struct BackwardPlan {
 int make_backward_plan(const MixerPlan& plan, BackwardPlan* bp) {
     if (!lsso_hip::backward_supported(plan.rank, plan.head_dim)) {
         return fail(LSSO_HIP_EUNSUPPORTED,
-                    "the HIP mixer backward supports head_dim <= 64, got " +
-                        std::to_string(plan.head_dim));
+                    "the HIP mixer backward supports rank in {16, 32, 48, 64}, got " +
+                        std::to_string(plan.rank));
     }
     bp->record_stride = lsso_hip::bwd_record_layout(plan.rank, plan.head_dim, &bp->off_m, &bp->off_e,
                                                     &bp->off_g, &bp->off_f, &bp->feature_k32);

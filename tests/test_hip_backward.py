@@ -173,3 +173,27 @@ def test_backward_column_sums_match_grad_projected(native, batch, rank, heads, h
         assert torch.equal(a, b)
     expected = grads[0].double().sum(dim=(0, 1))
     torch.testing.assert_close(sums.double(), expected, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize(("dim", "heads", "rank"), [(256, 2, 32), (192, 1, 64)])
+def test_module_wide_head_gradients_match_oracle_autograd(native, dim, heads, rank):
+    """head_dim 128 and 192: the panel-looped compact VJP and token map."""
+
+    torch.manual_seed(17 + dim)
+    config = LSSOConfig(dim=dim, num_heads=heads, rank=rank, bias=True)
+    layer = LSSO(config).cuda()
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.05)
+        layer.core_drive_weight.normal_(std=0.05)
+    x = torch.randn(2, 150, dim, generator=torch.Generator().manual_seed(18)).half().cuda().requires_grad_()
+    upstream = torch.randn(2, 150, dim, generator=torch.Generator().manual_seed(19))
+    y = layer(x, implementation="hip")
+    (y.float() * upstream.cuda()).sum().backward()
+    params = {name: p.detach().double().cpu().requires_grad_() for name, p in layer.named_parameters()}
+    x64 = x.detach().double().cpu().requires_grad_()
+    expected = oracle.lsso_forward(params, {"dim": dim, "num_heads": heads, "rank": rank, "bias": True}, x64)
+    (expected * upstream.double()).sum().backward()
+    assert _rel_l2(y, expected) <= 5e-3
+    assert _rel_l2(x.grad, x64.grad) <= GRAD_LIMIT
+    for name, parameter in layer.named_parameters():
+        assert _rel_l2(parameter.grad, params[name].grad) <= GRAD_LIMIT, (name, _rel_l2(parameter.grad, params[name].grad))

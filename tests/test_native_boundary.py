@@ -132,9 +132,13 @@ def test_backward_envelope_and_workspace(library) -> None:
     shape = _shape(heads=8, rank=48, head_dim=32, length=2048, batch=4)
     assert library.lsso_hip_mixer_backward_workspace_bytes(ctypes.byref(shape), 0, ctypes.byref(size)) == 0
     assert size.value > 0
-    wide = _shape(head_dim=65)
-    assert library.lsso_hip_mixer_backward_workspace_bytes(ctypes.byref(wide), 0, ctypes.byref(size)) == -2
-    assert "head_dim <= 64" in _message(library)
+    # Any head_dim: wide heads run the panel-looped compact VJP.
+    for head_dim in (65, 257, 512):
+        wide = _shape(head_dim=head_dim)
+        assert library.lsso_hip_mixer_backward_workspace_bytes(ctypes.byref(wide), 0, ctypes.byref(size)) == 0
+        assert size.value > 0
+    bad_rank = _shape(rank=24)
+    assert library.lsso_hip_mixer_backward_workspace_bytes(ctypes.byref(bad_rank), 0, ctypes.byref(size)) == -2
 
 
 def test_linear_validation(library) -> None:
