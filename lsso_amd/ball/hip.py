@@ -1054,6 +1054,20 @@ def project_mix(
     return mixed
 
 
+def _rows(value: torch.Tensor, features: int) -> torch.Tensor:
+    """value as a [rows, features] matrix whose rows the native kernels can
+    address: unit feature stride and a row stride of at least `features`.
+    Broadcast views (an expanded input, or the upstream gradient of a sum,
+    whose row stride is 0) and other overlapping layouts are copied."""
+
+    flat = value.reshape(-1, features)
+    if flat.shape[0] > 1 and (flat.stride(-1) != 1 or flat.stride(0) < features):
+        flat = flat.contiguous()
+    elif flat.shape[0] <= 1 and flat.stride(-1) != 1:
+        flat = flat.contiguous()
+    return flat
+
+
 def _linear_forward(
     value: torch.Tensor,
     weight: torch.Tensor,
@@ -1080,9 +1094,7 @@ def _linear_forward(
         raise ValueError(
             f"projection input and weight features must agree, got {in_features} and {weight.shape[1]}"
         )
-    flat = value.reshape(-1, in_features)
-    if flat.stride(-1) != 1:
-        flat = flat.contiguous()
+    flat = _rows(value, in_features)
     rows = flat.shape[0]
     out_features = weight.shape[0]
     output = torch.empty(value.shape[:-1] + (out_features,), dtype=output_dtype, device=value.device)
@@ -1098,7 +1110,7 @@ def _linear_forward(
             dtype_codes[value.dtype],
             rows,
             in_features,
-            flat.stride(0) if rows > 0 else in_features,
+            flat.stride(0) if rows > 1 else in_features,
             weight.data_ptr(),
             None if bias is None else bias.data_ptr(),
             mask_ptr,
@@ -1142,7 +1154,7 @@ def _grad_columns(
             dtype_codes[flat.dtype],
             rows,
             cols,
-            flat.stride(0) if rows > 0 else cols,
+            flat.stride(0) if rows > 1 else cols,
             None if mask is None else mask.data_ptr(),
             None if copy is None else copy.data_ptr(),
             None if sums is None else sums.data_ptr(),
@@ -1236,8 +1248,8 @@ def _linear_vjp(
     runs on the native projection kernel from dY in its own dtype."""
 
     out_features, in_features = weight.shape
-    flat_grad = grad_output.reshape(-1, out_features)
-    if flat_grad.stride(-1) != 1 or flat_grad.dtype not in (torch.float16, torch.bfloat16):
+    flat_grad = _rows(grad_output, out_features)
+    if flat_grad.dtype not in (torch.float16, torch.bfloat16):
         flat_grad = flat_grad.to(dtype=torch.bfloat16).contiguous()
     native_value = value.dtype in (torch.float16, torch.bfloat16) and out_features <= 640
     need_bf16 = need_weight or (need_value and not native_value)
@@ -1261,7 +1273,7 @@ def _linear_vjp(
             grad_value = _mm_fp32(grad_bf16, weight.to(dtype=torch.bfloat16))
             grad_value = grad_value.to(dtype=value.dtype).reshape(value.shape)
     if need_weight:
-        flat_value = value.reshape(-1, in_features)
+        flat_value = _rows(value, in_features)
         if flat_value.dtype in (torch.float16, torch.bfloat16) and flat_value.stride(-1) == 1 and (
             flat_value.dtype != torch.bfloat16 or row_mask is not None
         ):

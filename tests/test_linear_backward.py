@@ -118,3 +118,53 @@ def test_projection_vjp_matches_reference_statement(
     torch.testing.assert_close(got_value, want_value, rtol=torch.finfo(dtype).eps, atol=1e-5)
     torch.testing.assert_close(weight.grad, d_weight, rtol=1e-4, atol=1e-3)
     torch.testing.assert_close(bias.grad, d_bias, rtol=1e-5, atol=1e-4)
+
+
+def test_projection_vjp_of_a_broadcast_upstream_gradient(native) -> None:
+    """loss = y.sum(dim=(0, 1)) . v hands the projection an upstream gradient
+    whose row strides are 0; the native VJP must see it as the dense tensor
+    it stands for."""
+
+    generator = torch.Generator(device="cuda").manual_seed(31)
+    value = torch.randn(3, 70, 64, device="cuda", generator=generator).half().requires_grad_(True)
+    weight = (0.1 * torch.randn(48, 64, device="cuda", generator=generator)).requires_grad_(True)
+    bias = torch.randn(48, device="cuda", generator=generator).requires_grad_(True)
+    direction = torch.randn(48, device="cuda", generator=generator)
+    out = native.linear(value, weight, bias, torch.float16)
+    (out.sum(dim=(0, 1)).float() * direction).sum().backward()
+    dense = direction.half().expand(3, 70, 48).contiguous()
+    d_value, d_weight, d_bias = _reference_vjp(value.detach(), weight.detach(), dense, None)
+    torch.testing.assert_close(value.grad, d_value, rtol=torch.finfo(torch.float16).eps, atol=1e-5)
+    torch.testing.assert_close(weight.grad, d_weight, rtol=1e-4, atol=1e-3)
+    torch.testing.assert_close(bias.grad, d_bias, rtol=1e-5, atol=1e-4)
+
+
+def test_module_trains_with_a_summed_loss_and_runs_on_expanded_x(native) -> None:
+    from lsso_amd import LSSO, LSSOConfig
+    from oracle import lsso_reference as oracle
+
+    torch.manual_seed(7)
+    layer = LSSO(LSSOConfig(dim=64, num_heads=2, rank=16, bias=True)).cuda()
+    base = torch.randn(1, 40, 64, generator=torch.Generator().manual_seed(8)).half()
+    expanded = base.cuda().expand(3, 40, 64)
+    with torch.no_grad():
+        out_expanded = layer(expanded, implementation="hip")
+        out_dense = layer(expanded.contiguous(), implementation="hip")
+    assert torch.equal(out_expanded, out_dense)
+
+    x = expanded.contiguous().requires_grad_(True)
+    direction = torch.randn(64, generator=torch.Generator().manual_seed(9))
+    y = layer(x, implementation="hip")
+    (y.float().sum(dim=(0, 1)) * direction.cuda()).sum().backward()
+    params = {name: p.detach().double().cpu().requires_grad_() for name, p in layer.named_parameters()}
+    x64 = x.detach().double().cpu().requires_grad_()
+    y64 = oracle.lsso_forward(params, {"dim": 64, "num_heads": 2, "rank": 16, "bias": True}, x64)
+    (y64.sum(dim=(0, 1)) * direction.double()).sum().backward()
+
+    def rel(a, e):
+        a = a.detach().double().cpu()
+        return float((a - e).norm() / e.norm())
+
+    assert rel(x.grad, x64.grad) <= 3e-2
+    for name, parameter in layer.named_parameters():
+        assert rel(parameter.grad, params[name].grad) <= 3e-2, name
