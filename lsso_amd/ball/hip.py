@@ -1251,7 +1251,7 @@ def _linear_vjp(
     flat_grad = _rows(grad_output, out_features)
     if flat_grad.dtype not in (torch.float16, torch.bfloat16):
         flat_grad = flat_grad.to(dtype=torch.bfloat16).contiguous()
-    native_value = value.dtype in (torch.float16, torch.bfloat16) and out_features <= 640
+    native_value = value.dtype in (torch.float16, torch.bfloat16)
     need_bf16 = need_weight or (need_value and not native_value)
     copy_grad = need_bf16 and (flat_grad.dtype != torch.bfloat16 or row_mask is not None)
     grad_bf16 = None

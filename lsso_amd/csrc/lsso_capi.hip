@@ -1024,12 +1024,6 @@ int lsso_hip_linear(const void* x, int x_dtype, int64_t rows, int64_t in_feature
     if (x_row_stride < in_features) {
         return fail(LSSO_HIP_EINVAL, "x_row_stride must be >= in_features");
     }
-    const int tier = lsso_hip::linear_k_tier(in_features);
-    if (tier == 0) {
-        return fail(LSSO_HIP_EUNSUPPORTED,
-                    "the HIP projection supports in_features <= 640, got " +
-                        std::to_string(in_features));
-    }
     if (rows == 0) {
         return LSSO_HIP_OK;
     }

@@ -24,6 +24,8 @@
 namespace lsso_hip {
 
 constexpr int kXcds = 8;   // accelerator complex dies of an MI355X
+constexpr int kStreamRowsHost = 128;   // tile of the K-streaming tier
+constexpr int kStreamColsHost = 128;
 
 // Rows per x tile: 64, or 32 once K exceeds 384.
 template <int KSTEPS>
@@ -39,8 +41,11 @@ constexpr int linear_waves() { return (KSTEPS <= 16 || KSTEPS >= 32) ? 8 : 4; }
 template <int KSTEPS>
 constexpr int linear_ksplit() { return KSTEPS >= 32 ? 2 : 1; }
 
-int linear_tile_rows(int k_steps) { return k_steps <= 24 ? 64 : 32; }
-int linear_columns_per_group(int k_steps) { return (k_steps <= 16 ? 8 : 4) * 32; }
+// Tier 0 is the K-streaming kernel (any in_features above 640).
+int linear_tile_rows(int k_steps) { return k_steps == 0 ? kStreamRowsHost : (k_steps <= 24 ? 64 : 32); }
+int linear_columns_per_group(int k_steps) {
+    return k_steps == 0 ? kStreamColsHost : (k_steps <= 16 ? 8 : 4) * 32;
+}
 
 int linear_k_tier(int64_t in_features) {
     if (in_features <= 64) return 4;
@@ -50,7 +55,7 @@ int linear_k_tier(int64_t in_features) {
     if (in_features <= 384) return 24;
     if (in_features <= 512) return 32;
     if (in_features <= 640) return 40;
-    return 0;
+    return 0;   // K-streaming tier
 }
 
 // Load 8 consecutive x elements as BF16 one element at a time (rows whose
@@ -351,6 +356,219 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     }
 }
 
+// ---------------------------------------------------------------------------
+// K-streaming tier (in_features > 640): the W rows no longer fit the waves'
+// registers, so both operands stream through LDS.  A workgroup of four waves
+// computes a 128-row x 128-column output tile; each wave a 64 x 64 quarter
+// (2 x 2 blocks of v_mfma_f32_32x32x16_bf16 on y^T = W x^T).  K is taken in
+// stages of 64: the x and W stages of k-tile t + 1 are loaded into registers
+// (W converted from FP32 to BF16, x from FP16 to BF16, round to nearest even)
+// while k-tile t is multiplied from the other LDS buffer.  The K order is one
+// FP32 chain per output, ascending.  Row tiles sharing x are dealt to one XCD.
+constexpr int kStreamRows = 128;
+constexpr int kStreamCols = 128;
+constexpr int kStreamK = 64;
+constexpr int kStreamThreads = 256;
+
+template <int XT, int YT>
+__global__ __launch_bounds__(kStreamThreads) void linear_stream_kernel(LinearArgs a) {
+    constexpr int KP = kStreamK + 8;                 // LDS row pitch (bf16)
+    constexpr int kChunks = kStreamRows * (kStreamK / 8) / kStreamThreads;   // 16-byte pieces per thread
+    constexpr int YP = kStreamCols + 8;
+    __shared__ __attribute__((aligned(16))) uint16_t s_x[2][kStreamRows * KP];
+    __shared__ __attribute__((aligned(16))) uint16_t s_w[2][kStreamCols * KP];
+    __shared__ __attribute__((aligned(16))) uint16_t s_y[kStreamRows * YP];
+    __shared__ __attribute__((aligned(16))) float s_bias[kStreamCols];
+    __shared__ int s_keep[kStreamRows];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int half = lane >> 5;
+    const int64_t M = a.rows;
+    const int64_t N = a.out_features;
+    const int64_t K = a.in_features;
+    const int64_t tiles_n = a.column_groups;
+    // Block b runs on XCD b % 8; the column tiles of one row tile share it.
+    const int64_t xcd = blockIdx.x % kXcds;
+    const int64_t slot = blockIdx.x / kXcds;
+    const int64_t mt = (slot / tiles_n) * kXcds + xcd;
+    const int64_t nt = slot % tiles_n;
+    if (mt >= a.tiles) {
+        return;
+    }
+    const int64_t m0 = mt * kStreamRows;
+    const int64_t n0 = nt * kStreamCols;
+    for (int c = tid; c < kStreamCols; c += kStreamThreads) {
+        const int64_t n = n0 + c;
+        s_bias[c] = (a.bias != nullptr && n < N) ? a.bias[n] : 0.0f;
+    }
+    for (int r = tid; r < kStreamRows; r += kStreamThreads) {
+        const int64_t m = m0 + r;
+        s_keep[r] = m < M && (a.row_mask == nullptr || a.row_mask[m] != 0);
+    }
+
+    const uint16_t* x = static_cast<const uint16_t*>(a.x);
+    u32x4 xs[kChunks];
+    f32x4 ws[kChunks][2];
+    // Piece i of this thread: row (tid + 256 i) / 8, columns 8 ((tid + 256 i) % 8) .. + 7.
+    auto load = [&](int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int piece = tid + i * kStreamThreads;
+            const int r = piece >> 3;
+            const int64_t k = k0 + 8 * (piece & 7);
+            const int64_t m = m0 + r;
+            const int64_t n = n0 + r;
+            if (a.x_vector) {
+                const bool live = m < M && k < K;
+                xs[i] = live ? *reinterpret_cast<const u32x4*>(x + m * a.x_stride + k) : u32x4{};
+            } else {
+                uint32_t v[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const uint32_t lo = (m < M && k + 2 * p < K) ? x[m * a.x_stride + k + 2 * p] : 0u;
+                    const uint32_t hi = (m < M && k + 2 * p + 1 < K) ? x[m * a.x_stride + k + 2 * p + 1] : 0u;
+                    v[p] = lo | (hi << 16);
+                }
+                xs[i] = (u32x4){v[0], v[1], v[2], v[3]};
+            }
+            if (K % 4 == 0) {
+                const bool live0 = n < N && k < K;
+                const bool live1 = n < N && k + 4 < K;
+                ws[i][0] = live0 ? *reinterpret_cast<const f32x4*>(a.weight + n * K + k) : f32x4{};
+                ws[i][1] = live1 ? *reinterpret_cast<const f32x4*>(a.weight + n * K + k + 4) : f32x4{};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const bool live = n < N && k + e < K;
+                    ws[i][e / 4][e % 4] = live ? a.weight[n * K + k + e] : 0.0f;
+                }
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int piece = tid + i * kStreamThreads;
+            const int r = piece >> 3;
+            const int c = 8 * (piece & 7);
+            u32x4 xv = xs[i];
+            if constexpr (XT == LSSO_HIP_F16) {
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    xv[p] = pack_bf16(f16_lo(xv[p]), f16_hi(xv[p]));
+                }
+            }
+            *reinterpret_cast<u32x4*>(&s_x[buf][r * KP + c]) = xv;
+            const u32x4 wv = {pack_bf16(ws[i][0][0], ws[i][0][1]), pack_bf16(ws[i][0][2], ws[i][0][3]),
+                              pack_bf16(ws[i][1][0], ws[i][1][1]), pack_bf16(ws[i][1][2], ws[i][1][3])};
+            *reinterpret_cast<u32x4*>(&s_w[buf][r * KP + c]) = wv;
+        }
+    };
+
+    const int wn = wave & 1;    // 64-column half of the tile
+    const int wm = wave >> 1;   // 64-row half of the tile
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                acc[nb][mb][e] = 0.0f;
+            }
+        }
+    }
+    const int64_t k_tiles = (K + kStreamK - 1) / kStreamK;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int64_t kt = 0; kt < k_tiles; ++kt) {
+        const int buf = static_cast<int>(kt & 1);
+        if (kt + 1 < k_tiles) {
+            load((kt + 1) * kStreamK);
+        }
+        const uint16_t* wt = s_w[buf];
+        const uint16_t* xt = s_x[buf];
+#pragma unroll
+        for (int kk = 0; kk < kStreamK / 16; ++kk) {
+            u32x4 wf[2];
+            u32x4 xf[2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                wf[b] = *reinterpret_cast<const u32x4*>(&wt[(wn * 64 + b * 32 + (lane & 31)) * KP + 16 * kk + 8 * half]);
+                xf[b] = *reinterpret_cast<const u32x4*>(&xt[(wm * 64 + b * 32 + (lane & 31)) * KP + 16 * kk + 8 * half]);
+            }
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    acc[nb][mb] = mfma32x32x16(wf[nb], xf[mb], acc[nb][mb]);
+                }
+            }
+        }
+        if (kt + 1 < k_tiles) {
+            store(buf ^ 1);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue: bias, row mask, one rounding; the tile goes out through LDS
+    // as 16-byte pieces of whole row segments.  Lane (half, m) of block
+    // (nb, mb) holds row m of the 32-row block and features 8 q + 4 half + r.
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int mr = wm * 64 + mb * 32 + (lane & 31);
+            const bool keep = s_keep[mr] != 0;
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const int c = wn * 64 + nb * 32 + 8 * qd + 4 * half;
+                const f32x4 bias = *reinterpret_cast<const f32x4*>(&s_bias[c]);
+                const float v0 = keep ? acc[nb][mb][4 * qd + 0] + bias[0] : 0.0f;
+                const float v1 = keep ? acc[nb][mb][4 * qd + 1] + bias[1] : 0.0f;
+                const float v2 = keep ? acc[nb][mb][4 * qd + 2] + bias[2] : 0.0f;
+                const float v3 = keep ? acc[nb][mb][4 * qd + 3] + bias[3] : 0.0f;
+                u32x2 packed;
+                if constexpr (YT == LSSO_HIP_BF16) {
+                    packed.x = pack_bf16(v0, v1);
+                    packed.y = pack_bf16(v2, v3);
+                } else {
+                    packed.x = pack_f16(v0, v1);
+                    packed.y = pack_f16(v2, v3);
+                }
+                *reinterpret_cast<u32x2*>(&s_y[mr * YP + c]) = packed;
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int kStorePieces = kStreamRows * kStreamCols / 8 / kStreamThreads;
+#pragma unroll
+    for (int i = 0; i < kStorePieces; ++i) {
+        const int piece = tid + i * kStreamThreads;
+        const int mr = piece / (kStreamCols / 8);
+        const int c8 = 8 * (piece - mr * (kStreamCols / 8));
+        const int64_t m = m0 + mr;
+        const int64_t n = n0 + c8;
+        if (m < M && n < N) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(&s_y[mr * YP + c8]);
+            uint16_t* dst = static_cast<uint16_t*>(a.y) + m * N + n;
+            if (a.y_vector) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    if (n + r < N) {
+                        dst[r] = static_cast<uint16_t>(v[r >> 1] >> (16 * (r & 1)));
+                    }
+                }
+            }
+        }
+    }
+}
+
 template <int KSTEPS, bool XVEC>
 static hipError_t launch_linear_kv(const LinearArgs& a, int x_dtype, int y_dtype, dim3 grid,
                                    hipStream_t stream) {
@@ -380,6 +598,27 @@ static hipError_t launch_linear_k(const LinearArgs& a, int x_dtype, int y_dtype,
 
 hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,
                          int grid_groups, hipStream_t stream) {
+    if (k_steps == 0) {
+        // One block per output tile; row tiles rounded up to whole XCD rounds.
+        static_assert(kStreamRows == kStreamRowsHost && kStreamCols == kStreamColsHost, "tile");
+        const int64_t rounds = (a.tiles + kXcds - 1) / kXcds;
+        const dim3 grid(static_cast<unsigned>(rounds * kXcds * a.column_groups));
+        const dim3 block(kStreamThreads);
+        if (x_dtype == LSSO_HIP_F16) {
+            if (y_dtype == LSSO_HIP_F16) {
+                linear_stream_kernel<LSSO_HIP_F16, LSSO_HIP_F16><<<grid, block, 0, stream>>>(a);
+            } else {
+                linear_stream_kernel<LSSO_HIP_F16, LSSO_HIP_BF16><<<grid, block, 0, stream>>>(a);
+            }
+        } else {
+            if (y_dtype == LSSO_HIP_F16) {
+                linear_stream_kernel<LSSO_HIP_BF16, LSSO_HIP_F16><<<grid, block, 0, stream>>>(a);
+            } else {
+                linear_stream_kernel<LSSO_HIP_BF16, LSSO_HIP_BF16><<<grid, block, 0, stream>>>(a);
+            }
+        }
+        return hipGetLastError();
+    }
     const dim3 grid(static_cast<unsigned>(grid_groups * a.column_groups));
     switch (k_steps) {
         case 4: return launch_linear_k<4>(a, x_dtype, y_dtype, grid, stream);

@@ -197,3 +197,36 @@ def test_module_wide_head_gradients_match_oracle_autograd(native, dim, heads, ra
     assert _rel_l2(x.grad, x64.grad) <= GRAD_LIMIT
     for name, parameter in layer.named_parameters():
         assert _rel_l2(parameter.grad, params[name].grad) <= GRAD_LIMIT, (name, _rel_l2(parameter.grad, params[name].grad))
+
+
+def test_module_d768_contract_shape_forward_backward(native, parity_report):
+    """The reference's own exploratory contract-8 measurement shape
+    (docs/CUDA_CONTRACT.md:270-275): B=2, N=4096, D=768, H=12, r=48, FP16.
+    Both projections have in_features 768 and the input projection's value
+    gradient 1,344, past the register-resident tiers: the K-streaming tier."""
+
+    torch.manual_seed(768)
+    config = LSSOConfig(dim=768, num_heads=12, rank=48, bias=True)
+    layer = LSSO(config).cuda()
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.05)
+        layer.core_drive_weight.normal_(std=0.05)
+    x = torch.randn(2, 4096, 768, generator=torch.Generator().manual_seed(769)).half()
+    upstream = torch.randn(2, 4096, 768, generator=torch.Generator().manual_seed(770))
+    xd = x.cuda().requires_grad_()
+    y = layer(xd, implementation="hip")
+    (y.float() * upstream.cuda()).sum().backward()
+    torch.cuda.synchronize()
+    params = {name: p.detach().double().cpu().requires_grad_() for name, p in layer.named_parameters()}
+    x64 = x.double().requires_grad_()
+    cfg = {"dim": 768, "num_heads": 12, "rank": 48, "bias": True}
+    expected = oracle.lsso_forward(params, cfg, x64)
+    (expected * upstream.double()).sum().backward()
+    fp32 = oracle.lsso_forward({n: p.detach().float() for n, p in params.items()}, cfg, x.float())
+    parity_report.record("D768 H12 r48 B2 L4096 fp16 forward", y, fp32, expected.detach())
+    pairs = {"x": (xd.grad, x64.grad)}
+    pairs.update({name: (p.grad, params[name].grad) for name, p in layer.named_parameters()})
+    errors = parity_report.record_grads("D768 H12 r48 B2 L4096 fp16 backward", pairs)
+    assert _rel_l2(y, expected) <= 5e-3
+    for name, error in errors.items():
+        assert error <= GRAD_LIMIT, (name, error)

@@ -269,6 +269,13 @@ def test_linear_strides_and_tails(native, dtype) -> None:
         (4099, 640, 256, torch.bfloat16, torch.float16),
         (70, 600, 72, torch.float16, torch.bfloat16),
         (33, 34, 98, torch.float16, torch.bfloat16),
+        # K-streaming tier (in_features > 640): DeiT-III widths and the
+        # input projection's value gradient at D = 768, H = 12, r = 48.
+        (8192, 768, 1344, torch.float16, torch.bfloat16),
+        (8192, 1344, 768, torch.bfloat16, torch.float16),
+        (4099, 1024, 1024, torch.bfloat16, torch.bfloat16),
+        (129, 641, 200, torch.float16, torch.float16),
+        (300, 2050, 130, torch.bfloat16, torch.float16),
     ],
 )
 def test_linear_matches_fp32_evaluation_of_bf16_operands(

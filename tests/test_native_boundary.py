@@ -146,9 +146,13 @@ def test_linear_validation(library) -> None:
     assert library.lsso_hip_linear_workspace_bytes(10, 256, 512, ctypes.byref(size)) == 0
     assert size.value == 0
     assert library.lsso_hip_linear_workspace_bytes(-1, 256, 512, ctypes.byref(size)) == -1
+    # Any in_features (past 640 the K-streaming tier): only arguments are checked.
     status = library.lsso_hip_linear(None, 1, 4, 700, 700, None, None, None, 8, None, 1, None, 0, None)
-    assert status == -2
-    assert "in_features <= 640" in _message(library)
+    assert status == -1
+    assert "must not be NULL" in _message(library)
+    status = library.lsso_hip_linear(None, 1, 4, 700, 600, None, None, None, 8, None, 1, None, 0, None)
+    assert status == -1
+    assert "x_row_stride" in _message(library)
 
 
 def test_project_mix_forward_validates_before_launch(library) -> None:
