@@ -403,6 +403,29 @@ int lsso_hip_linear_grad_columns(const void* g, int g_dtype, int64_t rows, int64
                                  void* g_bf16, float* column_sums,
                                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Device scratch bytes needed by lsso_hip_linear_weight_grad. */
+int lsso_hip_linear_weight_grad_workspace_bytes(int64_t rows, int64_t in_features,
+                                                int64_t out_features, size_t* bytes);
+
+/* Weight and bias gradients of the biased projection, one pass over g and x:
+ *   grad_weight[n][k] = sum over rows m of bf16(g[m][n]) bf16(x[m][k])  (FP32)
+ *   grad_bias[n]      = sum over rows m of g[m][n]                       (FP32)
+ * g: [rows, out_features] of g_dtype with row stride g_row_stride; x: [rows,
+ * in_features] of x_dtype with row stride x_row_stride (LSSO_HIP_F16 or
+ * LSSO_HIP_BF16, unit column strides).  row_mask: optional device uint8
+ * [rows]; rows whose byte is 0 count as zero whatever g and x hold.
+ * grad_weight: float32 [out_features, in_features] (written, not
+ * accumulated); grad_bias: float32 [out_features] or NULL.  FP32
+ * accumulation over row splits whose partials are added in a fixed order:
+ * deterministic.
+ * Replaces: grad_weight = bf16(grad)^T bf16(x) and grad_bias = grad.sum(rows)
+ * in _TensorCoreLinear.backward (lsso/ball/reference.py:205-247). */
+int lsso_hip_linear_weight_grad(const void* g, int g_dtype, int64_t g_row_stride,
+                                const void* x, int x_dtype, int64_t x_row_stride,
+                                int64_t rows, int64_t in_features, int64_t out_features,
+                                const uint8_t* row_mask, float* grad_weight, float* grad_bias,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,8 @@ _SYMBOLS = (
     "lsso_hip_layer_forward",
     "lsso_hip_layer_forward_timed",
     "lsso_hip_project_mix_forward",
+    "lsso_hip_linear_weight_grad_workspace_bytes",
+    "lsso_hip_linear_weight_grad",
 )
 
 
@@ -130,6 +132,13 @@ def _declare(library: ctypes.CDLL) -> None:
     library.lsso_hip_linear_grad_columns.argtypes = [
         vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp, ctypes.c_size_t, vp,
     ]  # g, g_dtype, rows, cols, stride, row_mask, g_bf16, column_sums, ws, ws_bytes, stream
+    library.lsso_hip_linear_weight_grad_workspace_bytes.restype = ctypes.c_int
+    library.lsso_hip_linear_weight_grad_workspace_bytes.argtypes = [i64, i64, i64, size_p]
+    library.lsso_hip_linear_weight_grad.restype = ctypes.c_int
+    library.lsso_hip_linear_weight_grad.argtypes = [
+        vp, ctypes.c_int, i64, vp, ctypes.c_int, i64, i64, i64, i64, vp, vp, vp, vp, ctypes.c_size_t, vp,
+    ]  # g, g_dtype, g_stride, x, x_dtype, x_stride, rows, in, out, row_mask, grad_weight, grad_bias,
+    #    ws, ws_bytes, stream
     library.lsso_hip_layer_supported.restype = ctypes.c_int
     library.lsso_hip_layer_supported.argtypes = [shape_p]
     library.lsso_hip_layer_workspace_bytes.restype = ctypes.c_int
@@ -1166,36 +1175,49 @@ def _grad_columns(
     return copy, sums
 
 
-def _mm_fp32(left: torch.Tensor, right: torch.Tensor) -> torch.Tensor:
-    """FP32 result of BF16 operands with FP32 accumulation (hipBLASLt)."""
+def _weight_gradient(
+    flat_grad: torch.Tensor,
+    flat_value: torch.Tensor,
+    row_mask: torch.Tensor | None,
+    want_bias: bool,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """FP32 [out, in] = sum over rows of bf16(grad)^T bf16(value), and (when
+    asked) the FP32 column sums of grad, on the native weight-gradient kernel
+    (one pass over both operands, rows excluded by ``row_mask`` count as
+    zero, deterministic)."""
 
-    try:
-        return torch.mm(left, right, out_dtype=torch.float32)
-    except (NotImplementedError, RuntimeError, TypeError):
-        return left.float() @ right.float()
-
-
-def _weight_gradient(gradient: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
-    """FP32 [out, in] = bf16(gradient)^T bf16(value), FP32 accumulation.
-
-    The contraction runs over every row, so it is split over row chunks
-    (batched GEMMs, one output tile set per chunk) and the chunk partials are
-    summed in FP32 in chunk order; a single GEMM would leave most of the
-    device idle on its few output tiles."""
-
-    rows = gradient.shape[0]
-    chunks = 1
-    while chunks < 64 and rows % (2 * chunks) == 0 and rows // (2 * chunks) >= 1024:
-        chunks *= 2
-    if chunks == 1:
-        return _mm_fp32(gradient.mT, value)
-    grad_chunks = gradient.reshape(chunks, rows // chunks, gradient.shape[1])
-    value_chunks = value.reshape(chunks, rows // chunks, value.shape[1])
-    try:
-        partial = torch.bmm(grad_chunks.mT, value_chunks, out_dtype=torch.float32)
-    except (NotImplementedError, RuntimeError, TypeError):
-        partial = torch.bmm(grad_chunks.mT.float(), value_chunks.float())
-    return partial.sum(dim=0)
+    library = _library()
+    rows, out_features = flat_grad.shape
+    in_features = flat_value.shape[1]
+    dtype_codes = {torch.float16: _F16, torch.bfloat16: _BF16}
+    device = flat_grad.device
+    grad_weight = torch.empty((out_features, in_features), dtype=torch.float32, device=device)
+    grad_bias = torch.empty(out_features, dtype=torch.float32, device=device) if want_bias else None
+    size = ctypes.c_size_t(0)
+    _check(library.lsso_hip_linear_weight_grad_workspace_bytes(
+        rows, in_features, out_features, ctypes.byref(size)), library)
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
+    mask = None if row_mask is None else row_mask.reshape(-1).contiguous()
+    with torch.cuda.device(device):
+        status = library.lsso_hip_linear_weight_grad(
+            flat_grad.data_ptr(),
+            dtype_codes[flat_grad.dtype],
+            flat_grad.stride(0) if rows > 1 else out_features,
+            flat_value.data_ptr(),
+            dtype_codes[flat_value.dtype],
+            flat_value.stride(0) if rows > 1 else in_features,
+            rows,
+            in_features,
+            out_features,
+            None if mask is None else mask.data_ptr(),
+            grad_weight.data_ptr(),
+            None if grad_bias is None else grad_bias.data_ptr(),
+            workspace.data_ptr(),
+            size.value,
+            _stream(device),
+        )
+    _check(status, library)
+    return grad_weight, grad_bias
 
 
 class _Linear(torch.autograd.Function):
@@ -1243,44 +1265,32 @@ def _linear_vjp(
     them (over the rows ``row_mask`` keeps), so no pass over dY is made for
     the bias.
 
-    One native pass over dY writes its BF16 copy (excluded rows zero) for
-    the weight gradient and its FP32 column sums for the bias gradient; dX
-    runs on the native projection kernel from dY in its own dtype."""
+    dX runs on the native projection kernel from dY in its own dtype with the
+    transposed weight; dW (and db when it is still needed) on the native
+    weight-gradient kernel, which reads dY and x in their own dtypes; a bias
+    gradient alone takes one native column-sum pass over dY."""
 
     out_features, in_features = weight.shape
     flat_grad = _rows(grad_output, out_features)
     if flat_grad.dtype not in (torch.float16, torch.bfloat16):
         flat_grad = flat_grad.to(dtype=torch.bfloat16).contiguous()
-    native_value = value.dtype in (torch.float16, torch.bfloat16)
-    need_bf16 = need_weight or (need_value and not native_value)
-    copy_grad = need_bf16 and (flat_grad.dtype != torch.bfloat16 or row_mask is not None)
-    grad_bf16 = None
-    sums_needed = need_bias and grad_sums is None
-    if copy_grad or sums_needed:
-        grad_bf16, computed = _grad_columns(flat_grad, row_mask, copy_grad, sums_needed)
-        if sums_needed:
-            grad_sums = computed
-    if need_bf16 and grad_bf16 is None:
-        grad_bf16 = flat_grad
     grad_value = grad_weight = grad_bias = None
     if need_value:
-        if native_value:
-            grad_value = _linear_forward(
-                flat_grad, weight.mT.contiguous(), None, value.dtype,
-                None if row_mask is None else row_mask.reshape(-1),
-            ).reshape(value.shape)
-        else:
-            grad_value = _mm_fp32(grad_bf16, weight.to(dtype=torch.bfloat16))
-            grad_value = grad_value.to(dtype=value.dtype).reshape(value.shape)
+        grad_value = _linear_forward(
+            flat_grad, weight.mT.contiguous(), None, value.dtype,
+            None if row_mask is None else row_mask.reshape(-1),
+        ).reshape(value.shape)
+    sums_needed = need_bias and grad_sums is None
     if need_weight:
         flat_value = _rows(value, in_features)
-        if flat_value.dtype in (torch.float16, torch.bfloat16) and flat_value.stride(-1) == 1 and (
-            flat_value.dtype != torch.bfloat16 or row_mask is not None
-        ):
-            flat_value, _ = _grad_columns(flat_value, row_mask, True, False)
-        else:
-            flat_value = flat_value.to(dtype=torch.bfloat16)
-        grad_weight = _weight_gradient(grad_bf16, flat_value).to(dtype=weight.dtype)
+        if flat_value.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError("the HIP projection supports float16/bfloat16 activations")
+        grad_weight, computed = _weight_gradient(flat_grad, flat_value, row_mask, sums_needed)
+        grad_weight = grad_weight.to(dtype=weight.dtype)
+        if sums_needed:
+            grad_sums = computed
+    elif sums_needed:
+        _, grad_sums = _grad_columns(flat_grad, row_mask, False, True)
     if need_bias:
         grad_bias = grad_sums.to(dtype=bias_dtype)
     return grad_value, grad_weight, grad_bias

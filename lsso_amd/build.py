@@ -30,6 +30,7 @@ SOURCES = (
     "lsso_fused.hip",
     "lsso_backward.hip",
     "lsso_project_reduce.hip",
+    "lsso_weight_grad.hip",
 )
 
 # Packed FP32 VALU forms (v_pk_add/mul/fma_f32) are disabled for all device

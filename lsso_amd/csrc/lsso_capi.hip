@@ -1038,6 +1038,108 @@ int lsso_hip_linear(const void* x, int x_dtype, int64_t rows, int64_t in_feature
 
 namespace {
 
+struct WeightGradPlan {
+    int64_t splits, rows_per_split;
+    size_t off_bias, total;
+};
+
+void make_weight_grad_plan(int64_t rows, int64_t in_features, int64_t out_features,
+                           WeightGradPlan* p) {
+    lsso_hip::plan_weight_grad(rows, in_features, out_features, &p->splits, &p->rows_per_split);
+    p->off_bias = align_up(sizeof(float) * p->splits * out_features * in_features);
+    p->total = align_up(p->off_bias + sizeof(float) * p->splits * out_features);
+}
+
+}  // namespace
+
+extern "C" {
+
+int lsso_hip_linear_weight_grad_workspace_bytes(int64_t rows, int64_t in_features,
+                                                int64_t out_features, size_t* bytes) {
+    if (bytes == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "bytes must not be NULL");
+    }
+    if (rows < 0 || in_features <= 0 || out_features <= 0) {
+        return fail(LSSO_HIP_EINVAL, "rows must be >= 0 and features must be positive");
+    }
+    WeightGradPlan plan;
+    make_weight_grad_plan(rows, in_features, out_features, &plan);
+    *bytes = plan.total;
+    return LSSO_HIP_OK;
+}
+
+int lsso_hip_linear_weight_grad(const void* g, int g_dtype, int64_t g_row_stride, const void* x,
+                                int x_dtype, int64_t x_row_stride, int64_t rows,
+                                int64_t in_features, int64_t out_features,
+                                const uint8_t* row_mask, float* grad_weight, float* grad_bias,
+                                void* workspace, size_t workspace_bytes, void* stream_handle) {
+    if (rows < 0 || in_features <= 0 || out_features <= 0) {
+        return fail(LSSO_HIP_EINVAL, "rows must be >= 0 and features must be positive");
+    }
+    if ((g_dtype != LSSO_HIP_F16 && g_dtype != LSSO_HIP_BF16) ||
+        (x_dtype != LSSO_HIP_F16 && x_dtype != LSSO_HIP_BF16)) {
+        return fail(LSSO_HIP_EUNSUPPORTED, "the gradient and activation dtypes must be float16 or bfloat16");
+    }
+    if (g_row_stride < out_features || x_row_stride < in_features) {
+        return fail(LSSO_HIP_EINVAL, "g_row_stride must be >= out_features and x_row_stride >= in_features");
+    }
+    if (grad_weight == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "grad_weight must not be NULL");
+    }
+    if (rows > 0 && (g == nullptr || x == nullptr)) {
+        return fail(LSSO_HIP_EINVAL, "g and x must not be NULL");
+    }
+    if (!aligned(g, 2) || !aligned(x, 2) || !aligned(grad_weight, 4) || !aligned(grad_bias, 4)) {
+        return fail(LSSO_HIP_EINVAL, "g, x, grad_weight and grad_bias must be aligned to their element size");
+    }
+    WeightGradPlan plan;
+    make_weight_grad_plan(rows, in_features, out_features, &plan);
+    if (workspace == nullptr || workspace_bytes < plan.total || !aligned(workspace, 256)) {
+        return fail(LSSO_HIP_EINVAL, "workspace must be 256-byte aligned and hold " +
+                                         std::to_string(plan.total) + " bytes");
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    float* partials = static_cast<float*>(workspace);
+    float* bias_partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.off_bias);
+    lsso_hip::WeightGradArgs args{};
+    args.g = g;
+    args.g_stride = g_row_stride;
+    args.x = x;
+    args.x_stride = x_row_stride;
+    args.row_mask = row_mask;
+    args.rows = rows;
+    args.out_features = out_features;
+    args.in_features = in_features;
+    args.partials = partials;
+    args.bias_partials = grad_bias != nullptr ? bias_partials : nullptr;
+    args.rows_per_split = plan.rows_per_split;
+    args.splits = plan.splits;
+    args.tiles_n = ceil_div(out_features, lsso_hip::weight_grad_tile());
+    args.tiles_k = ceil_div(in_features, lsso_hip::weight_grad_tile());
+    args.vec = (out_features % 8 == 0 && in_features % 8 == 0 && g_row_stride % 8 == 0 &&
+                x_row_stride % 8 == 0 && aligned(g, 16) && aligned(x, 16)) ? 1 : 0;
+    hipError_t error = lsso_hip::launch_weight_grad(args, g_dtype, x_dtype, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "weight_grad_kernel launch");
+    }
+    error = lsso_hip::launch_column_sum(partials, plan.splits, out_features * in_features,
+                                        grad_weight, stream);
+    if (error != hipSuccess) {
+        return hip_failure(error, "column_sum_kernel launch (weight gradient)");
+    }
+    if (grad_bias != nullptr) {
+        error = lsso_hip::launch_column_sum(bias_partials, plan.splits, out_features, grad_bias, stream);
+        if (error != hipSuccess) {
+            return hip_failure(error, "column_sum_kernel launch (bias gradient)");
+        }
+    }
+    return LSSO_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
 // The whole-layer forward: x -> (projection + reductions) -> solve ->
 // (apply + output projection) -> y.  Returns the heads per projection group,
 // or 0 when the geometry is outside the fused projection + reduce envelope.

@@ -217,6 +217,26 @@ struct ProjectReduceArgs {
     int64_t head_groups;
 };
 
+// Weight and bias gradient of the biased projection: FP32 partials per row
+// split of sum_m bf16(g[m][n]) bf16(x[m][k]) and of sum_m g[m][n].
+struct WeightGradArgs {
+    const void* g;              // FP16/BF16 [rows, out_features], row stride g_stride
+    int64_t g_stride;
+    const void* x;              // FP16/BF16 [rows, in_features], row stride x_stride
+    int64_t x_stride;
+    const uint8_t* row_mask;    // [rows] or nullptr; 0 rows count as zero
+    int64_t rows;
+    int64_t out_features;
+    int64_t in_features;
+    float* partials;            // [splits, out_features, in_features]
+    float* bias_partials;       // [splits, out_features] or nullptr
+    int64_t rows_per_split;     // multiple of 32
+    int64_t splits;
+    int64_t tiles_n;
+    int64_t tiles_k;
+    int vec;                    // 16-byte loads of g and x are legal
+};
+
 hipError_t launch_phase(const PhaseArgs& a, hipStream_t stream);
 hipError_t launch_reduce(int rank, const ReduceArgs& a, int cpw, bool vec, hipStream_t stream);
 hipError_t launch_solve(int rank, const SolveArgs& a, int64_t systems, hipStream_t stream);
@@ -255,6 +275,10 @@ hipError_t launch_project_reduce(int rank, const ProjectReduceArgs& a, int x_dty
                                  hipStream_t stream);
 hipError_t launch_grad_columns(const GradColumnsArgs& a, int g_dtype, bool vec, int64_t splits,
                                int64_t slabs, float* column_sums, hipStream_t stream);
+void plan_weight_grad(int64_t rows, int64_t in_features, int64_t out_features, int64_t* splits,
+                      int64_t* rows_per_split);
+int weight_grad_tile();
+hipError_t launch_weight_grad(const WeightGradArgs& a, int g_dtype, int x_dtype, hipStream_t stream);
 int linear_tile_rows(int k_steps);
 int linear_columns_per_group(int k_steps);
 int linear_k_tier(int64_t in_features);

@@ -168,3 +168,51 @@ def test_module_trains_with_a_summed_loss_and_runs_on_expanded_x(native) -> None
     assert rel(x.grad, x64.grad) <= 3e-2
     for name, parameter in layer.named_parameters():
         assert rel(parameter.grad, params[name].grad) <= 3e-2, name
+
+
+@pytest.mark.parametrize(
+    ("rows", "in_features", "out_features", "g_dtype", "x_dtype", "masked", "pad"),
+    [
+        (131072, 256, 640, torch.bfloat16, torch.float16, False, 0),   # C5 input projection
+        (131072, 256, 256, torch.float16, torch.bfloat16, False, 0),   # C5 output projection
+        (8192, 768, 1344, torch.bfloat16, torch.float16, True, 0),     # D = 768 input projection
+        (4099, 200, 72, torch.float16, torch.float16, True, 8),        # strided rows, partial tiles
+        (777, 41, 13, torch.bfloat16, torch.float16, False, 3),        # scalar loads (odd widths)
+        (31, 64, 48, torch.float16, torch.float16, True, 0),           # fewer rows than one stage
+    ],
+)
+def test_weight_gradient_kernel_matches_fp64_of_bf16_operands(
+    native, rows, in_features, out_features, g_dtype, x_dtype, masked, pad
+) -> None:
+    generator = torch.Generator(device="cuda").manual_seed(rows + in_features + out_features)
+    g = (torch.randn(rows, out_features + pad, device="cuda", generator=generator)).to(g_dtype)[:, :out_features]
+    x = (torch.randn(rows, in_features + pad, device="cuda", generator=generator)).to(x_dtype)[:, :in_features]
+    mask = None
+    if masked:
+        mask = torch.rand(rows, device="cuda", generator=generator) > 0.3
+        g = g.clone()
+        x = x.clone()
+        g[~mask] = float("nan")   # excluded rows count as zero whatever they hold
+        x[~mask] = float("nan")
+    grad_weight, grad_bias = native._weight_gradient(g, x, mask, True)
+    keep = torch.ones(rows, dtype=torch.bool, device="cuda") if mask is None else mask
+    g64 = torch.where(keep[:, None], g.to(torch.bfloat16).double(), 0.0)
+    x64 = torch.where(keep[:, None], x.to(torch.bfloat16).double(), 0.0)
+    expected = g64.T @ x64
+    scale = g64.abs().T @ x64.abs()
+    error = (grad_weight.double() - expected).abs()
+    # FP32 accumulation: chains of at most a few thousand terms per split.
+    assert torch.all(error <= 1e-5 * scale + 1e-6), float((error / (scale + 1e-30)).max())
+    sums64 = torch.where(keep[:, None], g.double(), 0.0).sum(dim=0)
+    sum_scale = torch.where(keep[:, None], g.double().abs(), 0.0).sum(dim=0)
+    assert torch.all((grad_bias.double() - sums64).abs() <= 1e-6 * sum_scale + 1e-6)
+    again, again_bias = native._weight_gradient(g, x, mask, True)
+    assert torch.equal(again, grad_weight) and torch.equal(again_bias, grad_bias)
+
+
+def test_weight_gradient_of_no_rows_is_zero(native) -> None:
+    g = torch.empty(0, 24, device="cuda", dtype=torch.float16)
+    x = torch.empty(0, 40, device="cuda", dtype=torch.bfloat16)
+    grad_weight, grad_bias = native._weight_gradient(g, x, None, True)
+    assert torch.equal(grad_weight, torch.zeros(24, 40, device="cuda"))
+    assert torch.equal(grad_bias, torch.zeros(24, device="cuda"))

@@ -155,6 +155,27 @@ def test_linear_validation(library) -> None:
     assert "x_row_stride" in _message(library)
 
 
+def test_weight_gradient_validation(library) -> None:
+    size = ctypes.c_size_t()
+    assert library.lsso_hip_linear_weight_grad_workspace_bytes(131072, 256, 640, ctypes.byref(size)) == 0
+    assert size.value >= 640 * 256 * 4 and size.value % 256 == 0
+    assert library.lsso_hip_linear_weight_grad_workspace_bytes(0, 256, 640, ctypes.byref(size)) == 0
+    assert library.lsso_hip_linear_weight_grad_workspace_bytes(-1, 256, 640, ctypes.byref(size)) == -1
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    status = library.lsso_hip_linear_weight_grad(fake, 1, 64, fake, 3, 64, 10, 64, 64, None, fake, None,
+                                                 fake, 1 << 20, None)
+    assert status == -2 and "float16 or bfloat16" in _message(library)
+    status = library.lsso_hip_linear_weight_grad(fake, 1, 32, fake, 1, 64, 10, 64, 64, None, fake, None,
+                                                 fake, 1 << 20, None)
+    assert status == -1 and "g_row_stride" in _message(library)
+    status = library.lsso_hip_linear_weight_grad(fake, 1, 64, fake, 1, 64, 10, 64, 64, None, None, None,
+                                                 fake, 1 << 20, None)
+    assert status == -1 and "grad_weight" in _message(library)
+    status = library.lsso_hip_linear_weight_grad(fake, 1, 64, fake, 1, 64, 10, 64, 64, None, fake, None,
+                                                 fake, 16, None)
+    assert status == -1 and "workspace" in _message(library)
+
+
 def test_project_mix_forward_validates_before_launch(library) -> None:
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
     # head_dim 17 is outside the fused envelope (a multiple of 16 is needed).
