@@ -384,6 +384,7 @@ def main() -> int:
             "rank": rank,
             "bias": True,
             "io_dtype": "fp16",
+            "packed_dtype": "bf16",
             "positions": "default",
             "mask": False,
             "accumulate_dtype": "fp32",
