@@ -36,7 +36,13 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=100)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--batch", type=int, default=64)
+    parser.add_argument("--batch", type=int, default=None,
+                        help="batch (default 64; 32 for --config c4)")
+    parser.add_argument("--config", choices=("c3", "c4"), default="c3",
+                        help="forward workload: c3 is the headline shell B64 D256 H8 r32 FP16 "
+                             "(--length 1024 is config C2, 2048 and 4096 config C3); c4 is "
+                             "B32 D384 H6 r64 BF16 with trailing-padding masks and per-sample "
+                             "positions (config C4)")
     parser.add_argument("--length", type=int, default=None,
                         help="sequence length (default 4096; 2048 for --workload train)")
     parser.add_argument("--workload", choices=("forward", "train"), default="forward",
@@ -93,7 +99,8 @@ def error_figures(actual: torch.Tensor, expected: torch.Tensor) -> dict:
     }
 
 
-def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> tuple[dict, torch.Tensor]:
+def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int, mask=None,
+                 position_ids=None) -> tuple[dict, torch.Tensor]:
     """Time the CPU oracle (reference CPU path restated, FP32) on `samples`
     sequences of the workload; tokens/s is scaled by the sample size.
     Returns the record and the oracle's FP32 output for those sequences."""
@@ -106,12 +113,14 @@ def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> tupl
     config = {"dim": layer.config.dim, "num_heads": layer.config.num_heads,
               "rank": layer.config.rank, "bias": layer.config.bias}
     x = x_cpu[:samples].contiguous()
+    sample_mask = None if mask is None else mask[:samples]
+    sample_positions = None if position_ids is None else position_ids[:samples]
     with torch.no_grad():
-        output = oracle.lsso_forward(params, config, x)  # warmup
+        output = oracle.lsso_forward(params, config, x, sample_mask, sample_positions)  # warmup
         times = []
         for _ in range(repeats):
             start = time.perf_counter()
-            oracle.lsso_forward(params, config, x)
+            oracle.lsso_forward(params, config, x, sample_mask, sample_positions)
             times.append(time.perf_counter() - start)
     seconds = statistics.median(times)
     tokens = x.shape[0] * x.shape[1]
@@ -137,7 +146,7 @@ def cpu_baseline(layer, x_cpu: torch.Tensor, samples: int, repeats: int) -> tupl
 
 
 def parity(layer, x_cpu: torch.Tensor, y: torch.Tensor, fp32_output: torch.Tensor | None,
-           fp32_samples: int) -> dict:
+           fp32_samples: int, mask=None, position_ids=None) -> dict:
     """Error figures of the GPU output y against the FP32 CPU oracle (on the
     sequences the CPU baseline ran, or on 3 when it did not run) and its
     rel-L2 error against the FP64 oracle on sequences 0, B/2 and B-1."""
@@ -150,12 +159,17 @@ def parity(layer, x_cpu: torch.Tensor, y: torch.Tensor, fp32_output: torch.Tenso
         fp32_samples = min(3, x_cpu.shape[0])
         params = {name: p.detach().float().cpu() for name, p in layer.named_parameters()}
         with torch.no_grad():
-            fp32_output = oracle.lsso_forward(params, config, x_cpu[:fp32_samples].contiguous())
+            fp32_output = oracle.lsso_forward(
+                params, config, x_cpu[:fp32_samples].contiguous(),
+                None if mask is None else mask[:fp32_samples],
+                None if position_ids is None else position_ids[:fp32_samples])
     figures = error_figures(y[:fp32_samples], fp32_output)
     picks = sorted({0, x_cpu.shape[0] // 2, x_cpu.shape[0] - 1})
     params64 = {name: p.detach().double().cpu() for name, p in layer.named_parameters()}
     with torch.no_grad():
-        fp64_output = oracle.lsso_forward(params64, config, x_cpu[picks].double())
+        fp64_output = oracle.lsso_forward(params64, config, x_cpu[picks].double(),
+                                          None if mask is None else mask[picks],
+                                          None if position_ids is None else position_ids[picks])
     figures["rel_l2_fp64"] = error_figures(y[picks], fp64_output)["rel_l2"]
     figures["reference"] = (f"FP32 CPU oracle on sequences 0..{fp32_samples - 1} (max_rel = max|a-e| / "
                             f"max|e|); FP64 oracle on sequences {picks}")
@@ -250,19 +264,40 @@ def main() -> int:
 
     hip.load()
     if args.workload == "train":
+        if args.batch is None:
+            args.batch = 64
         return train_benchmark(args)
     device = torch.device("cuda", 0)
     if args.length is None:
         args.length = 4096
-    batch, length, dim, heads, rank = args.batch, args.length, 256, 8, 32
+    masked = args.config == "c4"
+    if args.batch is None:
+        args.batch = 32 if masked else 64
+    if masked:
+        batch, length, dim, heads, rank = args.batch, args.length, 384, 6, 64
+    else:
+        batch, length, dim, heads, rank = args.batch, args.length, 256, 8, 32
     torch.manual_seed(0)
     layer = LSSO(LSSOConfig(dim=dim, num_heads=heads, rank=rank, bias=True))
     with torch.no_grad():
         layer.core_base_raw.normal_(std=0.05)
         layer.core_drive_weight.normal_(std=0.05)
     layer = layer.to(device).eval()
-    x_cpu = torch.randn(batch, length, dim, generator=torch.Generator().manual_seed(1)).half()
+    generator = torch.Generator().manual_seed(1)
+    mask_cpu = position_ids_cpu = None
+    if masked:
+        # C4: valid lengths ~ U[L/4, L] with trailing padding, per-sample
+        # positions start_b + arange(L) with start_b ~ U[0, 1024).
+        lengths = torch.randint(length // 4, length + 1, (batch,), generator=generator)
+        mask_cpu = torch.arange(length)[None, :] < lengths[:, None]
+        starts = torch.randint(0, 1024, (batch,), generator=generator)
+        position_ids_cpu = starts[:, None] + torch.arange(length)[None, :]
+        x_cpu = torch.randn(batch, length, dim, generator=generator).bfloat16()
+    else:
+        x_cpu = torch.randn(batch, length, dim, generator=generator).half()
     x = x_cpu.to(device)
+    mask = None if mask_cpu is None else mask_cpu.to(device)
+    position_ids = None if position_ids_cpu is None else position_ids_cpu.to(device)
     tokens = batch * length
 
     w_bc, b_bc = layer.w_bc.weight, layer.w_bc.bias
@@ -277,22 +312,48 @@ def main() -> int:
     # on the launch stream (lsso_hip_layer_forward_timed).
     stage_names = ("phase_table", "project_reduce", "solve", "mix_project")
     width = heads * rank + dim
+    io_bytes = 2  # FP16 or BF16 x and y
+    with torch.inference_mode():
+        centered_positions, valid_counts, row_mask = layer._native_geometry(x, mask, position_ids)
+    # Which kernels the layer call runs: the input projection is fused with
+    # the reductions up to rank 32, and the apply with the output projection
+    # inside the fused readout's envelope (lsso_hip_mixer_projected_supported).
+    fused_in = rank <= 32
+    probe = torch.empty(1, 1, width, dtype=torch.bfloat16, device=device)
+    fused_out = hip.mix_project_supported(probe, layer.core_base_raw, layer.core_drive_weight,
+                                          layer.eta_raw)
+    del probe
     # Algorithmic bytes per launch, counting the ABI tensors once (the FP32
     # partials and apply records in the workspace are left out):
     #   project_reduce: x read (FP16) + packed write (BF16) + W_in, b_in (FP32)
     #   mix_project:    packed read (BF16) + y write (FP16) + W_o, b_o (FP32)
+    # Outside the fused envelopes a stage runs two kernels with a BF16
+    # round trip between them (packed written and read back, or mixed), and
+    # its bytes count both.
     stage_kernels = {
-        "project_reduce": ("lsso_hip::project_reduce_kernel<",
-                           tokens * (dim * 2 + width * 2) + width * dim * 4 + width * 4,
-                           "fused input projection + token reductions (x -> packed, G, S)"),
-        "mix_project": ("lsso_hip::mix_project_kernel<",
-                        tokens * (width * 2 + dim * 2) + dim * dim * 4 + dim * 4,
-                        "fused apply + output projection (packed -> y)"),
+        "project_reduce": (
+            "lsso_hip::project_reduce_kernel<",
+            tokens * (dim * io_bytes + width * 2) + width * dim * 4 + width * 4,
+            "fused input projection + token reductions (x -> packed, G, S)",
+        ) if fused_in else (
+            "lsso_hip::linear_kernel<",
+            tokens * (dim * io_bytes + 2 * width * 2) + width * dim * 4 + width * 4,
+            "input projection then token reductions (x -> packed -> G, S)",
+        ),
+        "mix_project": (
+            "lsso_hip::mix_project_kernel<",
+            tokens * (width * 2 + dim * io_bytes) + dim * dim * 4 + dim * 4,
+            "fused apply + output projection (packed -> y)",
+        ) if fused_out else (
+            "lsso_hip::apply_kernel<",
+            tokens * (width * 2 + 2 * dim * 2 + dim * io_bytes) + dim * dim * 4 + dim * 4,
+            "apply then output projection (packed -> mixed -> y)",
+        ),
     }
 
     def step(events) -> torch.Tensor:
-        return hip.layer_forward(x, w_bc, b_bc, base, drive, eta_raw, None, None, w_o, b_o,
-                                 stage_events=events)
+        return hip.layer_forward(x, w_bc, b_bc, base, drive, eta_raw, centered_positions, valid_counts,
+                                 w_o, b_o, row_mask=row_mask, stage_events=events)
 
     def recorded_events(count):
         # torch creates the HIP event on its first record.
@@ -302,11 +363,11 @@ def main() -> int:
         return events
 
     with torch.inference_mode():
-        reference_out = layer(x, implementation="hip")
+        reference_out = layer(x, valid_mask=mask, position_ids=position_ids, implementation="hip")
         check = step(None)
-        projected = hip.linear(x, w_bc, b_bc, torch.bfloat16)
-        mixed = hip.forward_inference(projected, base, drive, eta_raw)
-        three_calls = hip.linear(mixed, w_o, b_o, x.dtype)
+        projected = hip.linear(x, w_bc, b_bc, torch.bfloat16, row_mask=row_mask)
+        mixed = hip.forward_inference(projected, base, drive, eta_raw, centered_positions, valid_counts)
+        three_calls = hip.linear(mixed, w_o, b_o, x.dtype, row_mask=row_mask)
         del projected, mixed
         if not (torch.equal(check, reference_out) and torch.equal(check, three_calls)):
             print("the layer step differs from LSSO.forward(implementation='hip') or from "
@@ -354,16 +415,22 @@ def main() -> int:
     kernel_ms = statistics.mean(start_event.elapsed_time(end_event) for start_event, end_event in timed_pairs)
     kernel_prefix, kernel_bytes, kernel_role = stage_kernels[dominant]
     achieved = kernel_bytes / (kernel_ms * 1e-3) / 1e9
-    # HBM bytes per token the chain moves by design: x read (FP16), packed
-    # written and read back (BF16), y written (FP16).
-    chain_bytes_per_token = dim * 2 + 2 * width * 2 + dim * 2
+    # HBM bytes per token the chain moves by design: x read, packed written
+    # and read back (BF16), y written; plus a second packed read when the
+    # input projection is not fused with the reductions and a mixed round
+    # trip (BF16) when the apply is not fused with the output projection.
+    chain_bytes_per_token = (dim * io_bytes + 2 * width * 2 + dim * io_bytes
+                             + (0 if fused_in else width * 2) + (0 if fused_out else 2 * dim * 2))
     chain_bytes = tokens * chain_bytes_per_token
-    headline = (batch, length) == (64, 4096)
+    headline = (batch, length) == (64, 4096) and not masked
     kernel_name, traffic = measured_traffic(kernel_prefix) if headline else (None, None)
     if kernel_name is None:
         kernel_name = kernel_prefix.rstrip("<")
+    io_name = "bf16" if masked else "fp16"
     result = {
-        "metric": "mixer fwd tokens/s @B64 D256 H8 r32 L4096 fp16; % HBM roofline",
+        "metric": ("mixer fwd tokens/s @B64 D256 H8 r32 L4096 fp16; % HBM roofline" if headline else
+                   f"mixer fwd tokens/s @B{batch} D{dim} H{heads} r{rank} L{length} {io_name}"
+                   + (" masked" if masked else "")),
         "value": value,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -374,7 +441,9 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": value / REFERENCE_TOKENS_PER_S if headline else None,
         "dtype": "bf16",
-        "data": "synthetic: x ~ N(0,1) fp16, seeded random-init weights",
+        "data": (f"synthetic: x ~ N(0,1) {io_name}, seeded random-init weights"
+                 + ("; valid lengths ~ U[L/4, L] with trailing padding, per-sample positions "
+                    "start ~ U[0, 1024); tokens/s counts all B*L rows" if masked else "")),
         "config": {
             "workload": "lsso_mixer_forward",
             "batch": batch,
@@ -383,10 +452,12 @@ def main() -> int:
             "heads": heads,
             "rank": rank,
             "bias": True,
-            "io_dtype": "fp16",
+            "io_dtype": io_name,
             "packed_dtype": "bf16",
-            "positions": "default",
-            "mask": False,
+            "positions": "per-sample" if masked else "default",
+            "mask": masked,
+            "fused_input_projection": fused_in,
+            "fused_output_projection": fused_out,
             "accumulate_dtype": "fp32",
             "chain_bytes_per_token": chain_bytes_per_token,
             "chain_hbm_fraction": chain_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS,
@@ -409,9 +480,10 @@ def main() -> int:
     fp32_output = None
     samples = min(args.cpu_samples, batch)
     if args.cpu_samples > 0:
-        result["cpu_baseline"], fp32_output = cpu_baseline(layer, x_cpu, samples, args.cpu_repeats)
+        result["cpu_baseline"], fp32_output = cpu_baseline(layer, x_cpu, samples, args.cpu_repeats,
+                                                           mask_cpu, position_ids_cpu)
     if not args.no_parity:
-        result["parity"] = parity(layer, x_cpu, check, fp32_output, samples)
+        result["parity"] = parity(layer, x_cpu, check, fp32_output, samples, mask_cpu, position_ids_cpu)
     print(json.dumps(result), flush=True)
     return 0
 
