@@ -56,6 +56,11 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--cpu-repeats", type=int, default=7)
     parser.add_argument("--no-parity", action="store_true",
                         help="skip the error figures against the CPU oracle")
+    parser.add_argument("--slices", type=int, default=1,
+                        help="forward only: split the batch into this many equal slices, one "
+                             "layer call each, issued alternately on two streams of default "
+                             "priority, so that one slice's compact solve can overlap another "
+                             "slice's streaming kernels (A/B of that overlap; default 1 = one call)")
     parser.add_argument("--copy-mib", type=int, default=0,
                         help="after the timed region, run one device copy of this many MiB "
                              "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -355,6 +360,38 @@ def main() -> int:
         return hip.layer_forward(x, w_bc, b_bc, base, drive, eta_raw, centered_positions, valid_counts,
                                  w_o, b_o, row_mask=row_mask, stage_events=events)
 
+    slices = args.slices
+    if slices < 1 or batch % slices:
+        print(f"--slices {slices} must divide the batch {batch}", file=sys.stderr)
+        return 2
+    if slices > 1 and masked:
+        print("--slices is only wired for the unmasked workload", file=sys.stderr)
+        return 2
+    launch_stream = torch.cuda.current_stream(device)
+    slice_streams = [torch.cuda.Stream(device) for _ in range(2)] if slices > 1 else []
+    per_slice = batch // slices
+
+    def sliced_step(events) -> list:
+        # Slice k runs on stream k % 2; the events (if any) go with slice 0.
+        outputs = []
+        for stream in slice_streams:
+            stream.wait_stream(launch_stream)
+        for k in range(slices):
+            with torch.cuda.stream(slice_streams[k % 2]):
+                rows = slice(k * per_slice, (k + 1) * per_slice)
+                outputs.append(hip.layer_forward(x[rows], w_bc, b_bc, base, drive, eta_raw, centered_positions,
+                                                 valid_counts, w_o, b_o, row_mask=None,
+                                                 stage_events=events if k == 0 else None))
+        for stream in slice_streams:
+            launch_stream.wait_stream(stream)
+        return outputs
+
+    def timed_step(events) -> None:
+        if slices == 1:
+            step(events)
+        else:
+            sliced_step(events)
+
     def recorded_events(count):
         # torch creates the HIP event on its first record.
         events = [torch.cuda.Event(enable_timing=True) for _ in range(count)]
@@ -374,8 +411,14 @@ def main() -> int:
                   "linear -> forward_inference -> linear", file=sys.stderr)
             return 1
         del three_calls
+        if slices > 1:
+            # Results do not depend on the batch composition, so the slices
+            # reproduce the one-call output bit for bit.
+            if not torch.equal(torch.cat(sliced_step(None), 0), check):
+                print(f"the {slices}-slice step differs from the one-call step", file=sys.stderr)
+                return 1
         for _ in range(args.warmup):
-            step(None)
+            timed_step(None)
         # Per-stage times from untimed steps with events around all four
         # stages.  Each event record is a queue packet with a release; eight
         # of them add tens of microseconds to a step, so the timed steps record
@@ -398,7 +441,7 @@ def main() -> int:
         torch.cuda.synchronize()
         start = time.perf_counter()
         for index in range(args.steps):
-            step(timed_events[index])
+            timed_step(timed_events[index])
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
 
@@ -414,6 +457,11 @@ def main() -> int:
     value = tokens * args.steps / elapsed
     kernel_ms = statistics.mean(start_event.elapsed_time(end_event) for start_event, end_event in timed_pairs)
     kernel_prefix, kernel_bytes, kernel_role = stage_kernels[dominant]
+    if slices > 1:
+        # The timed events bracket slice 0's launch of the dominant kernel,
+        # which streams 1 / slices of the tokens and reads the weights once.
+        weight_bytes = dim * dim * 4 + dim * 4 if dominant == "mix_project" else width * dim * 4 + width * 4
+        kernel_bytes = (kernel_bytes - weight_bytes) // slices + weight_bytes
     achieved = kernel_bytes / (kernel_ms * 1e-3) / 1e9
     # HBM bytes per token the chain moves by design: x read, packed written
     # and read back (BF16), y written; plus a second packed read when the
@@ -422,7 +470,7 @@ def main() -> int:
     chain_bytes_per_token = (dim * io_bytes + 2 * width * 2 + dim * io_bytes
                              + (0 if fused_in else width * 2) + (0 if fused_out else 2 * dim * 2))
     chain_bytes = tokens * chain_bytes_per_token
-    headline = (batch, length) == (64, 4096) and not masked
+    headline = (batch, length) == (64, 4096) and not masked and slices == 1
     kernel_name, traffic = measured_traffic(kernel_prefix) if headline else (None, None)
     if kernel_name is None:
         kernel_name = kernel_prefix.rstrip("<")
@@ -430,7 +478,7 @@ def main() -> int:
     result = {
         "metric": ("mixer fwd tokens/s @B64 D256 H8 r32 L4096 fp16; % HBM roofline" if headline else
                    f"mixer fwd tokens/s @B{batch} D{dim} H{heads} r{rank} L{length} {io_name}"
-                   + (" masked" if masked else "")),
+                   + (" masked" if masked else "") + (f" in {slices} slices on 2 streams" if slices > 1 else "")),
         "value": value,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -456,6 +504,7 @@ def main() -> int:
             "packed_dtype": "bf16",
             "positions": "per-sample" if masked else "default",
             "mask": masked,
+            "slices": slices,
             "fused_input_projection": fused_in,
             "fused_output_projection": fused_out,
             "accumulate_dtype": "fp32",

@@ -42,7 +42,9 @@ __device__ __forceinline__ int stage_offset(int column, int group) {
     return column * kWgPitch + 8 * (group ^ ((column >> 4) & 7));
 }
 constexpr int kWgXcds = 8;
-constexpr int kWgTargetBlocks = 512;
+// Resident workgroups per XCD on MI355X: 32 CUs x 2 (the two stage buffers
+// take 76 KB of a CU's 160 KB of LDS).
+constexpr int kWgSlotsPerXcd = 64;
 
 template <int T>
 __device__ __forceinline__ float bits_to_float(uint32_t bits) {
@@ -287,7 +289,12 @@ void plan_weight_grad(int64_t rows, int64_t in_features, int64_t out_features, i
                       int64_t* rows_per_split) {
     const int64_t tiles = ((out_features + kWgTile - 1) / kWgTile) * ((in_features + kWgTile - 1) / kWgTile);
     const int64_t stages = (rows + kWgRows - 1) / kWgRows;
-    int64_t want = (kWgTargetBlocks + tiles - 1) / tiles;
+    // As many row splits per XCD as let all of that XCD's workgroups (its
+    // splits x the output tiles) be resident at once: one more, nearly empty
+    // round of workgroups would take as long as the first.
+    int64_t per_xcd = kWgSlotsPerXcd / tiles;
+    if (per_xcd < 1) per_xcd = 1;
+    int64_t want = kWgXcds * per_xcd;
     if (want > stages) want = stages;
     if (want < 1) want = 1;
     const int64_t per = (rows + want - 1) / want;
