@@ -93,7 +93,10 @@ int make_plan(const lsso_hip_mixer_shape* shape, int positions_mode, MixerPlan* 
     p->pairs = p->rank / 2;
     p->phase_batches = positions_mode == LSSO_HIP_POSITIONS_BATCHED ? p->batch : 1;
 
-    p->cpw = p->head_dim > 32 ? 2 : 1;
+    // Two 32-feature column groups per reduction wave where the registers
+    // allow two waves per SIMD (rank <= 32); from rank 48 on the two-group
+    // form runs one wave per SIMD, and one group per wave is faster.
+    p->cpw = p->head_dim > 32 && p->rank <= 32 ? 2 : 1;
     p->column_groups = ceil_div(p->head_dim, 32 * p->cpw);
     // Chunks are whole 64-token tiles, so the fused projection + reduce and
     // the standalone reduce share one chunking (and their partials agree).

@@ -5,10 +5,10 @@
 // FP32 accumulation, FP32 bias added to the accumulator, one final FP16 or
 // BF16 store; FP16 output never rounds through BF16.
 //
-// Schedule: persistent workgroups of 8 waves (4 when 256 < K <= 384).  Each
-// wave keeps a 32-column slice of W (BF16, K padded to 16) in registers for
-// the whole launch, so the weights are read once per workgroup; past K = 384
-// two waves share a slice, one per half of K.  64-row x tiles (32-row once
+// Schedule: persistent workgroups of 8 waves.  Each wave keeps a 32-column
+// slice of W (BF16, K padded to 16) in registers for the whole launch, so the
+// weights are read once per workgroup; past K = 384 two waves share a slice,
+// one per half of K.  64-row x tiles (32-row once
 // K > 384, so that two of them and the split's partials fit LDS) are staged
 // through a double-buffered LDS tile (converted to BF16 once) and shared by
 // the workgroup's waves.
@@ -31,20 +31,22 @@ constexpr int kStreamColsHost = 128;
 template <int KSTEPS>
 constexpr int linear_tile_rows_k() { return KSTEPS <= 24 ? 64 : 32; }
 
-// Waves per workgroup: eight (two per SIMD, 256 registers each) while the
-// resident W slice fits; four for K in (256, 384]; eight again past 384,
-// where two waves share each 32-column slice, one per half of K, and add
-// their accumulators through LDS.  Up to K = 384 the K order is a single
-// chain, the one the fused projection kernels reproduce bit for bit.
+// Waves per workgroup: eight, two per SIMD at up to 256 registers each.  Up
+// to K = 384 each wave holds its whole 32-column slice (96 VGPRs at K = 384;
+// with four waves, one per SIMD, the K = 384 tier took 175 us instead of
+// 131 us for 32 x 4096 rows of 384 -> 768) and the K order is a single
+// chain, the one the fused projection kernels reproduce bit for bit.  Past
+// K = 384 two waves share each 32-column slice, one per half of K, and add
+// their accumulators through LDS.
 template <int KSTEPS>
-constexpr int linear_waves() { return (KSTEPS <= 16 || KSTEPS >= 32) ? 8 : 4; }
+constexpr int linear_waves() { return 8; }
 template <int KSTEPS>
 constexpr int linear_ksplit() { return KSTEPS >= 32 ? 2 : 1; }
 
 // Tier 0 is the K-streaming kernel (any in_features above 640).
 int linear_tile_rows(int k_steps) { return k_steps == 0 ? kStreamRowsHost : (k_steps <= 24 ? 64 : 32); }
 int linear_columns_per_group(int k_steps) {
-    return k_steps == 0 ? kStreamColsHost : (k_steps <= 16 ? 8 : 4) * 32;
+    return k_steps == 0 ? kStreamColsHost : (k_steps <= 24 ? 8 : 4) * 32;
 }
 
 int linear_k_tier(int64_t in_features) {

@@ -1062,34 +1062,96 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
     const int64_t begin = chunk * a.chunk_tokens;
     const int64_t end = begin + a.chunk_tokens < a.length ? begin + a.chunk_tokens : a.length;
     const int64_t content_offset = a.heads * R + h * d;
-    for (int64_t t0 = begin; t0 < end; t0 += 16) {
+
+    // The raw operands of one 16-token step (relation pairs, phases and, at
+    // rank 64, the content of this wave's feature blocks).  At rank 64 the
+    // loop issues the next step's loads before it rotates and multiplies the
+    // current step, so their latency runs under this step's MFMAs (125.7 ->
+    // 100.6 us at B32 N4096 H6 d64).  At lower ranks the registers this takes
+    // would cost waves per SIMD (7 -> 5 at rank 32, 109 -> 118 us), so each
+    // step loads its own operands and reads the content just before its store.
+    constexpr bool kPipelined = R == 64;
+    struct StepLoads {
+        u32x4 rel32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
+        u32x4 ph32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
+        u32x2 rel16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
+        u32x2 ph16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
+        u32x2 con[NFBW];
+    };
+    auto load_step = [&](int64_t t0, StepLoads& l) {
         const int64_t token = t0 + q;
         const bool live = token < end;
         const int64_t safe_token = live ? token : begin;
         const uint16_t* row = a.projected + (b * a.length + safe_token) * a.width;
         const uint32_t* phase_row = a.phases + b * a.phase_batch_stride + safe_token * PAIRS;
+#pragma unroll
+        for (int s = 0; s < AL::kSteps32; ++s) {
+            const int first_rank = 32 * s + 8 * g;
+            if constexpr (VEC) {
+                l.rel32[s] = *reinterpret_cast<const u32x4*>(row + h * R + first_rank);
+                l.ph32[s] = *reinterpret_cast<const u32x4*>(phase_row + first_rank / 2);
+            } else {
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    l.rel32[s][p] = load_pair<false>(row + h * R + first_rank + 2 * p, true);
+                    l.ph32[s][p] = phase_row[first_rank / 2 + p];
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < AL::kSteps16; ++s) {
+            const int first_rank = 16 * s + 4 * g;
+            if constexpr (VEC) {
+                l.rel16[s] = *reinterpret_cast<const u32x2*>(row + h * R + first_rank);
+                l.ph16[s] = *reinterpret_cast<const u32x2*>(phase_row + first_rank / 2);
+            } else {
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    l.rel16[s][p] = load_pair<false>(row + h * R + first_rank + 2 * p, true);
+                    l.ph16[s][p] = phase_row[first_rank / 2 + p];
+                }
+            }
+        }
+        if constexpr (VEC && kPipelined) {
+#pragma unroll
+            for (int f = 0; f < NFBW; ++f) {
+                const int64_t feature = (fbg * NFBW + f) * 16 + 4 * g;
+                l.con[f] = feature + 3 < d
+                               ? *reinterpret_cast<const u32x2*>(row + content_offset + feature)
+                               : (u32x2){0u, 0u};
+            }
+        }
+    };
+
+    StepLoads next;
+    if constexpr (kPipelined) {
+        if (begin < end) {
+            load_step(begin, next);
+        }
+    }
+    for (int64_t t0 = begin; t0 < end; t0 += 16) {
+        StepLoads cur;
+        if constexpr (kPipelined) {
+            cur = next;
+            if (t0 + 16 < end) {
+                load_step(t0 + 16, next);
+            }
+        } else {
+            load_step(t0, cur);
+        }
+        const int64_t token = t0 + q;
+        const bool live = token < end;
+        const int64_t safe_token = live ? token : begin;
+        const uint16_t* row = a.projected + (b * a.length + safe_token) * a.width;
 
         u32x4 b_hi32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
         u32x4 b_lo32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
 #pragma unroll
         for (int s = 0; s < AL::kSteps32; ++s) {
-            const int first_rank = 32 * s + 8 * g;
-            u32x4 rel;
-            u32x4 ph;
-            if constexpr (VEC) {
-                rel = *reinterpret_cast<const u32x4*>(row + h * R + first_rank);
-                ph = *reinterpret_cast<const u32x4*>(phase_row + first_rank / 2);
-            } else {
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    rel[p] = load_pair<false>(row + h * R + first_rank + 2 * p, true);
-                    ph[p] = phase_row[first_rank / 2 + p];
-                }
-            }
             float v[8];
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                rotate_pair(rel[p], ph[p], v[2 * p], v[2 * p + 1]);
+                rotate_pair(cur.rel32[s][p], cur.ph32[s][p], v[2 * p], v[2 * p + 1]);
             }
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
@@ -1103,23 +1165,10 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
         u32x2 b_lo16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
 #pragma unroll
         for (int s = 0; s < AL::kSteps16; ++s) {
-            const int first_rank = 16 * s + 4 * g;
-            u32x2 rel;
-            u32x2 ph;
-            if constexpr (VEC) {
-                rel = *reinterpret_cast<const u32x2*>(row + h * R + first_rank);
-                ph = *reinterpret_cast<const u32x2*>(phase_row + first_rank / 2);
-            } else {
-#pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    rel[p] = load_pair<false>(row + h * R + first_rank + 2 * p, true);
-                    ph[p] = phase_row[first_rank / 2 + p];
-                }
-            }
             float v[4];
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
-                rotate_pair(rel[p], ph[p], v[2 * p], v[2 * p + 1]);
+                rotate_pair(cur.rel16[s][p], cur.ph16[s][p], v[2 * p], v[2 * p + 1]);
             }
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
@@ -1154,14 +1203,15 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
             }
             const int64_t feature = fb * 16 + 4 * g;
             uint16_t* out = a.output + (b * a.length + token) * a.out_width + h * d + feature;
-            const uint16_t* content = row + content_offset + feature;
             if (VEC && feature + 3 < d) {
-                const u32x2 c = *reinterpret_cast<const u32x2*>(content);
+                const u32x2 c = kPipelined ? cur.con[f]
+                                           : *reinterpret_cast<const u32x2*>(row + content_offset + feature);
                 u32x2 y;
                 y.x = pack_bf16(fmaf(eta, bf16_lo(c.x), acc[0]), fmaf(eta, bf16_hi(c.x), acc[1]));
                 y.y = pack_bf16(fmaf(eta, bf16_lo(c.y), acc[2]), fmaf(eta, bf16_hi(c.y), acc[3]));
                 *reinterpret_cast<u32x2*>(out) = y;
             } else {
+                const uint16_t* content = row + content_offset + feature;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     if (feature + i < d) {
