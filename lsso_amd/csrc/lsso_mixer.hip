@@ -898,9 +898,17 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
                 gj_step(k);
             }
         } else {
+            // Rolled over 16-column blocks, unrolled within one: the column
+            // index within a 16-float register chunk is then a constant, and
+            // only the choice of chunk is a run-time select (a run-time
+            // element index costs a select over all 16 elements of every
+            // chunk, for the read and again for the write of column k).
 #pragma unroll 1
-            for (int k = 0; k < R; ++k) {
-                gj_step(k);
+            for (int kb = 0; kb < R / 16; ++kb) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    gj_step(16 * kb + j);
+                }
             }
         }
         if (live) {
@@ -1071,6 +1079,34 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
     // would cost waves per SIMD (7 -> 5 at rank 32, 109 -> 118 us), so each
     // step loads its own operands and reads the content just before its store.
     constexpr bool kPipelined = R == 64;
+    // Relation pairs and phases of ranks 32 s + 8 g .. + 7 (the 32-rank
+    // steps) or 16 s + 4 g .. + 3 (the 16-rank step) of one token.
+    auto load32 = [&](const uint16_t* row, const uint32_t* phase_row, int s, u32x4& rel, u32x4& ph) {
+        const int first_rank = 32 * s + 8 * g;
+        if constexpr (VEC) {
+            rel = *reinterpret_cast<const u32x4*>(row + h * R + first_rank);
+            ph = *reinterpret_cast<const u32x4*>(phase_row + first_rank / 2);
+        } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                rel[p] = load_pair<false>(row + h * R + first_rank + 2 * p, true);
+                ph[p] = phase_row[first_rank / 2 + p];
+            }
+        }
+    };
+    auto load16 = [&](const uint16_t* row, const uint32_t* phase_row, int s, u32x2& rel, u32x2& ph) {
+        const int first_rank = 16 * s + 4 * g;
+        if constexpr (VEC) {
+            rel = *reinterpret_cast<const u32x2*>(row + h * R + first_rank);
+            ph = *reinterpret_cast<const u32x2*>(phase_row + first_rank / 2);
+        } else {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                rel[p] = load_pair<false>(row + h * R + first_rank + 2 * p, true);
+                ph[p] = phase_row[first_rank / 2 + p];
+            }
+        }
+    };
     struct StepLoads {
         u32x4 rel32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
         u32x4 ph32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
@@ -1078,41 +1114,21 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
         u32x2 ph16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
         u32x2 con[NFBW];
     };
+    // All operands of the 16-token step at t0 (the pipelined form).
     auto load_step = [&](int64_t t0, StepLoads& l) {
         const int64_t token = t0 + q;
-        const bool live = token < end;
-        const int64_t safe_token = live ? token : begin;
+        const int64_t safe_token = token < end ? token : begin;
         const uint16_t* row = a.projected + (b * a.length + safe_token) * a.width;
         const uint32_t* phase_row = a.phases + b * a.phase_batch_stride + safe_token * PAIRS;
 #pragma unroll
         for (int s = 0; s < AL::kSteps32; ++s) {
-            const int first_rank = 32 * s + 8 * g;
-            if constexpr (VEC) {
-                l.rel32[s] = *reinterpret_cast<const u32x4*>(row + h * R + first_rank);
-                l.ph32[s] = *reinterpret_cast<const u32x4*>(phase_row + first_rank / 2);
-            } else {
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    l.rel32[s][p] = load_pair<false>(row + h * R + first_rank + 2 * p, true);
-                    l.ph32[s][p] = phase_row[first_rank / 2 + p];
-                }
-            }
+            load32(row, phase_row, s, l.rel32[s], l.ph32[s]);
         }
 #pragma unroll
         for (int s = 0; s < AL::kSteps16; ++s) {
-            const int first_rank = 16 * s + 4 * g;
-            if constexpr (VEC) {
-                l.rel16[s] = *reinterpret_cast<const u32x2*>(row + h * R + first_rank);
-                l.ph16[s] = *reinterpret_cast<const u32x2*>(phase_row + first_rank / 2);
-            } else {
-#pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    l.rel16[s][p] = load_pair<false>(row + h * R + first_rank + 2 * p, true);
-                    l.ph16[s][p] = phase_row[first_rank / 2 + p];
-                }
-            }
+            load16(row, phase_row, s, l.rel16[s], l.ph16[s]);
         }
-        if constexpr (VEC && kPipelined) {
+        if constexpr (VEC) {
 #pragma unroll
             for (int f = 0; f < NFBW; ++f) {
                 const int64_t feature = (fbg * NFBW + f) * 16 + 4 * g;
@@ -1136,22 +1152,29 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
             if (t0 + 16 < end) {
                 load_step(t0 + 16, next);
             }
-        } else {
-            load_step(t0, cur);
         }
         const int64_t token = t0 + q;
         const bool live = token < end;
         const int64_t safe_token = live ? token : begin;
         const uint16_t* row = a.projected + (b * a.length + safe_token) * a.width;
+        const uint32_t* phase_row = a.phases + b * a.phase_batch_stride + safe_token * PAIRS;
 
         u32x4 b_hi32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
         u32x4 b_lo32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
 #pragma unroll
         for (int s = 0; s < AL::kSteps32; ++s) {
+            u32x4 rel;
+            u32x4 ph;
+            if constexpr (kPipelined) {
+                rel = cur.rel32[s];
+                ph = cur.ph32[s];
+            } else {
+                load32(row, phase_row, s, rel, ph);
+            }
             float v[8];
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                rotate_pair(cur.rel32[s][p], cur.ph32[s][p], v[2 * p], v[2 * p + 1]);
+                rotate_pair(rel[p], ph[p], v[2 * p], v[2 * p + 1]);
             }
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
@@ -1165,10 +1188,18 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
         u32x2 b_lo16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
 #pragma unroll
         for (int s = 0; s < AL::kSteps16; ++s) {
+            u32x2 rel;
+            u32x2 ph;
+            if constexpr (kPipelined) {
+                rel = cur.rel16[s];
+                ph = cur.ph16[s];
+            } else {
+                load16(row, phase_row, s, rel, ph);
+            }
             float v[4];
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
-                rotate_pair(cur.rel16[s][p], cur.ph16[s][p], v[2 * p], v[2 * p + 1]);
+                rotate_pair(rel[p], ph[p], v[2 * p], v[2 * p + 1]);
             }
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
