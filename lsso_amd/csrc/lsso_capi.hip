@@ -92,6 +92,11 @@ int make_plan(const lsso_hip_mixer_shape* shape, int positions_mode, MixerPlan* 
     p->out_width = p->heads * p->head_dim;
     p->pairs = p->rank / 2;
     p->phase_batches = positions_mode == LSSO_HIP_POSITIONS_BATCHED ? p->batch : 1;
+    // The phase kernel indexes (position, 4 pairs) pieces with 32-bit integers.
+    if (p->phase_batches * p->length > (int64_t{1} << 31) / p->pairs * 4) {
+        return fail(LSSO_HIP_EUNSUPPORTED, "the phase table (B*N*rank/2 entries with per-sample "
+                                           "positions, else N*rank/2) must stay below 2^33 entries");
+    }
 
     // Two 32-feature column groups per reduction wave where the registers
     // allow two waves per SIMD (rank <= 32); from rank 48 on the two-group

@@ -28,22 +28,32 @@
 namespace lsso_hip {
 
 // ---------------------------------------------------------------------------
-// Phase table.
+// Phase table: one thread per (position, 4 consecutive pairs), 32-bit
+// indices and a compile-time pair count, so the index split is a multiply
+// (a 64-bit division per entry cost more than the sines) and each thread
+// writes one 16-byte piece.
+template <int PAIRS>
 __global__ __launch_bounds__(256) void phase_kernel(PhaseArgs a) {
-    const int64_t index = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (index >= a.count) {
+    constexpr uint32_t kQuads = PAIRS / 4;
+    const uint32_t index = blockIdx.x * 256u + threadIdx.x;
+    if (index >= static_cast<uint32_t>(a.count / 4)) {
         return;
     }
-    const int pair = static_cast<int>(index % a.pairs);
-    const int64_t position_index = index / a.pairs;
+    const uint32_t position_index = index / kQuads;
+    const int quad = static_cast<int>(index - position_index * kQuads);
     const float position = a.positions != nullptr
         ? a.positions[position_index]
         : static_cast<float>(position_index) - 0.5f * static_cast<float>(a.length - 1);
-    const float angle = position * a.inverse_frequency[pair];
-    float sine;
-    float cosine;
-    sincosf(angle, &sine, &cosine);
-    a.phases[index] = pack_f16(cosine, sine);
+    u32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float angle = position * a.inverse_frequency[4 * quad + e];
+        float sine;
+        float cosine;
+        sincosf(angle, &sine, &cosine);
+        out[e] = pack_f16(cosine, sine);
+    }
+    *reinterpret_cast<u32x4*>(a.phases + 4 * static_cast<uint64_t>(index)) = out;
 }
 
 // ---------------------------------------------------------------------------
@@ -1296,8 +1306,15 @@ static hipError_t launch_apply(const ApplyArgs& a, int nfbw, bool vec, hipStream
 }
 
 hipError_t launch_phase(const PhaseArgs& a, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>((a.count + 255) / 256));
-    phase_kernel<<<grid, 256, 0, stream>>>(a);
+    // The table has pairs = rank / 2 in {8, 16, 24, 32} entries per position
+    // and fewer than 2^32 entries (the plan bounds B * N * pairs).
+    const dim3 grid(static_cast<unsigned>((a.count / 4 + 255) / 256));
+    switch (a.pairs) {
+        case 8: phase_kernel<8><<<grid, 256, 0, stream>>>(a); break;
+        case 16: phase_kernel<16><<<grid, 256, 0, stream>>>(a); break;
+        case 24: phase_kernel<24><<<grid, 256, 0, stream>>>(a); break;
+        default: phase_kernel<32><<<grid, 256, 0, stream>>>(a); break;
+    }
     return hipGetLastError();
 }
 
