@@ -263,6 +263,10 @@ def test_linear_strides_and_tails(native, dtype) -> None:
         (65536, 256, 512, torch.float16, torch.bfloat16),
         (65536, 256, 256, torch.bfloat16, torch.float16),
         (4099, 384, 768, torch.bfloat16, torch.bfloat16),
+        # K in (256, 384] with in_features not a multiple of 8 (the
+        # element-wise x loads of that tier).
+        (515, 300, 200, torch.float16, torch.bfloat16),
+        (67, 383, 130, torch.bfloat16, torch.float16),
         (520, 192, 240, torch.float16, torch.bfloat16),
         (77, 96, 144, torch.float16, torch.float16),
         (130, 512, 64, torch.bfloat16, torch.bfloat16),
