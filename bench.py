@@ -419,10 +419,10 @@ def main() -> int:
                 return 1
         for _ in range(args.warmup):
             timed_step(None)
-        # Per-stage times from untimed steps with events around all four
-        # stages.  Each event record is a queue packet with a release; eight
-        # of them add tens of microseconds to a step, so the timed steps record
-        # only the two around the dominant kernel.
+        # Per-stage times from untimed steps with events on all four stages
+        # (the library's kernel dispatches record them).  Events on every
+        # stage still add about ten microseconds to a step, so the timed
+        # steps carry only the two of the dominant kernel.
         stage_events = [recorded_events(8) for _ in range(STAGE_PROBE_STEPS)]
         torch.cuda.synchronize()
         for events in stage_events:

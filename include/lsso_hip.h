@@ -297,10 +297,13 @@ int lsso_hip_layer_forward(const lsso_hip_mixer_shape* shape,
                            void* stream);
 
 /* lsso_hip_layer_forward with timing marks for profiling callers: events
- * points to 8 hipEvent_t handles (entries may be NULL); events[2k] and
- * events[2k+1] are recorded on the stream around stage k: 0 the phase table,
- * 1 the fused input projection + reductions, 2 the compact solve, 3 the apply
- * + output projection.  Results are those of lsso_hip_layer_forward.
+ * points to 8 hipEvent_t handles created with timing enabled (entries may be
+ * NULL); events[2k] takes the begin of the first kernel and events[2k+1] the
+ * end of the last kernel of stage k: 0 the phase table, 1 the fused input
+ * projection + reductions, 2 the compact solve, 3 the apply + output
+ * projection.  The kernel dispatches record them (hipExtLaunchKernel), so the
+ * timing adds no queue packet between the kernels.  Results are those of
+ * lsso_hip_layer_forward.
  * Replaces: the CUDA events around the timed region of the reference's
  * benchmark (benchmarks/benchmark_ball.py:189-206), moved inside the call so
  * that each stage is timed on its own. */

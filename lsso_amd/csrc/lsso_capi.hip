@@ -12,6 +12,15 @@
 #include "lsso_hip.h"
 #include "lsso_internal.h"
 
+namespace lsso_hip {
+
+DispatchEvents& dispatch_events() {
+    thread_local DispatchEvents events;
+    return events;
+}
+
+}  // namespace lsso_hip
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -1410,41 +1419,38 @@ int layer_forward_impl(const lsso_hip_mixer_shape* shape, const void* x, int x_d
         return fail(LSSO_HIP_EINVAL, "y must be 16-byte aligned");
     }
     hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-    // Optional timing marks: events[2 k] and events[2 k + 1] bracket stage k
-    // (0 phase table, 1 projection + reductions, 2 compact solve, 3 apply +
-    // output projection); NULL entries are skipped.
-    auto mark = [&](int index) -> int {
-        if (events == nullptr || events[index] == nullptr) {
-            return LSSO_HIP_OK;
+    // Optional timing: events[2 k] and events[2 k + 1] take the begin of the
+    // first and the end of the last kernel of stage k (0 phase table,
+    // 1 projection + reductions, 2 compact solve, 3 apply + output
+    // projection), recorded by the dispatches themselves; NULL entries are
+    // skipped.  The guard clears them on every return.
+    struct StageEvents {
+        void* const* events;
+        void set(int stage) const {
+            lsso_hip::DispatchEvents& d = lsso_hip::dispatch_events();
+            d.start = events != nullptr ? static_cast<hipEvent_t>(events[2 * stage]) : nullptr;
+            d.stop = events != nullptr ? static_cast<hipEvent_t>(events[2 * stage + 1]) : nullptr;
         }
-        const hipError_t error = hipEventRecord(static_cast<hipEvent_t>(events[index]), stream);
-        return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "hipEventRecord");
-    };
-    if ((status = mark(0)) != LSSO_HIP_OK) {
-        return status;
-    }
+        ~StageEvents() { lsso_hip::dispatch_events() = lsso_hip::DispatchEvents{}; }
+    } stage{events};
+    stage.set(0);
     status = run_phase(plan, buf, inverse_frequency, centered_positions, positions_mode, stream);
-    if (status != LSSO_HIP_OK || (status = mark(1)) != LSSO_HIP_OK) {
+    if (status != LSSO_HIP_OK) {
         return status;
     }
-
-    if ((status = mark(2)) != LSSO_HIP_OK) {
-        return status;
-    }
+    stage.set(1);
     status = run_project_reduce(plan, buf, x, x_dtype, in_weight, in_bias, row_mask, packed,
                                 positions_mode, group_heads, stream);
     if (status != LSSO_HIP_OK) {
         return status;
     }
-    if ((status = mark(3)) != LSSO_HIP_OK || (status = mark(4)) != LSSO_HIP_OK) {
-        return status;
-    }
+    stage.set(2);
     status = run_solve(plan, buf, core_base_raw, core_drive_weight, eta_raw, valid_counts, nullptr,
                        stream);
-    if (status != LSSO_HIP_OK || (status = mark(5)) != LSSO_HIP_OK ||
-        (status = mark(6)) != LSSO_HIP_OK) {
+    if (status != LSSO_HIP_OK) {
         return status;
     }
+    stage.set(3);
     if (lp.fused_out) {
         status = run_mix_project(plan, buf, packed, eta_raw, positions_mode, out_weight, out_bias,
                                  row_mask, y, y_dtype, stream);
@@ -1457,7 +1463,7 @@ int layer_forward_impl(const lsso_hip_mixer_shape* shape, const void* x, int x_d
                                 y_dtype, stream);
         }
     }
-    return status != LSSO_HIP_OK ? status : mark(7);
+    return status;
 }
 
 }  // namespace

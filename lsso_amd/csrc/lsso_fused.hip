@@ -462,9 +462,9 @@ static hipError_t launch_mix_project_hpw(const MixProjectArgs& a, int y_dtype, d
                                          hipStream_t stream) {
     constexpr int kDepth = mix_depth<R, NFB, HPW>();
     if (y_dtype == LSSO_HIP_F16) {
-        mix_project_kernel<R, NFB, LSSO_HIP_F16, kDepth, HPW><<<grid, kMixThreads, 0, stream>>>(a);
+        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_F16, kDepth, HPW>, grid, kMixThreads, stream, a);
     } else {
-        mix_project_kernel<R, NFB, LSSO_HIP_BF16, kDepth, HPW><<<grid, kMixThreads, 0, stream>>>(a);
+        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_BF16, kDepth, HPW>, grid, kMixThreads, stream, a);
     }
     return hipGetLastError();
 }

@@ -2,11 +2,35 @@
 // units and the C ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
 namespace lsso_hip {
+
+// Events recorded by kernel dispatches themselves (hipExtLaunchKernel):
+// `start` with the begin of the next dispatch, `stop` with the end of every
+// dispatch, so that after a group of launches it holds the last one's end.
+// Set per stage by the timed entry point around its own launches and cleared
+// before it returns; unset, dispatches are plain launches.  Unlike
+// hipEventRecord, this adds no queue packet between the kernels.
+struct DispatchEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+DispatchEvents& dispatch_events();   // this thread's
+
+template <typename... KArgs, typename... Args>
+inline void dispatch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream, Args... args) {
+    DispatchEvents& events = dispatch_events();
+    if (events.start == nullptr && events.stop == nullptr) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+        return;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, events.start, events.stop, 0, args...);
+    events.start = nullptr;
+}
 
 constexpr int kMaxPairs = 32;
 

@@ -577,15 +577,15 @@ static hipError_t launch_linear_kv(const LinearArgs& a, int x_dtype, int y_dtype
     const dim3 block(linear_waves<KSTEPS>() * 64);
     if (x_dtype == LSSO_HIP_F16) {
         if (y_dtype == LSSO_HIP_F16) {
-            linear_kernel<KSTEPS, LSSO_HIP_F16, LSSO_HIP_F16, XVEC><<<grid, block, 0, stream>>>(a);
+            dispatch(linear_kernel<KSTEPS, LSSO_HIP_F16, LSSO_HIP_F16, XVEC>, grid, block, stream, a);
         } else {
-            linear_kernel<KSTEPS, LSSO_HIP_F16, LSSO_HIP_BF16, XVEC><<<grid, block, 0, stream>>>(a);
+            dispatch(linear_kernel<KSTEPS, LSSO_HIP_F16, LSSO_HIP_BF16, XVEC>, grid, block, stream, a);
         }
     } else {
         if (y_dtype == LSSO_HIP_F16) {
-            linear_kernel<KSTEPS, LSSO_HIP_BF16, LSSO_HIP_F16, XVEC><<<grid, block, 0, stream>>>(a);
+            dispatch(linear_kernel<KSTEPS, LSSO_HIP_BF16, LSSO_HIP_F16, XVEC>, grid, block, stream, a);
         } else {
-            linear_kernel<KSTEPS, LSSO_HIP_BF16, LSSO_HIP_BF16, XVEC><<<grid, block, 0, stream>>>(a);
+            dispatch(linear_kernel<KSTEPS, LSSO_HIP_BF16, LSSO_HIP_BF16, XVEC>, grid, block, stream, a);
         }
     }
     return hipGetLastError();
@@ -608,15 +608,15 @@ hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dt
         const dim3 block(kStreamThreads);
         if (x_dtype == LSSO_HIP_F16) {
             if (y_dtype == LSSO_HIP_F16) {
-                linear_stream_kernel<LSSO_HIP_F16, LSSO_HIP_F16><<<grid, block, 0, stream>>>(a);
+                dispatch(linear_stream_kernel<LSSO_HIP_F16, LSSO_HIP_F16>, grid, block, stream, a);
             } else {
-                linear_stream_kernel<LSSO_HIP_F16, LSSO_HIP_BF16><<<grid, block, 0, stream>>>(a);
+                dispatch(linear_stream_kernel<LSSO_HIP_F16, LSSO_HIP_BF16>, grid, block, stream, a);
             }
         } else {
             if (y_dtype == LSSO_HIP_F16) {
-                linear_stream_kernel<LSSO_HIP_BF16, LSSO_HIP_F16><<<grid, block, 0, stream>>>(a);
+                dispatch(linear_stream_kernel<LSSO_HIP_BF16, LSSO_HIP_F16>, grid, block, stream, a);
             } else {
-                linear_stream_kernel<LSSO_HIP_BF16, LSSO_HIP_BF16><<<grid, block, 0, stream>>>(a);
+                dispatch(linear_stream_kernel<LSSO_HIP_BF16, LSSO_HIP_BF16>, grid, block, stream, a);
             }
         }
         return hipGetLastError();

@@ -1271,15 +1271,15 @@ static hipError_t launch_reduce(const ReduceArgs& a, int cpw, bool vec, hipStrea
     const dim3 grid(static_cast<unsigned>((a.total_waves + 3) / 4));
     if (cpw == 1) {
         if (vec) {
-            reduce_kernel<R, 1, true><<<grid, 256, 0, stream>>>(a);
+            dispatch(reduce_kernel<R, 1, true>, grid, 256, stream, a);
         } else {
-            reduce_kernel<R, 1, false><<<grid, 256, 0, stream>>>(a);
+            dispatch(reduce_kernel<R, 1, false>, grid, 256, stream, a);
         }
     } else {
         if (vec) {
-            reduce_kernel<R, 2, true><<<grid, 256, 0, stream>>>(a);
+            dispatch(reduce_kernel<R, 2, true>, grid, 256, stream, a);
         } else {
-            reduce_kernel<R, 2, false><<<grid, 256, 0, stream>>>(a);
+            dispatch(reduce_kernel<R, 2, false>, grid, 256, stream, a);
         }
     }
     return hipGetLastError();
@@ -1290,16 +1290,16 @@ static hipError_t launch_apply(const ApplyArgs& a, int nfbw, bool vec, hipStream
     const dim3 grid(static_cast<unsigned>((a.total_waves + 3) / 4));
     switch (nfbw) {
         case 1:
-            if (vec) apply_kernel<R, 1, true><<<grid, 256, 0, stream>>>(a);
-            else apply_kernel<R, 1, false><<<grid, 256, 0, stream>>>(a);
+            if (vec) dispatch(apply_kernel<R, 1, true>, grid, 256, stream, a);
+            else dispatch(apply_kernel<R, 1, false>, grid, 256, stream, a);
             break;
         case 2:
-            if (vec) apply_kernel<R, 2, true><<<grid, 256, 0, stream>>>(a);
-            else apply_kernel<R, 2, false><<<grid, 256, 0, stream>>>(a);
+            if (vec) dispatch(apply_kernel<R, 2, true>, grid, 256, stream, a);
+            else dispatch(apply_kernel<R, 2, false>, grid, 256, stream, a);
             break;
         default:
-            if (vec) apply_kernel<R, 4, true><<<grid, 256, 0, stream>>>(a);
-            else apply_kernel<R, 4, false><<<grid, 256, 0, stream>>>(a);
+            if (vec) dispatch(apply_kernel<R, 4, true>, grid, 256, stream, a);
+            else dispatch(apply_kernel<R, 4, false>, grid, 256, stream, a);
             break;
     }
     return hipGetLastError();
@@ -1310,10 +1310,10 @@ hipError_t launch_phase(const PhaseArgs& a, hipStream_t stream) {
     // and fewer than 2^32 entries (the plan bounds B * N * pairs).
     const dim3 grid(static_cast<unsigned>((a.count / 4 + 255) / 256));
     switch (a.pairs) {
-        case 8: phase_kernel<8><<<grid, 256, 0, stream>>>(a); break;
-        case 16: phase_kernel<16><<<grid, 256, 0, stream>>>(a); break;
-        case 24: phase_kernel<24><<<grid, 256, 0, stream>>>(a); break;
-        default: phase_kernel<32><<<grid, 256, 0, stream>>>(a); break;
+        case 8: dispatch(phase_kernel<8>, grid, 256, stream, a); break;
+        case 16: dispatch(phase_kernel<16>, grid, 256, stream, a); break;
+        case 24: dispatch(phase_kernel<24>, grid, 256, stream, a); break;
+        default: dispatch(phase_kernel<32>, grid, 256, stream, a); break;
     }
     return hipGetLastError();
 }
@@ -1330,10 +1330,10 @@ hipError_t launch_reduce(int rank, const ReduceArgs& a, int cpw, bool vec, hipSt
 hipError_t launch_solve(int rank, const SolveArgs& a, int64_t systems, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(systems));
     switch (rank) {
-        case 16: solve_kernel<16><<<grid, kSolveThreads, 0, stream>>>(a); break;
-        case 32: solve_kernel<32><<<grid, kSolveThreads, 0, stream>>>(a); break;
-        case 48: solve_kernel<48><<<grid, kSolveThreads, 0, stream>>>(a); break;
-        default: solve_kernel<64><<<grid, kSolveThreads, 0, stream>>>(a); break;
+        case 16: dispatch(solve_kernel<16>, grid, kSolveThreads, stream, a); break;
+        case 32: dispatch(solve_kernel<32>, grid, kSolveThreads, stream, a); break;
+        case 48: dispatch(solve_kernel<48>, grid, kSolveThreads, stream, a); break;
+        default: dispatch(solve_kernel<64>, grid, kSolveThreads, stream, a); break;
     }
     return hipGetLastError();
 }

@@ -607,9 +607,9 @@ template <int KSTEPS, int R, int CPW>
 hipError_t launch_pr_x(const ProjectReduceArgs& a, int x_dtype, int grid, hipStream_t stream) {
     const dim3 block(pr_waves<KSTEPS>() * 64);
     if (x_dtype == LSSO_HIP_F16) {
-        project_reduce_kernel<KSTEPS, R, CPW, LSSO_HIP_F16><<<grid, block, 0, stream>>>(a);
+        dispatch(project_reduce_kernel<KSTEPS, R, CPW, LSSO_HIP_F16>, grid, block, stream, a);
     } else {
-        project_reduce_kernel<KSTEPS, R, CPW, LSSO_HIP_BF16><<<grid, block, 0, stream>>>(a);
+        dispatch(project_reduce_kernel<KSTEPS, R, CPW, LSSO_HIP_BF16>, grid, block, stream, a);
     }
     return hipGetLastError();
 }
