@@ -136,6 +136,34 @@ def test_mixer_pivoting_systems_match_fp64_oracle(native, rank: int) -> None:
     assert _rel_l2(out, expected) <= 5e-3
 
 
+@pytest.mark.parametrize(("rank", "head_dim"), [(16, 32), (32, 32), (48, 32), (64, 64)])
+def test_mixer_default_init_is_the_complement_projection(native, rank, head_dim) -> None:
+    """At the default initialisation (Theta0 = W_drive = 0, so K = I and
+    U = Z / 2) the mixer output has the closed form Y = eta (C - P P^T C)
+    with P P^T = A (I + A^T A)^-1 A^T, A = rot(R) / sqrt(N) (reference
+    paper/main.tex:357-360): the native solve, apply and reductions checked
+    against a dense FP64 evaluation that shares none of their algebra."""
+
+    batch, heads, length = 2, 3, 777
+    projected, _base, _drive, eta_raw = _mixer_inputs(batch, rank, heads, head_dim, length, seed=rank + 5)
+    eta_raw = torch.tensor([0.9, -0.4, 0.05])
+    base = torch.zeros(heads, rank, rank)
+    drive = torch.zeros(heads, head_dim, rank)
+    mixed = _run_mixer(native, projected, base, drive, eta_raw)
+    wide = projected.double()
+    positions = torch.arange(length, dtype=torch.float64) - 0.5 * (length - 1)
+    relation = wide[..., : heads * rank].view(batch, length, heads, rank).transpose(1, 2)
+    content = wide[..., heads * rank:].view(batch, length, heads, head_dim).transpose(1, 2)
+    a = oracle.rank_rotary(relation, positions.view(1, -1).expand(batch, -1)) / length ** 0.5
+    eye = torch.eye(rank, dtype=torch.float64)
+    ppt = a @ torch.linalg.solve(eye + a.mT @ a, a.mT)
+    eta = (1 - 2.0 ** -23) * torch.tanh(eta_raw.double())
+    expected = eta.view(1, heads, 1, 1) * (content - ppt @ content)
+    expected = expected.transpose(1, 2).reshape(batch, length, heads * head_dim)
+    assert torch.isfinite(mixed).all()
+    assert _rel_l2(mixed, expected) < 5e-3
+
+
 @pytest.mark.parametrize("scale", (0.001, 64.0))
 def test_mixer_relation_scale_extremes(native, scale: float) -> None:
     """Reference tests/cuda/test_fast_path.py:1482-1509 (forward part)."""
