@@ -207,7 +207,7 @@ int lsso_hip_mixer_backward_ex(const lsso_hip_mixer_shape* shape,
 /* 1 if lsso_hip_mixer_forward_projected handles this shape, 0 if not (use
  * lsso_hip_mixer_forward followed by lsso_hip_linear), or a negative code for
  * an invalid shape.  The fused path covers heads <= 8, head_dim a multiple of
- * 16 up to 64, heads*head_dim <= 256 and heads*(rank+head_dim) <= 512.
+ * 16 up to 64, heads*head_dim <= 256 and heads*(rank+head_dim) <= 640.
  * Replaces: the choice between the native mixer and its output projection
  * in LSSO._forward_cuda (lsso/ball/model.py:389-405). */
 int lsso_hip_mixer_projected_supported(const lsso_hip_mixer_shape* shape);
@@ -360,6 +360,41 @@ int lsso_hip_project_mix_forward(const lsso_hip_mixer_shape* shape,
                                  void* packed,
                                  void* mixed,
                                  float* tape,
+                                 void* workspace,
+                                 size_t workspace_bytes,
+                                 void* stream);
+
+/* Training forward of the whole layer, one call: lsso_hip_project_mix_forward
+ * (packed, mixed and the tape for the backward) followed by the output
+ * projection y = lsso_hip_linear(mixed, out_weight, out_bias, row_mask,
+ * y_dtype).  Inside the fused readout's envelope
+ * (lsso_hip_mixer_projected_supported, packed rows up to 640 columns) the
+ * apply and the output projection run as one kernel that also stores mixed,
+ * so mixed is written once and not read back; outside it, as two kernels.
+ * All four outputs are bitwise those of the separate calls.  Workspace:
+ * lsso_hip_mixer_workspace_bytes.
+ * Replaces: the module's training forward, K1 + forward_train + K5
+ * (lsso/ball/model.py:270-405 with csrc/ball/binding.cpp:80-95). */
+int lsso_hip_layer_forward_train(const lsso_hip_mixer_shape* shape,
+                                 const void* x,
+                                 int x_dtype,
+                                 const float* in_weight,
+                                 const float* in_bias,
+                                 const uint8_t* row_mask,
+                                 const float* core_base_raw,
+                                 const float* core_drive_weight,
+                                 const float* eta_raw,
+                                 const float* inverse_frequency,
+                                 const float* centered_positions,
+                                 int positions_mode,
+                                 const float* valid_counts,
+                                 const float* out_weight,
+                                 const float* out_bias,
+                                 void* packed,
+                                 void* mixed,
+                                 float* tape,
+                                 void* y,
+                                 int y_dtype,
                                  void* workspace,
                                  size_t workspace_bytes,
                                  void* stream);

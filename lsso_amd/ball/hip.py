@@ -57,6 +57,7 @@ _SYMBOLS = (
     "lsso_hip_layer_forward",
     "lsso_hip_layer_forward_timed",
     "lsso_hip_project_mix_forward",
+    "lsso_hip_layer_forward_train",
     "lsso_hip_linear_weight_grad_workspace_bytes",
     "lsso_hip_linear_weight_grad",
 )
@@ -161,6 +162,13 @@ def _declare(library: ctypes.CDLL) -> None:
         ctypes.c_size_t, vp,
     ]  # shape, x, x_dtype, in_weight, in_bias, row_mask, base, drive, eta, inv_freq, positions,
     #    mode, counts, packed, mixed, tape, workspace, workspace_bytes, stream
+    library.lsso_hip_layer_forward_train.restype = ctypes.c_int
+    library.lsso_hip_layer_forward_train.argtypes = [
+        shape_p, vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_int, vp, vp, vp, vp, vp, vp,
+        vp, ctypes.c_int, vp, ctypes.c_size_t, vp,
+    ]  # shape, x, x_dtype, in_weight, in_bias, row_mask, base, drive, eta, inv_freq, positions,
+    #    mode, counts, out_weight, out_bias, packed, mixed, tape, y, y_dtype, workspace,
+    #    workspace_bytes, stream
 
 
 def default_library_path() -> Path:
@@ -906,8 +914,12 @@ def _project_mix_forward(
     valid_counts: torch.Tensor | None,
     row_mask: torch.Tensor | None,
     record_tape: bool,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
-    """(packed, mixed, tape) of lsso_hip_project_mix_forward (no autograd)."""
+    out_weight: torch.Tensor | None = None,
+    out_bias: torch.Tensor | None = None,
+):
+    """(packed, mixed, tape) of lsso_hip_project_mix_forward, or (packed,
+    mixed, tape, y) of lsso_hip_layer_forward_train when ``out_weight`` is
+    given (no autograd)."""
 
     library = _library()
     shape, mode = _layer_shape(
@@ -943,30 +955,61 @@ def _project_mix_forward(
         floats = ctypes.c_size_t()
         _check(library.lsso_hip_mixer_tape_floats(ctypes.byref(shape), ctypes.byref(floats)), library)
         tape = torch.empty(floats.value, dtype=torch.float32, device=device)
+    common = (
+        ctypes.byref(shape),
+        x.data_ptr(),
+        dtype_codes[x.dtype],
+        in_weight.data_ptr(),
+        None if in_bias is None else in_bias.data_ptr(),
+        mask_ptr,
+        core_base_raw.data_ptr(),
+        core_drive_weight.data_ptr(),
+        eta_raw.data_ptr(),
+        ctypes.cast(_inverse_frequency(shape.rank), ctypes.c_void_p),
+        None if centered_positions is None else centered_positions.data_ptr(),
+        mode,
+        None if valid_counts is None else valid_counts.data_ptr(),
+    )
+    if out_weight is None:
+        with torch.cuda.device(device):
+            status = library.lsso_hip_project_mix_forward(
+                *common,
+                packed.data_ptr(),
+                mixed.data_ptr(),
+                None if tape is None else tape.data_ptr(),
+                workspace.data_ptr(),
+                workspace_bytes.value,
+                _stream(device),
+            )
+        _check(status, library)
+        return packed, mixed, tape
+    dim = shape.heads * shape.head_dim
+    if out_weight.dtype != torch.float32 or tuple(out_weight.shape) != (dim, dim):
+        raise TypeError(f"out_weight must be float32 [{dim}, {dim}]")
+    if out_bias is not None and (out_bias.dtype != torch.float32 or tuple(out_bias.shape) != (dim,)):
+        raise TypeError(f"out_bias must be float32 [{dim}]")
+    _require_device_tensor(out_weight, "out_weight", device)
+    if out_bias is not None:
+        _require_device_tensor(out_bias, "out_bias", device)
+    out_weight = out_weight.contiguous()
+    out_bias = None if out_bias is None else out_bias.contiguous()
+    y = torch.empty((shape.batch, shape.length, dim), dtype=x.dtype, device=device)
     with torch.cuda.device(device):
-        status = library.lsso_hip_project_mix_forward(
-            ctypes.byref(shape),
-            x.data_ptr(),
-            dtype_codes[x.dtype],
-            in_weight.data_ptr(),
-            None if in_bias is None else in_bias.data_ptr(),
-            mask_ptr,
-            core_base_raw.data_ptr(),
-            core_drive_weight.data_ptr(),
-            eta_raw.data_ptr(),
-            ctypes.cast(_inverse_frequency(shape.rank), ctypes.c_void_p),
-            None if centered_positions is None else centered_positions.data_ptr(),
-            mode,
-            None if valid_counts is None else valid_counts.data_ptr(),
+        status = library.lsso_hip_layer_forward_train(
+            *common,
+            out_weight.data_ptr(),
+            None if out_bias is None else out_bias.data_ptr(),
             packed.data_ptr(),
             mixed.data_ptr(),
             None if tape is None else tape.data_ptr(),
+            y.data_ptr(),
+            dtype_codes[x.dtype],
             workspace.data_ptr(),
             workspace_bytes.value,
             _stream(device),
         )
     _check(status, library)
-    return packed, mixed, tape
+    return packed, mixed, tape, y
 
 
 class _ProjectMix(torch.autograd.Function):
@@ -1061,6 +1104,111 @@ def project_mix(
         centered_positions, valid_counts, row_mask, False,
     )
     return mixed
+
+
+class _Layer(torch.autograd.Function):
+    """Autograd of the whole layer run as one native training call
+    (lsso_hip_layer_forward_train: input projection, mixer with the tape and
+    output projection).  The backward is the output projection's VJP
+    (reference.py:205-247), the mixer VJP (cuda.py:256-280) and the input
+    projection's VJP, exactly as when the three run separately."""
+
+    @staticmethod
+    def forward(ctx, x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw,
+                out_weight, out_bias, centered_positions, valid_counts, row_mask):
+        with torch.no_grad():
+            packed, mixed, tape, y = _project_mix_forward(
+                x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw,
+                centered_positions, valid_counts, row_mask, True, out_weight, out_bias,
+            )
+        ctx.save_for_backward(x, in_weight, packed, core_base_raw, core_drive_weight, eta_raw, tape,
+                              row_mask, mixed, out_weight)
+        ctx.centered_positions = centered_positions
+        ctx.valid_counts = valid_counts
+        ctx.in_bias_dtype = None if in_bias is None else in_bias.dtype
+        ctx.out_bias_dtype = None if out_bias is None else out_bias.dtype
+        return y
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_y):
+        (x, in_weight, packed, core_base_raw, core_drive_weight, eta_raw, tape, row_mask, mixed,
+         out_weight) = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        need_mixer = any(needs[:6])
+        grad_mixed, grad_out_weight, grad_out_bias = _linear_vjp(
+            grad_y, mixed, out_weight, row_mask, need_mixer, needs[6],
+            ctx.out_bias_dtype is not None and needs[7], ctx.out_bias_dtype,
+        )
+        grad_x = grad_in_weight = grad_in_bias = grad_base = grad_drive = grad_eta = None
+        if need_mixer:
+            need_in_bias = ctx.in_bias_dtype is not None and needs[2]
+            fused_sums = need_in_bias and row_mask is None
+            grads = backward(
+                grad_mixed.to(dtype=torch.bfloat16),
+                packed,
+                core_base_raw,
+                core_drive_weight,
+                eta_raw,
+                tape,
+                ctx.centered_positions,
+                ctx.valid_counts,
+                column_sums=fused_sums,
+            )
+            grad_packed, grad_base, grad_drive, grad_eta = grads[:4]
+            grad_x, grad_in_weight, grad_in_bias = _linear_vjp(
+                grad_packed, x, in_weight, row_mask, needs[0], needs[1], need_in_bias,
+                ctx.in_bias_dtype, grads[4] if fused_sums else None,
+            )
+        return (
+            grad_x,
+            grad_in_weight,
+            grad_in_bias,
+            grad_base if needs[3] else None,
+            grad_drive if needs[4] else None,
+            grad_eta if needs[5] else None,
+            grad_out_weight,
+            grad_out_bias,
+            None,
+            None,
+            None,
+        )
+
+
+def layer_train(
+    x: torch.Tensor,
+    in_weight: torch.Tensor,
+    in_bias: torch.Tensor | None,
+    core_base_raw: torch.Tensor,
+    core_drive_weight: torch.Tensor,
+    eta_raw: torch.Tensor,
+    out_weight: torch.Tensor,
+    out_bias: torch.Tensor | None,
+    centered_positions: torch.Tensor | None = None,
+    valid_counts: torch.Tensor | None = None,
+    row_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """y = linear(project_mix(x, ...), out_weight, out_bias, x.dtype, row_mask)
+    in one native call (lsso_hip_layer_forward_train), bitwise that of the
+    two, with the apply and the output projection in one kernel inside the
+    fused readout's envelope.  Differentiable (first order); ask
+    ``layer_supported`` first."""
+
+    for name, value in (("centered_positions", centered_positions), ("valid_counts", valid_counts)):
+        if value is not None and value.requires_grad:
+            raise ValueError(f"the LSSO HIP fast path does not support gradients for {name}")
+    require_available()
+    if torch.is_grad_enabled() and _any_requires_grad(
+        x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw, out_weight, out_bias
+    ):
+        return _Layer.apply(
+            x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw, out_weight, out_bias,
+            centered_positions, valid_counts, row_mask,
+        )
+    return _project_mix_forward(
+        x, in_weight, in_bias, core_base_raw, core_drive_weight, eta_raw,
+        centered_positions, valid_counts, row_mask, False, out_weight, out_bias,
+    )[3]
 
 
 def _rows(value: torch.Tensor, features: int) -> torch.Tensor:
@@ -1225,10 +1373,10 @@ class _Linear(torch.autograd.Function):
     (lsso/ball/reference.py:205-247): BF16 operands with FP32 accumulation
     for the value and weight gradients, an FP32 sum of the upstream gradient
     for the bias.  The value gradient runs on the native projection kernel
-    (dX = bf16(dY) bf16(W), stored once in the value's dtype).  One native
-    pass over dY writes its BF16 copy for the weight gradient (a library GEMM
-    over all rows) and its column sums for the bias gradient.  Rows excluded
-    by ``row_mask`` carry no gradient."""
+    (dX = bf16(dY) bf16(W), stored once in the value's dtype), the weight and
+    bias gradients on the native weight-gradient kernel, which reads dY and
+    the value in their own dtypes.  Rows excluded by ``row_mask`` carry no
+    gradient."""
 
     @staticmethod
     def forward(ctx, value, weight, bias, output_dtype, row_mask):
@@ -1323,6 +1471,7 @@ __all__ = [
     "forward_train",
     "is_available",
     "layer_forward",
+    "layer_train",
     "layer_supported",
     "linear",
     "load",

@@ -306,24 +306,27 @@ class LSSO(nn.Module):
         if needs_grad and x.is_contiguous() and hip.layer_supported(
             x, self.w_bc.weight, self.core_base_raw, self.core_drive_weight, self.eta_raw
         ):
-            # Training: the input projection runs fused with the token
-            # reductions (one read of x, one write of the packed projection),
-            # bitwise equal to the separate linear + fast_mix below.
+            # Training: the whole layer in one native call that also keeps
+            # packed, mixed and the tape for the backward (the input
+            # projection runs fused with the token reductions, the apply with
+            # the output projection where the shapes allow), bitwise equal to
+            # the separate linear + fast_mix + linear below.
             centered_positions, valid_counts, mask = self._native_geometry(
                 x, valid_mask, position_ids
             )
-            mixed = hip.project_mix(
+            return hip.layer_train(
                 x,
                 self.w_bc.weight,
                 self.w_bc.bias,
                 self.core_base_raw,
                 self.core_drive_weight,
                 self.eta_raw,
+                self.w_o.weight,
+                self.w_o.bias,
                 centered_positions,
                 valid_counts,
                 row_mask=mask,
             )
-            return hip.linear(mixed, self.w_o.weight, self.w_o.bias, x.dtype, row_mask=mask)
         projected, centered_positions, valid_counts, mask = self._native_inputs(
             x, valid_mask, position_ids
         )

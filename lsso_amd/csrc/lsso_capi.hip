@@ -371,7 +371,7 @@ int compute_units(int* units) {
 int run_mix_project(const MixerPlan& plan, const MixerBuffers& buf, const void* projected,
                     const float* eta_raw, int positions_mode, const float* out_weight,
                     const float* out_bias, const uint8_t* row_mask, void* y, int y_dtype,
-                    hipStream_t stream) {
+                    hipStream_t stream, void* mixed = nullptr) {
     int units = 0;
     const int status = compute_units(&units);
     if (status != LSSO_HIP_OK) {
@@ -395,6 +395,7 @@ int run_mix_project(const MixerPlan& plan, const MixerBuffers& buf, const void* 
     mix.bias = out_bias;
     mix.row_mask = row_mask;
     mix.y = y;
+    mix.mixed = static_cast<uint16_t*>(mixed);
     mix.batch = plan.batch;
     mix.length = plan.length;
     mix.heads = plan.heads;
@@ -602,7 +603,7 @@ int lsso_hip_mixer_forward_projected(const lsso_hip_mixer_shape* shape, const vo
     if (!projected_shape_supported(plan)) {
         return fail(LSSO_HIP_EUNSUPPORTED,
                     "the fused mixer + output projection supports heads <= 8, head_dim a multiple "
-                    "of 16 up to 64, H*head_dim <= 256 and H*(rank+head_dim) <= 512; use "
+                    "of 16 up to 64, H*head_dim <= 256 and H*(rank+head_dim) <= 640; use "
                     "lsso_hip_mixer_forward followed by lsso_hip_linear");
     }
     if (y_dtype != LSSO_HIP_F16 && y_dtype != LSSO_HIP_BF16) {
@@ -1196,6 +1197,82 @@ int run_project_reduce(const MixerPlan& plan, const MixerBuffers& buf, const voi
 
 }  // namespace
 
+namespace {
+
+// Input projection + mixer with the tape (lsso_hip_project_mix_forward) and,
+// when out_weight is set, the output projection into y: fused with the apply
+// (which then also stores mixed) inside the fused readout's envelope, else
+// lsso_hip_linear over mixed.
+int project_mix_impl(const lsso_hip_mixer_shape* shape, const void* x, int x_dtype,
+                     const float* in_weight, const float* in_bias, const uint8_t* row_mask,
+                     const float* core_base_raw, const float* core_drive_weight,
+                     const float* eta_raw, const float* inverse_frequency,
+                     const float* centered_positions, int positions_mode,
+                     const float* valid_counts, const float* out_weight, const float* out_bias,
+                     void* packed, void* mixed, float* tape, void* y, int y_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream_handle) {
+    MixerPlan plan;
+    int status = make_plan(shape, positions_mode, &plan);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    const int group_heads = layer_group_heads(plan);
+    if (group_heads == 0) {
+        return fail(LSSO_HIP_EUNSUPPORTED,
+                    "the fused projection + mixer supports head_dim a multiple of 16 up to 64 and "
+                    "H*head_dim <= 384; use lsso_hip_linear and lsso_hip_mixer_forward");
+    }
+    if (x_dtype != LSSO_HIP_F16 && x_dtype != LSSO_HIP_BF16) {
+        return fail(LSSO_HIP_EINVAL, "x_dtype must be LSSO_HIP_F16 or LSSO_HIP_BF16");
+    }
+    if (x == nullptr || in_weight == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "x and in_weight must not be NULL");
+    }
+    if (!aligned(x, 16) || !aligned(packed, 16)) {
+        return fail(LSSO_HIP_EINVAL, "x and packed must be 16-byte aligned");
+    }
+    MixerBuffers buf{};
+    status = check_mixer_call(plan, packed, core_base_raw, core_drive_weight, eta_raw, mixed,
+                              centered_positions, positions_mode, workspace, workspace_bytes, &buf);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+    status = run_phase(plan, buf, inverse_frequency, centered_positions, positions_mode, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    status = run_project_reduce(plan, buf, x, x_dtype, in_weight, in_bias, row_mask, packed,
+                                positions_mode, group_heads, stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    status = run_solve(plan, buf, core_base_raw, core_drive_weight, eta_raw, valid_counts, tape,
+                       stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    if (out_weight == nullptr) {
+        return run_apply(plan, buf, packed, eta_raw, positions_mode, mixed,
+                         vector_rows(plan, packed, mixed), stream);
+    }
+    if (projected_shape_supported(plan)) {
+        return run_mix_project(plan, buf, packed, eta_raw, positions_mode, out_weight, out_bias,
+                               row_mask, y, y_dtype, stream, mixed);
+    }
+    status = run_apply(plan, buf, packed, eta_raw, positions_mode, mixed,
+                       vector_rows(plan, packed, mixed), stream);
+    if (status != LSSO_HIP_OK) {
+        return status;
+    }
+    return run_linear(mixed, LSSO_HIP_BF16, plan.batch * plan.length, plan.out_width,
+                      plan.out_width, out_weight, out_bias, row_mask, plan.out_width, y, y_dtype,
+                      stream);
+}
+
+
+}  // namespace
+
 extern "C" {
 
 int lsso_hip_layer_supported(const lsso_hip_mixer_shape* shape) {
@@ -1263,49 +1340,34 @@ int lsso_hip_project_mix_forward(const lsso_hip_mixer_shape* shape, const void* 
                                  int positions_mode, const float* valid_counts, void* packed,
                                  void* mixed, float* tape, void* workspace, size_t workspace_bytes,
                                  void* stream_handle) {
-    MixerPlan plan;
-    int status = make_plan(shape, positions_mode, &plan);
-    if (status != LSSO_HIP_OK) {
-        return status;
+    return project_mix_impl(shape, x, x_dtype, in_weight, in_bias, row_mask, core_base_raw,
+                            core_drive_weight, eta_raw, inverse_frequency, centered_positions,
+                            positions_mode, valid_counts, nullptr, nullptr, packed, mixed, tape,
+                            nullptr, 0, workspace, workspace_bytes, stream_handle);
+}
+
+int lsso_hip_layer_forward_train(const lsso_hip_mixer_shape* shape, const void* x, int x_dtype,
+                                 const float* in_weight, const float* in_bias,
+                                 const uint8_t* row_mask, const float* core_base_raw,
+                                 const float* core_drive_weight, const float* eta_raw,
+                                 const float* inverse_frequency, const float* centered_positions,
+                                 int positions_mode, const float* valid_counts,
+                                 const float* out_weight, const float* out_bias, void* packed,
+                                 void* mixed, float* tape, void* y, int y_dtype, void* workspace,
+                                 size_t workspace_bytes, void* stream_handle) {
+    if (out_weight == nullptr || y == nullptr || mixed == nullptr) {
+        return fail(LSSO_HIP_EINVAL, "out_weight, mixed and y must not be NULL");
     }
-    const int group_heads = layer_group_heads(plan);
-    if (group_heads == 0) {
-        return fail(LSSO_HIP_EUNSUPPORTED,
-                    "the fused projection + mixer supports head_dim a multiple of 16 up to 64 and "
-                    "H*head_dim <= 384; use lsso_hip_linear and lsso_hip_mixer_forward");
+    if (y_dtype != LSSO_HIP_F16 && y_dtype != LSSO_HIP_BF16) {
+        return fail(LSSO_HIP_EINVAL, "y_dtype must be LSSO_HIP_F16 or LSSO_HIP_BF16");
     }
-    if (x_dtype != LSSO_HIP_F16 && x_dtype != LSSO_HIP_BF16) {
-        return fail(LSSO_HIP_EINVAL, "x_dtype must be LSSO_HIP_F16 or LSSO_HIP_BF16");
+    if (!aligned(y, 16) || !aligned(mixed, 16)) {
+        return fail(LSSO_HIP_EINVAL, "y and mixed must be 16-byte aligned");
     }
-    if (x == nullptr || in_weight == nullptr) {
-        return fail(LSSO_HIP_EINVAL, "x and in_weight must not be NULL");
-    }
-    if (!aligned(x, 16) || !aligned(packed, 16)) {
-        return fail(LSSO_HIP_EINVAL, "x and packed must be 16-byte aligned");
-    }
-    MixerBuffers buf{};
-    status = check_mixer_call(plan, packed, core_base_raw, core_drive_weight, eta_raw, mixed,
-                              centered_positions, positions_mode, workspace, workspace_bytes, &buf);
-    if (status != LSSO_HIP_OK) {
-        return status;
-    }
-    hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-    status = run_phase(plan, buf, inverse_frequency, centered_positions, positions_mode, stream);
-    if (status != LSSO_HIP_OK) {
-        return status;
-    }
-    status = run_project_reduce(plan, buf, x, x_dtype, in_weight, in_bias, row_mask, packed,
-                                positions_mode, group_heads, stream);
-    if (status != LSSO_HIP_OK) {
-        return status;
-    }
-    status = run_solve(plan, buf, core_base_raw, core_drive_weight, eta_raw, valid_counts, tape,
-                       stream);
-    if (status != LSSO_HIP_OK) {
-        return status;
-    }
-    return run_apply(plan, buf, packed, eta_raw, positions_mode, mixed,
-                     vector_rows(plan, packed, mixed), stream);
+    return project_mix_impl(shape, x, x_dtype, in_weight, in_bias, row_mask, core_base_raw,
+                            core_drive_weight, eta_raw, inverse_frequency, centered_positions,
+                            positions_mode, valid_counts, out_weight, out_bias, packed, mixed, tape,
+                            y, y_dtype, workspace, workspace_bytes, stream_handle);
 }
 
 }  // extern "C"

@@ -30,12 +30,18 @@ constexpr int kMixThreads = 64 * kMixWaves;
 constexpr int kMixProjWaves = 4;                   // waves 0..3: output projection
 constexpr int kMixApplyWaves = kMixWaves - kMixProjWaves;
 constexpr int kMixIoThreads = 64 * kMixApplyWaves; // apply waves also stage the rows
-constexpr int kMixMaxWidth = 512;                  // packed row, BF16
-constexpr int kMixPitch = kMixMaxWidth + 8;        // LDS row pitch of the packed tile
+// Packed rows (BF16) of up to 512 columns, or of up to 640 in a second tier
+// (rank 48 at H = 8, d = 32: W = 640), whose larger packed tiles still fit
+// LDS (about 144 KB) and whose staging takes 10 instead of 8 16-byte pieces
+// per thread.
+constexpr int kMixMaxWidth = 640;
+template <int WMAX>
+constexpr int mix_pitch() { return WMAX + 8; }      // LDS row pitch of the packed tile
 constexpr int kMixKSteps = 16;                     // D <= 256
 constexpr int kMixDPitch = 16 * kMixKSteps + 8;    // LDS row pitch of the mixed tile
 constexpr int kMixStPitch = 64 + 8;                // LDS row pitch of a projection wave's output
-constexpr int kMixChunks = kMixRows * kMixMaxWidth / 8 / kMixIoThreads;
+template <int WMAX>
+constexpr int mix_chunks() { return kMixRows * WMAX / 8 / kMixIoThreads; }
 
 bool mix_project_supported(int64_t rank, int64_t heads, int64_t head_dim, int64_t width) {
     const bool rank_ok = rank == 16 || rank == 32 || rank == 48 || rank == 64;
@@ -47,10 +53,13 @@ bool mix_project_supported(int64_t rank, int64_t heads, int64_t head_dim, int64_
 int mix_project_tile_rows() { return kMixRows; }
 
 // HPW: heads per apply wave (1 for H <= 4, else 2); DEPTH: row tiles staged
-// in registers ahead of the one being applied (1 or 2).
-template <int R, int NFB, int YT, int DEPTH, int HPW>
+// in registers ahead of the one being applied (1 or 2); WMAX: the packed row
+// tier (512 or 640 columns); MIXED: also store the mixed tiles (a.mixed).
+template <int R, int NFB, int YT, int DEPTH, int HPW, int WMAX, bool MIXED>
 __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs a) {
     using AL = ApplyLayout<R>;
+    constexpr int kMixPitch = mix_pitch<WMAX>();
+    constexpr int kMixChunks = mix_chunks<WMAX>();
     constexpr int PAIRS = R / 2;
     constexpr int PHP = PAIRS + 4;                 // LDS phase row pitch (u32)
     constexpr int S32 = AL::kSteps32 > 0 ? AL::kSteps32 : 1;
@@ -194,6 +203,22 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
 #pragma unroll
                 for (int i = 0; i < kMixRows * 8 / 64; ++i) {
                     buffer_store16(*reinterpret_cast<const u32x4*>(stage + piece_lds[i]), ybuf, piece_off[i]);
+                }
+            }
+            if (MIXED && k >= 1) {
+                // The training entry also keeps the mixed tile (the output
+                // projection's backward needs it): 16-byte pieces of whole
+                // rows, from the LDS tile the MFMAs above read.
+                const int t = k - 1;
+                const uint16_t* xt = s_mx[t & 1];
+                const int row_pieces = Di / 8;
+                const BufferRsrc mbuf = make_buffer(a.mixed + (b * a.length + tile_t0(t)) * D,
+                                                    int64_t{2} * tile_rows(t) * Di);
+                for (int p = wave * 64 + lane; p < kMixRows * row_pieces; p += 64 * kMixProjWaves) {
+                    const int row = p / row_pieces;
+                    const int c8 = 8 * (p - row * row_pieces);
+                    buffer_store16(*reinterpret_cast<const u32x4*>(xt + row * kMixDPitch + c8), mbuf,
+                                   2u * static_cast<uint32_t>(row * Di + c8));
                 }
             }
             __syncthreads();
@@ -454,19 +479,41 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
 
 // Two row tiles in flight where the register budget allows it (operand
 // records of at most four 32-rank feature blocks per wave), one otherwise.
-template <int R, int NFB, int HPW>
-constexpr int mix_depth() { return HPW * NFB * ((R + 31) / 32) <= 4 ? 2 : 1; }
+template <int R, int NFB, int HPW, int WMAX>
+constexpr int mix_depth() { return HPW * NFB * ((R + 31) / 32) <= 4 && WMAX <= 512 ? 2 : 1; }
 
+template <int R, int NFB, int HPW, int WMAX, bool MIXED>
+static void launch_mix_project_m(const MixProjectArgs& a, int y_dtype, dim3 grid, hipStream_t stream) {
+    constexpr int kDepth = mix_depth<R, NFB, HPW, WMAX>();
+    if (y_dtype == LSSO_HIP_F16) {
+        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_F16, kDepth, HPW, WMAX, MIXED>, grid, kMixThreads, stream, a);
+    } else {
+        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_BF16, kDepth, HPW, WMAX, MIXED>, grid, kMixThreads, stream,
+                 a);
+    }
+}
+
+template <int R, int NFB, int HPW, int WMAX>
+static hipError_t launch_mix_project_w(const MixProjectArgs& a, int y_dtype, dim3 grid,
+                                       hipStream_t stream) {
+    if (a.mixed != nullptr) {
+        launch_mix_project_m<R, NFB, HPW, WMAX, true>(a, y_dtype, grid, stream);
+    } else {
+        launch_mix_project_m<R, NFB, HPW, WMAX, false>(a, y_dtype, grid, stream);
+    }
+    return hipGetLastError();
+}
+
+// Packed rows wider than 512 occur only from rank 48 on (H * d <= 256).
 template <int R, int NFB, int HPW>
 static hipError_t launch_mix_project_hpw(const MixProjectArgs& a, int y_dtype, dim3 grid,
                                          hipStream_t stream) {
-    constexpr int kDepth = mix_depth<R, NFB, HPW>();
-    if (y_dtype == LSSO_HIP_F16) {
-        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_F16, kDepth, HPW>, grid, kMixThreads, stream, a);
-    } else {
-        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_BF16, kDepth, HPW>, grid, kMixThreads, stream, a);
+    if constexpr (R >= 48) {
+        if (a.width > 512) {
+            return launch_mix_project_w<R, NFB, HPW, 640>(a, y_dtype, grid, stream);
+        }
     }
-    return hipGetLastError();
+    return launch_mix_project_w<R, NFB, HPW, 512>(a, y_dtype, grid, stream);
 }
 
 template <int R, int NFB>

@@ -112,6 +112,7 @@ struct MixProjectArgs {
     const float* bias;          // FP32 [D] or nullptr
     const uint8_t* row_mask;    // [B * N] or nullptr
     void* y;                    // FP16/BF16 [B, N, D]
+    uint16_t* mixed;            // BF16 [B, N, D] (the apply output, kept for training) or nullptr
     int64_t batch;
     int64_t length;
     int64_t heads;
@@ -269,7 +270,7 @@ hipError_t launch_apply(int rank, const ApplyArgs& a, int nfbw, bool vec, hipStr
 // Projection launcher; k_steps = ceil(in_features / 16) rounded to a
 // compiled tier.  Returns hipErrorInvalidValue for an unsupported tier.
 // Shapes the fused apply + output projection handles: heads <= 8, head_dim a
-// multiple of 16 up to 64, D = heads * head_dim <= 256, width <= 512.
+// multiple of 16 up to 64, D = heads * head_dim <= 256, width <= 640.
 bool mix_project_supported(int64_t rank, int64_t heads, int64_t head_dim, int64_t width);
 int mix_project_tile_rows();
 hipError_t launch_mix_project(int rank, const MixProjectArgs& a, int y_dtype, hipStream_t stream);

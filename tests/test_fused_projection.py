@@ -42,6 +42,9 @@ def _two_step(native, projected, base, drive, eta_raw, positions, counts, weight
         (1, 64, 4, 64, 257),    # rank 64, widest operands
         (2, 16, 8, 16, 31),     # shorter than one tile
         (1, 32, 1, 48, 100),    # one head, three feature blocks
+        (2, 48, 8, 32, 333),    # C5 geometry: packed rows of 640 columns
+        (1, 64, 6, 16, 129),    # rank 64 at 480 columns, two heads per apply wave
+        (1, 64, 8, 16, 70),     # rank 64 at 640 columns
     ],
 )
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))

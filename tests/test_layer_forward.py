@@ -223,3 +223,91 @@ def test_project_mix_gradients_equal_the_two_call_path(native):
             torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
         else:
             assert torch.equal(got, want), name
+
+
+# -- training forward of the whole layer in one call --------------------------
+@pytest.mark.parametrize(
+    ("batch", "rank", "heads", "head_dim", "length", "masked"),
+    [
+        (2, 48, 8, 32, 333, False),   # C5 geometry: apply + output projection fused, 640-column rows
+        (2, 32, 8, 32, 1000, True),
+        (1, 64, 6, 64, 300, True),    # C4 geometry: D = 384, apply and projection separate
+        (3, 16, 8, 16, 65, False),
+    ],
+)
+def test_layer_train_is_bitwise_the_three_call_path(native, batch, rank, heads, head_dim, length, masked):
+    x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(
+        batch, rank, heads, head_dim, length, seed=6000 + rank + length
+    )
+    positions, counts, mask = None, None, None
+    if masked:
+        generator = torch.Generator().manual_seed(length + 1)
+        valid = torch.randint(length // 4, length + 1, (batch,), generator=generator)
+        mask = (torch.arange(length)[None, :] < valid[:, None]).cuda()
+        counts = valid.float().cuda()
+        raw = torch.arange(length, dtype=torch.float32)[None, :].repeat(batch, 1)
+        centre = (raw * mask.cpu()).sum(dim=1, keepdim=True) / valid[:, None]
+        positions = (raw - centre).cuda()
+    with torch.no_grad():
+        packed, mixed, tape, y = native._project_mix_forward(
+            x, in_w, in_b, base, drive, eta_raw, positions, counts, mask, True, out_w, out_b
+        )
+        expected_packed, expected_mixed, expected_tape = native._project_mix_forward(
+            x, in_w, in_b, base, drive, eta_raw, positions, counts, mask, True
+        )
+        expected_y = native.linear(expected_mixed, out_w, out_b, x.dtype, row_mask=mask)
+    torch.cuda.synchronize()
+    assert torch.equal(packed, expected_packed)
+    assert torch.equal(mixed, expected_mixed)
+    assert torch.equal(tape, expected_tape)
+    assert torch.equal(y, expected_y)
+    if mask is not None:
+        assert not y[~mask].any()
+
+
+def test_layer_train_gradients_equal_the_three_call_path(native):
+    x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(2, 48, 8, 32, 300, seed=78)
+    mask = torch.ones(2, 300, dtype=torch.bool, device="cuda")
+    mask[1, 250:] = False
+    counts = mask.sum(dim=1).float()
+    positions = torch.arange(300, dtype=torch.float32, device="cuda")[None, :].repeat(2, 1)
+    positions = positions - (positions * mask).sum(dim=1, keepdim=True) / counts[:, None]
+    upstream = torch.randn(2, 300, 8 * 32, device="cuda").half()
+
+    def run(fused: bool):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (x, in_w, in_b, base, drive, eta_raw, out_w, out_b)]
+        if fused:
+            y = native.layer_train(*leaves, positions, counts, row_mask=mask)
+        else:
+            mixed = native.project_mix(*leaves[:6], positions, counts, row_mask=mask)
+            y = native.linear(mixed, leaves[6], leaves[7], x.dtype, row_mask=mask)
+        y.backward(upstream)
+        return y.detach(), [leaf.grad for leaf in leaves]
+
+    fused_out, fused_grads = run(True)
+    split_out, split_grads = run(False)
+    assert torch.equal(fused_out, split_out)
+    names = ("x", "in_weight", "in_bias", "base", "drive", "eta", "out_weight", "out_bias")
+    for name, got, want in zip(names, fused_grads, split_grads):
+        assert got is not None and torch.isfinite(got).all(), name
+        assert torch.equal(got, want), name
+
+
+def test_module_training_forward_takes_the_one_call_path(native, monkeypatch):
+    from lsso_amd import LSSO, LSSOConfig
+
+    calls = []
+    original = native.layer_train
+
+    def spy(*args, **kwargs):
+        calls.append(1)
+        return original(*args, **kwargs)
+
+    monkeypatch.setattr(native, "layer_train", spy)
+    torch.manual_seed(0)
+    layer = LSSO(LSSOConfig(dim=256, num_heads=8, rank=48, bias=True)).cuda()
+    x = torch.randn(2, 200, 256, device="cuda").half().requires_grad_(True)
+    y = layer(x, implementation="hip")
+    y.float().square().mean().backward()
+    assert calls, "module training did not take the one-call layer path"
+    assert x.grad is not None and torch.isfinite(x.grad).all()

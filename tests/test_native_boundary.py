@@ -123,7 +123,9 @@ def test_fused_projection_envelope(library) -> None:
     assert library.lsso_hip_mixer_projected_supported(ctypes.byref(_shape(heads=8, rank=32, head_dim=32))) == 1
     assert library.lsso_hip_mixer_projected_supported(ctypes.byref(_shape(heads=2, rank=32, head_dim=96))) == 0
     assert library.lsso_hip_mixer_projected_supported(ctypes.byref(_shape(heads=9, rank=16, head_dim=16))) == 0
-    assert library.lsso_hip_mixer_projected_supported(ctypes.byref(_shape(heads=8, rank=48, head_dim=32))) == 0
+    # Packed rows up to 640 columns (rank 48 at H = 8, d = 32), not 768.
+    assert library.lsso_hip_mixer_projected_supported(ctypes.byref(_shape(heads=8, rank=48, head_dim=32))) == 1
+    assert library.lsso_hip_mixer_projected_supported(ctypes.byref(_shape(heads=8, rank=64, head_dim=32))) == 0
     assert library.lsso_hip_mixer_projected_supported(ctypes.byref(_shape(rank=20))) == -2
 
 
