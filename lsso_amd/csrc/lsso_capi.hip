@@ -49,6 +49,15 @@ size_t align_up(size_t value) { return (value + 255) & ~static_cast<size_t>(255)
 constexpr int64_t kReduceChunkTokens = 512;
 constexpr int64_t kApplyTargetWaves = 4096;
 
+// From 4,096 tokens on, where the fused projection + reduce runs (rank <= 32),
+// chunks of 1,024 tokens halve the partials it writes and the solve reads
+// (8.4 MB each at C3) and still leave four chunks per sequence; the
+// standalone reduce keeps 512-token chunks for its wave count.  Either choice
+// depends on the sequence length and rank only, never on the batch.
+int64_t reduce_chunk_tokens(int64_t length, int64_t rank) {
+    return length >= 4096 && rank <= 32 ? 2 * kReduceChunkTokens : kReduceChunkTokens;
+}
+
 struct MixerPlan {
     int64_t batch, length, heads, rank, head_dim;
     int64_t width, out_width, pairs, phase_batches;
@@ -115,8 +124,8 @@ int make_plan(const lsso_hip_mixer_shape* shape, int positions_mode, MixerPlan* 
     // Chunks are whole 64-token tiles, so the fused projection + reduce and
     // the standalone reduce share one chunking (and their partials agree).
     static_assert(kReduceChunkTokens % 64 == 0, "reduce chunks are whole projection tiles");
-    p->reduce_chunk_tokens = kReduceChunkTokens;
-    p->reduce_chunks = ceil_div(p->length, kReduceChunkTokens);
+    p->reduce_chunk_tokens = reduce_chunk_tokens(p->length, p->rank);
+    p->reduce_chunks = ceil_div(p->length, p->reduce_chunk_tokens);
     if (lsso_hip::project_reduce_tile_rows() != 64) {
         return fail(LSSO_HIP_ERUNTIME, "internal: the projection tile is not 64 rows");
     }
