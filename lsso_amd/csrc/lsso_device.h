@@ -75,6 +75,18 @@ __device__ __forceinline__ void buffer_store16(u32x4 value, BufferRsrc buffer, u
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, value),
                                            buffer, offset, 0, 0);
 }
+// Streaming forms: the cache-policy operand 2 sets the instruction's `nt`
+// bit, so the lines are kept in the caches as streaming (first to be
+// evicted).  Used for the bulk token tensors a kernel touches once, so
+// that they do not push out what is reused (weights, phase tables,
+// partials, records, and the second head group's read of an x tile).
+__device__ __forceinline__ u32x4 buffer_load16_stream(BufferRsrc buffer, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(buffer, offset, 0, 2));
+}
+__device__ __forceinline__ void buffer_store16_stream(u32x4 value, BufferRsrc buffer, uint32_t offset) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, value),
+                                           buffer, offset, 0, 2);
+}
 
 // Round two floats to BF16 (round to nearest even, v_cvt_pk_bf16_f32) and
 // pack them, first value in the low half.

@@ -287,7 +287,7 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
         const BufferRsrc pk = make_buffer(sample_rows + static_cast<int64_t>(t0) * Wi, int64_t{2} * rows * Wi);
 #pragma unroll
         for (int c = 0; c < kMixChunks; ++c) {
-            st.chunk[c] = buffer_load16(pk, 16u * static_cast<uint32_t>(io + c * kMixIoThreads));
+            st.chunk[c] = buffer_load16_stream(pk, 16u * static_cast<uint32_t>(io + c * kMixIoThreads));
         }
         const BufferRsrc ph = make_buffer(sample_phases + static_cast<int64_t>(t0) * PAIRS,
                                           int64_t{4} * rows * PAIRS);

@@ -220,7 +220,7 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
             return (u32x4){lo.x, lo.y, hi.x, hi.y};
         };
         auto write_piece = [&](const BufferRsrc& obuf, const u32x4& v, int i) {
-            buffer_store16(v, obuf, store_base + static_cast<uint32_t>(i) * store_step);
+            buffer_store16_stream(v, obuf, store_base + static_cast<uint32_t>(i) * store_step);
         };
         auto store_piece = [&](const BufferRsrc& obuf, const uint16_t* yprev, int i) {
             write_piece(obuf, read_piece(yprev, i), i);
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
             const uint32_t base = 8 * cc < Di ? 2u * static_cast<uint32_t>(rr0 * Di + 8 * cc) : kOutOfRange;
 #pragma unroll
             for (int i = 0; i < kXChunks; ++i) {
-                st.x[i] = buffer_load16(xbuf, base + 2u * static_cast<uint32_t>(i * kRowStep * Di));
+                st.x[i] = buffer_load16_stream(xbuf, base + 2u * static_cast<uint32_t>(i * kRowStep * Di));
             }
         } else {
 #pragma unroll
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
                 const int rr = chunk / kChunksPerRow;
                 const int cc = chunk - rr * kChunksPerRow;
                 const uint32_t offset = 8 * cc < Di ? 2u * static_cast<uint32_t>(rr * Di + 8 * cc) : kOutOfRange;
-                st.x[i] = buffer_load16(xbuf, offset);
+                st.x[i] = buffer_load16_stream(xbuf, offset);
             }
         }
         const BufferRsrc pbuf = make_buffer(a.phases + c.b * a.phase_batch_stride + int64_t{c.t0} * PAIRS,
