@@ -65,12 +65,73 @@ def parse_args() -> argparse.Namespace:
                              "priority, so that one slice's compact solve can overlap another "
                              "slice's streaming kernels (A/B of that overlap; default 1 = one call)")
     parser.add_argument("--copy-mib", type=int, default=0,
-                        help="after the timed region, run one device copy of this many MiB "
-                             "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+                        help="after the timed region, run one torch device copy of this many MiB "
+                             "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE), then "
+                             "the copy/read/write probes, and report their rates as copy_ceiling")
     return parser.parse_args()
 
 
 STAGE_PROBE_STEPS = 10
+
+
+def copy_ceiling(mib, device):
+    """Device-copy rates on buffers of `mib` MiB, after the timed region.
+
+    First one torch `copy_` (ROCm's `__amd_rocclr_copyBuffer`), the dispatch
+    that scales rocprofv3's FETCH_SIZE / WRITE_SIZE; then the probes of
+    liblsso_probe_gfx950.so (one 16-byte vector per thread: a plain copy, the
+    same with the nontemporal hint, a read and a write), five launches each
+    on torch's current stream, timed with events around each launch.
+    Returns {probe: {"bytes", "ms", "GB/s"}} with the median time.
+    """
+    import ctypes
+    from lsso_amd.build import probe_library_path
+
+    source = torch.empty(mib << 20, dtype=torch.uint8, device=device).fill_(1)
+    target = torch.empty_like(source)
+    sink = torch.zeros(4, dtype=torch.int32, device=device)
+    torch.cuda.synchronize()
+    rates = {}
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    target.copy_(source)
+    stop.record()
+    torch.cuda.synchronize()
+    nbytes = source.numel()
+    rates["torch_copy"] = {"bytes": 2 * nbytes, "ms": start.elapsed_time(stop)}
+    path = probe_library_path()
+    if path.exists():
+        probe = ctypes.CDLL(str(path))
+        probe.lsso_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                          ctypes.c_int, ctypes.c_void_p]
+        probe.lsso_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                          ctypes.c_void_p]
+        probe.lsso_probe_write.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+        stream = torch.cuda.current_stream(device).cuda_stream
+        src, dst = source.data_ptr(), target.data_ptr()
+        probes = {
+            "probe_copy": (2 * nbytes, lambda: probe.lsso_probe_copy(src, dst, nbytes, 0, stream)),
+            "probe_copy_streaming": (2 * nbytes,
+                                     lambda: probe.lsso_probe_copy(src, dst, nbytes, 1, stream)),
+            "probe_read": (nbytes, lambda: probe.lsso_probe_read(src, sink.data_ptr(), nbytes, stream)),
+            "probe_write": (nbytes, lambda: probe.lsso_probe_write(dst, nbytes, stream)),
+        }
+        for name, (moved, launch) in probes.items():
+            pairs = []
+            for _ in range(5):
+                begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                begin.record()
+                code = launch()
+                end.record()
+                if code != 0:
+                    raise RuntimeError(f"{name} failed with code {code}")
+                pairs.append((begin, end))
+            torch.cuda.synchronize()
+            rates[name] = {"bytes": moved, "ms": statistics.median(b.elapsed_time(e) for b, e in pairs)}
+    for entry in rates.values():
+        entry["GB/s"] = entry["bytes"] / (entry["ms"] * 1e-3) / 1e9
+    del source, target, sink
+    return rates
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "mixer_forward_c3_l4096_hbm_traffic.md")
 
@@ -448,13 +509,7 @@ def main() -> int:
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
 
-    if args.copy_mib > 0:
-        source = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=device).fill_(1)
-        target = torch.empty_like(source)
-        torch.cuda.synchronize()
-        target.copy_(source)
-        torch.cuda.synchronize()
-        del source, target
+    copy_rates = copy_ceiling(args.copy_mib, device) if args.copy_mib > 0 else None
 
     ms_per_step = 1e3 * elapsed / args.steps
     value = tokens * args.steps / elapsed
@@ -536,6 +591,8 @@ def main() -> int:
                                                            mask_cpu, position_ids_cpu)
     if not args.no_parity:
         result["parity"] = parity(layer, x_cpu, check, fp32_output, samples, mask_cpu, position_ids_cpu)
+    if copy_rates is not None:
+        result["copy_ceiling"] = copy_rates
     print(json.dumps(result), flush=True)
     return 0
 

@@ -3,7 +3,9 @@
 Usage: ``python -m lsso_amd.build`` (or ``lsso_amd.build.build_library()``).
 The shared library lands in ``lsso_amd/_lib/liblsso_hip_gfx950.so``; object
 files go to ``_build/`` at the repository root.  Each translation unit is
-compiled in its own hipcc process, then linked once.
+compiled in its own hipcc process, then linked once.  The benchmark's HBM
+probes (``lsso_probe.hip``, not part of the mixer's C ABI) are linked into
+their own ``liblsso_probe_gfx950.so`` beside it.
 """
 
 from __future__ import annotations
@@ -32,6 +34,8 @@ SOURCES = (
     "lsso_project_reduce.hip",
     "lsso_weight_grad.hip",
 )
+PROBE_SOURCE = "lsso_probe.hip"
+PROBE_LIBRARY_NAME = f"liblsso_probe_{OFFLOAD_ARCH}.so"
 
 # Packed FP32 VALU forms (v_pk_add/mul/fma_f32) are disabled for all device
 # code: some of their forms have returned wrong results on the MI355X boxes
@@ -51,6 +55,10 @@ DEVICE_FLAGS = (
 
 def library_path() -> Path:
     return OUTPUT_DIR / LIBRARY_NAME
+
+
+def probe_library_path() -> Path:
+    return OUTPUT_DIR / PROBE_LIBRARY_NAME
 
 
 def _hipcc() -> str:
@@ -85,19 +93,23 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
         commands.append(
             [hipcc, *DEVICE_FLAGS, *include, "-c", str(SOURCE_DIR / source), "-o", str(obj)]
         )
+    probe_object = OBJECT_DIR / (PROBE_SOURCE + ".o")
+    commands.append(
+        [hipcc, *DEVICE_FLAGS, "-c", str(SOURCE_DIR / PROBE_SOURCE), "-o", str(probe_object)]
+    )
     workers = jobs or min(len(commands), os.cpu_count() or 1, 8)
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         for future in [pool.submit(_run, command, verbose) for command in commands]:
             future.result()
-    output = library_path()
-    temporary = output.with_suffix(".so.tmp")
-    _run(
-        [hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC",
-         *[str(o) for o in objects], "-o", str(temporary)],
-        verbose,
-    )
-    os.replace(temporary, output)
-    return output
+    for linked, output in ((objects, library_path()), ([probe_object], probe_library_path())):
+        temporary = output.with_suffix(".so.tmp")
+        _run(
+            [hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC",
+             *[str(o) for o in linked], "-o", str(temporary)],
+            verbose,
+        )
+        os.replace(temporary, output)
+    return library_path()
 
 
 if __name__ == "__main__":

@@ -247,3 +247,27 @@ def test_errors_are_thread_local(library) -> None:
     thread.join()
     assert seen == [""]
     assert "rank in" in _message(library)
+
+
+def test_probe_library_rejects_sizes_before_launch() -> None:
+    """The benchmark's HBM probes (liblsso_probe_gfx950.so, outside the
+    mixer's C ABI) load without a GPU and refuse sizes that are not whole
+    4,096-byte granules, and null or unaligned buffers, before any launch."""
+    from lsso_amd.build import probe_library_path
+
+    path = probe_library_path()
+    if not path.is_file():
+        pytest.fail(f"the probe library is not built at {path}; run __graft_entry__.build()")
+    probe = ctypes.CDLL(str(path))
+    probe.lsso_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                      ctypes.c_int, ctypes.c_void_p]
+    probe.lsso_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                      ctypes.c_void_p]
+    probe.lsso_probe_write.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    aligned = 1 << 20
+    assert probe.lsso_probe_copy(aligned, aligned, 0, 0, None) == 22
+    assert probe.lsso_probe_copy(aligned, aligned, 4096 + 16, 0, None) == 22
+    assert probe.lsso_probe_copy(aligned + 8, aligned, 4096, 1, None) == 22
+    assert probe.lsso_probe_copy(None, aligned, 4096, 0, None) == 22
+    assert probe.lsso_probe_read(aligned, None, 4096, None) == 22
+    assert probe.lsso_probe_write(aligned, 100, None) == 22
