@@ -109,3 +109,49 @@ def test_native_diagnostics_certify_the_native_operator() -> None:
     assert torch.all(native["q"] < 1.0)
     assert torch.all(native["state_bound_usage"] <= 1.0 + 1e-9)
     assert torch.all(native["adjoint_bound_usage"] <= 1.0 + 1e-9)
+
+
+@pytest.mark.gpu
+def test_native_diagnostics_match_the_dense_oracle_operator() -> None:
+    """The native certificates against closed forms of the oracle's compact
+    problem (oracle/lsso_reference.py, independent of the package's torch
+    path): q = ||T||_2 of the dense N x N operator
+    T = eta I + P (2 (I + K)^-1 - I - eta I) P^T, mu = lambda_min(sym(I + K)),
+    and the solve / adjoint ratios from dense FP64 solves."""
+
+    from lsso_amd.ball import hip
+    from oracle import lsso_reference as oracle
+
+    hip.load()
+    torch.manual_seed(74)
+    dim, heads, rank, length = 128, 4, 32, 300
+    layer = LSSO(LSSOConfig(dim=dim, num_heads=heads, rank=rank, bias=True)).cuda().eval()
+    with torch.no_grad():
+        layer.core_base_raw.normal_(std=0.1)
+        layer.core_drive_weight.normal_(std=0.1)
+        layer.eta_raw.normal_(std=0.3)
+    x = torch.randn(2, length, dim, generator=torch.Generator().manual_seed(75)).half()
+    mask = torch.arange(length)[None, :] < torch.tensor([[length], [120]])
+    rhs = torch.randn(2, heads, rank, dim // heads, dtype=torch.float64,
+                      generator=torch.Generator().manual_seed(76))
+    native = layer.diagnostics(x.cuda(), valid_mask=mask.cuda(), adjoint_rhs=rhs.cuda(), implementation="hip")
+    torch.cuda.synchronize()
+
+    params = {name: p.detach().float().cpu() for name, p in layer.named_parameters()}
+    config = {"dim": dim, "num_heads": heads, "rank": rank, "bias": True}
+    _, frame, state, _, generator, eta = oracle.compact_problem(params, config, x.float(), mask)
+    frame, state, generator, eta = (t.double() for t in (frame, state, generator, eta))
+    identity = torch.eye(rank, dtype=torch.float64)
+    system = identity + generator
+    eta4 = eta.view(1, heads, 1, 1)
+    reflection = 2.0 * torch.linalg.inv(system) - identity
+    dense = eta4 * torch.eye(length, dtype=torch.float64) + frame @ (reflection - eta4 * identity) @ frame.mT
+    expected = {
+        "q": torch.linalg.matrix_norm(dense, ord=2),
+        "mu": torch.linalg.eigvalsh(0.5 * (system + system.mT))[..., 0],
+        "state_ratio": torch.linalg.solve(system, state).norm(dim=(-2, -1)) / state.norm(dim=(-2, -1)),
+        "adjoint_ratio": torch.linalg.solve(system.mT, rhs).norm(dim=(-2, -1)) / rhs.norm(dim=(-2, -1)),
+    }
+    for key, value in expected.items():
+        rel = ((native[key].cpu() - value).abs() / value.abs()).max().item()
+        assert rel < 2e-2, (key, rel)

@@ -61,6 +61,30 @@ def test_mixer_lengths_match_fp64_oracle(native, length: int) -> None:
     assert _rel_l2(out, expected) <= 5e-3
 
 
+@pytest.mark.parametrize("tag", ("r32", "r48"))
+def test_mixer_matches_reference_written_abi_vectors(native, tag: str) -> None:
+    """The ABI vectors the real reference wrote in FP64
+    (tests/golden/fast_mix.npz, made by tests/golden/make_golden.py: BF16
+    packed input, default centred positions, head_dim 17 and 24) through the
+    native mixer."""
+
+    import numpy as np
+    from pathlib import Path
+
+    with np.load(Path(__file__).resolve().parent / "golden" / "fast_mix.npz") as data:
+        stored = torch.from_numpy(data[f"{tag}:projected"])
+        base = torch.from_numpy(data[f"{tag}:base"])
+        drive = torch.from_numpy(data[f"{tag}:drive"])
+        eta_raw = torch.from_numpy(data[f"{tag}:eta_raw"])
+        expected = torch.from_numpy(data[f"{tag}:mixed64"])
+    projected = stored.bfloat16()
+    assert torch.equal(projected.float(), stored)  # the stored values are BF16 values
+    out = _run_mixer(native, projected, base, drive, eta_raw)
+    assert out.shape == expected.shape
+    assert torch.isfinite(out).all()
+    assert _rel_l2(out, expected) <= 5e-3
+
+
 # Reference tests/cuda/test_fast_path.py:859-952 shape sweep (forward).
 EXPANDED = [
     (1, 16, 1, 1, 31), (1, 16, 1, 15, 31), (1, 16, 1, 17, 31), (1, 16, 1, 31, 33),
