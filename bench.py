@@ -80,7 +80,9 @@ def copy_ceiling(mib, device):
     First one torch `copy_` (ROCm's `__amd_rocclr_copyBuffer`), the dispatch
     that scales rocprofv3's FETCH_SIZE / WRITE_SIZE; then the probes of
     liblsso_probe_gfx950.so (one 16-byte vector per thread: a plain copy, the
-    same with the nontemporal hint, a read and a write), five launches each
+    same with the nontemporal hint, a read, a write, and the write as a raw
+    buffer store under cache-policy operands 0, 2 (nt), 16 (sc1) and 18),
+    five launches each
     on torch's current stream, timed with events around each launch.
     Returns {probe: {"bytes", "ms", "GB/s"}} with the median time.
     """
@@ -107,6 +109,8 @@ def copy_ceiling(mib, device):
         probe.lsso_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
                                           ctypes.c_void_p]
         probe.lsso_probe_write.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+        probe.lsso_probe_write_policy.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
+                                                  ctypes.c_void_p]
         stream = torch.cuda.current_stream(device).cuda_stream
         src, dst = source.data_ptr(), target.data_ptr()
         probes = {
@@ -115,6 +119,9 @@ def copy_ceiling(mib, device):
                                      lambda: probe.lsso_probe_copy(src, dst, nbytes, 1, stream)),
             "probe_read": (nbytes, lambda: probe.lsso_probe_read(src, sink.data_ptr(), nbytes, stream)),
             "probe_write": (nbytes, lambda: probe.lsso_probe_write(dst, nbytes, stream)),
+            **{f"probe_write_policy_{policy}": (
+                nbytes, lambda policy=policy: probe.lsso_probe_write_policy(dst, nbytes, policy, stream))
+               for policy in (0, 2, 16, 18)},
         }
         for name, (moved, launch) in probes.items():
             pairs = []

@@ -45,6 +45,16 @@ __global__ __launch_bounds__(kProbeThreads) void probe_write_kernel(probe_u32x4*
     dst[i] = (probe_u32x4){static_cast<uint32_t>(i), 0u, 0u, 0u};
 }
 
+// The same write through a raw buffer store whose cache-policy operand is
+// POLICY (2 = nt, 16 = sc1), one 4 KiB buffer per workgroup.
+template <int POLICY>
+__global__ __launch_bounds__(kProbeThreads) void probe_write_policy_kernel(probe_u32x4* __restrict__ dst) {
+    const __amdgpu_buffer_rsrc_t buffer = __builtin_amdgcn_make_buffer_rsrc(
+        dst + static_cast<size_t>(blockIdx.x) * kProbeThreads, 0, 16 * kProbeThreads, 0x00020000);
+    const probe_u32x4 value = {blockIdx.x * kProbeThreads + threadIdx.x, 0u, 0u, 0u};
+    __builtin_amdgcn_raw_buffer_store_b128(value, buffer, 16u * threadIdx.x, 0, POLICY);
+}
+
 constexpr uint64_t kProbeGranule = 16u * kProbeThreads;
 
 bool probe_size_ok(uint64_t bytes) {
@@ -85,6 +95,24 @@ int lsso_probe_read(const void* src, void* sink, uint64_t bytes, hipStream_t str
     hipLaunchKernelGGL(probe_read_kernel, dim3(static_cast<unsigned>(bytes / kProbeGranule)),
                        dim3(kProbeThreads), 0, stream, static_cast<const probe_u32x4*>(src),
                        static_cast<uint32_t*>(sink));
+    return static_cast<int>(hipGetLastError());
+}
+
+// Writes `bytes` of dst with the buffer-store cache-policy operand `policy`
+// (0, 2 = nt, 16 = sc1 or 18 = both); 22 (EINVAL) for another value.
+int lsso_probe_write_policy(void* dst, uint64_t bytes, int policy, hipStream_t stream) {
+    if (!probe_size_ok(bytes) || dst == nullptr || reinterpret_cast<uintptr_t>(dst) % 16 != 0) {
+        return 22;
+    }
+    const dim3 grid(static_cast<unsigned>(bytes / kProbeGranule));
+    auto* d = static_cast<probe_u32x4*>(dst);
+    switch (policy) {
+        case 0: hipLaunchKernelGGL(probe_write_policy_kernel<0>, grid, dim3(kProbeThreads), 0, stream, d); break;
+        case 2: hipLaunchKernelGGL(probe_write_policy_kernel<2>, grid, dim3(kProbeThreads), 0, stream, d); break;
+        case 16: hipLaunchKernelGGL(probe_write_policy_kernel<16>, grid, dim3(kProbeThreads), 0, stream, d); break;
+        case 18: hipLaunchKernelGGL(probe_write_policy_kernel<18>, grid, dim3(kProbeThreads), 0, stream, d); break;
+        default: return 22;
+    }
     return static_cast<int>(hipGetLastError());
 }
 

@@ -271,3 +271,7 @@ def test_probe_library_rejects_sizes_before_launch() -> None:
     assert probe.lsso_probe_copy(None, aligned, 4096, 0, None) == 22
     assert probe.lsso_probe_read(aligned, None, 4096, None) == 22
     assert probe.lsso_probe_write(aligned, 100, None) == 22
+    probe.lsso_probe_write_policy.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
+                                              ctypes.c_void_p]
+    assert probe.lsso_probe_write_policy(aligned, 4096, 1, None) == 22
+    assert probe.lsso_probe_write_policy(aligned, 100, 2, None) == 22
