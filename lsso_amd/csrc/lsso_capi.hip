@@ -49,13 +49,15 @@ size_t align_up(size_t value) { return (value + 255) & ~static_cast<size_t>(255)
 constexpr int64_t kReduceChunkTokens = 512;
 constexpr int64_t kApplyTargetWaves = 4096;
 
-// From 4,096 tokens on, where the fused projection + reduce runs (rank <= 32),
-// chunks of 1,024 tokens halve the partials it writes and the solve reads
-// (8.4 MB each at C3) and still leave four chunks per sequence; the
-// standalone reduce keeps 512-token chunks for its wave count.  Either choice
-// depends on the sequence length and rank only, never on the batch.
-int64_t reduce_chunk_tokens(int64_t length, int64_t rank) {
-    return length >= 4096 && rank <= 32 ? 2 * kReduceChunkTokens : kReduceChunkTokens;
+// From 4,096 tokens on, chunks of 1,024 tokens halve the partials the
+// reductions write and the solve reads (8.4 MB each at C3) and still leave
+// four chunks per sequence (measured: the C3 call 0.251 against 0.256 ms, C4
+// 485.7 against 490.2 us).  Shorter sequences keep 512-token chunks: at 2,048
+// tokens, two chunks per sequence leave the standalone reduce too few waves
+// (the C5 step 1,166 against 1,139 us).  The choice depends on the sequence
+// length only, never on the batch.
+int64_t reduce_chunk_tokens(int64_t length) {
+    return length >= 4096 ? 2 * kReduceChunkTokens : kReduceChunkTokens;
 }
 
 struct MixerPlan {
@@ -124,7 +126,7 @@ int make_plan(const lsso_hip_mixer_shape* shape, int positions_mode, MixerPlan* 
     // Chunks are whole 64-token tiles, so the fused projection + reduce and
     // the standalone reduce share one chunking (and their partials agree).
     static_assert(kReduceChunkTokens % 64 == 0, "reduce chunks are whole projection tiles");
-    p->reduce_chunk_tokens = reduce_chunk_tokens(p->length, p->rank);
+    p->reduce_chunk_tokens = reduce_chunk_tokens(p->length);
     p->reduce_chunks = ceil_div(p->length, p->reduce_chunk_tokens);
     if (lsso_hip::project_reduce_tile_rows() != 64) {
         return fail(LSSO_HIP_ERUNTIME, "internal: the projection tile is not 64 rows");
