@@ -374,14 +374,22 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
     constexpr bool kRowStride = kIo % kChunksPerRow == 0;
     constexpr int kRowStep = kIo / kChunksPerRow;
     constexpr bool kPhaseStride = kIo % (PAIRS / 4) == 0;
-    auto load_stage = [&](Stage& st, const Cursor& c) {
+    // A stage is loaded in two halves (`part` 0: row mask, phases and the
+    // first half of the x pieces; 1: the rest), issued at the start and at
+    // the end of a step: the wave's loads then wait less for the memory
+    // pipeline behind the projection waves' packed stores (measured 0.8%
+    // faster per call than issuing all of them at once, and slower again
+    // with four parts).
+    auto load_stage = [&](Stage& st, const Cursor& c, int part) {
         const int io_o = opaque_int(io);
         const int rows = tile_rows(c);
         st.rows = rows;
-        const BufferRsrc mbuf = make_buffer(
-            a.row_mask + (a.row_mask != nullptr ? tile_row0(c) : 0),
-            a.row_mask != nullptr ? rows : 0);
-        st.mask = buffer_load_byte(mbuf, static_cast<uint32_t>(io_o));
+        if (part == 0) {
+            const BufferRsrc mbuf = make_buffer(
+                a.row_mask + (a.row_mask != nullptr ? tile_row0(c) : 0),
+                a.row_mask != nullptr ? rows : 0);
+            st.mask = buffer_load_byte(mbuf, static_cast<uint32_t>(io_o));
+        }
         const BufferRsrc xbuf = make_buffer(
             static_cast<const uint16_t*>(a.x) + tile_row0(c) * D, int64_t{2} * rows * D);
         const int Di = static_cast<int>(D);
@@ -391,17 +399,25 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
             const uint32_t base = 8 * cc < Di ? 2u * static_cast<uint32_t>(rr0 * Di + 8 * cc) : kOutOfRange;
 #pragma unroll
             for (int i = 0; i < kXChunks; ++i) {
-                st.x[i] = buffer_load16_stream(xbuf, base + 2u * static_cast<uint32_t>(i * kRowStep * Di));
+                if ((i < kXChunks / 2) == (part == 0)) {
+                    st.x[i] = buffer_load16_stream(xbuf, base + 2u * static_cast<uint32_t>(i * kRowStep * Di));
+                }
             }
         } else {
 #pragma unroll
             for (int i = 0; i < kXChunks; ++i) {
-                const int chunk = io_o + i * kIo;
-                const int rr = chunk / kChunksPerRow;
-                const int cc = chunk - rr * kChunksPerRow;
-                const uint32_t offset = 8 * cc < Di ? 2u * static_cast<uint32_t>(rr * Di + 8 * cc) : kOutOfRange;
-                st.x[i] = buffer_load16_stream(xbuf, offset);
+                if ((i < kXChunks / 2) == (part == 0)) {
+                    const int chunk = io_o + i * kIo;
+                    const int rr = chunk / kChunksPerRow;
+                    const int cc = chunk - rr * kChunksPerRow;
+                    const uint32_t offset =
+                        8 * cc < Di ? 2u * static_cast<uint32_t>(rr * Di + 8 * cc) : kOutOfRange;
+                    st.x[i] = buffer_load16_stream(xbuf, offset);
+                }
             }
+        }
+        if (part != 0) {
+            return;
         }
         const BufferRsrc pbuf = make_buffer(a.phases + c.b * a.phase_batch_stride + int64_t{c.t0} * PAIRS,
                                             int64_t{4} * rows * PAIRS);
@@ -510,11 +526,12 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
         }
     };
 
-    // One step for tile k (`cur`): loads of tile k + 2, reductions and (if it
-    // closes its chunk) partials of tile k - 1, tile k + 1 into LDS.
+    // One step for tile k (`cur`): loads of tile k + 2 (in two halves, around
+    // the reductions), reductions and (if it closes its chunk) partials of
+    // tile k - 1, tile k + 1 into LDS.
     auto step = [&](const Cursor& prev, const Cursor& cur, const Cursor& nx1, const Cursor& ahead,
                     Stage& load, const Stage& next, int k2, int k3) {
-        load_stage(load, ahead);
+        load_stage(load, ahead, 0);
         if (prev.item < n_items) {
             const uint16_t* yt = s_y[k2 ^ 1];
             const uint32_t* pt = s_ph[k3 == 0 ? 2 : k3 - 1];
@@ -558,6 +575,7 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
                 clear_units();
             }
         }
+        load_stage(load, ahead, 1);
         if (nx1.item < n_items) {
             write_stage(next, k2 ^ 1, k3 == 2 ? 0 : k3 + 1);
         }
@@ -568,8 +586,10 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
     Stage stage_b;
     Cursor cur = open_item(static_cast<int>(slot));
     Cursor nx1 = advance(cur);
-    load_stage(stage_a, cur);
-    load_stage(stage_b, nx1);
+    load_stage(stage_a, cur, 0);
+    load_stage(stage_a, cur, 1);
+    load_stage(stage_b, nx1, 0);
+    load_stage(stage_b, nx1, 1);
     write_stage(stage_a, 0, 0);
     __syncthreads();   // s_bias, s_col and tile 0 are in LDS
     Cursor prev = cur;
