@@ -121,7 +121,7 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape,
  * a GPU until the process ends.  Geometries whose
  * lsso_hip_mixer_workspace_bytes() exceeds that size are rejected with
  * LSSO_HIP_EUNSUPPORTED (B = 64, N = 4096, H = 8, r = 32, d = 32 needs about
- * 38 MB).  All calls on one GPU share its array: calls in flight at the same
+ * 21 MB).  All calls on one GPU share its array: calls in flight at the same
  * time on one GPU (on different streams) race, calls ordered on one stream do
  * not.  Arguments and results are those of lsso_hip_mixer_forward.
  * No counterpart in the reference: this entry point is for callers that cannot
