@@ -7,9 +7,13 @@ mask.  One step is one forward x -> y including both
 projections (reference protocol: benchmarks/benchmark_ball.py:156-208).
 
 Prints one JSON line with the driver's fields plus
-  roofline      the dominant kernel (the longer of the two fused streaming
-                kernels) from HIP events that the library records around each
-                stage of every timed step;
+  roofline      the projection + reduction stage (at the headline shape the
+                fused input projection + reduce kernel, the longest of the
+                call) from HIP events that the library records around that
+                stage in every timed step;
+  settle        the untimed back-to-back steps run before the warmup so that
+                the timed steps see the device's sustained clocks, with the
+                per-step time of the same number of steps started cold;
   cpu_baseline  the CPU oracle (FP32 restatement of the reference CPU path)
                 timed on this host on a bounded sample of the same workload.
 """
@@ -64,6 +68,15 @@ def parse_args() -> argparse.Namespace:
                              "layer call each, issued alternately on two streams of default "
                              "priority, so that one slice's compact solve can overlap another "
                              "slice's streaming kernels (A/B of that overlap; default 1 = one call)")
+    parser.add_argument("--settle-ms", type=float, default=250.0,
+                        help="before the warmup, run steps back to back for about this many "
+                             "milliseconds of GPU time so that the timed steps see the device's "
+                             "sustained clocks (0 disables; the JSON line reports the settle and the "
+                             "per-step time of --steps steps started right after an idle gap)")
+    parser.add_argument("--clock-trace", type=int, default=0,
+                        help="forward only: after the timed region, idle, then run this many steps, "
+                             "each followed by a one-wave shader-clock probe, and report the "
+                             "projection + reduce kernel time and the clock over windows of steps")
     parser.add_argument("--copy-mib", type=int, default=0,
                         help="after the timed region, run one torch device copy of this many MiB "
                              "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE), then "
@@ -72,6 +85,48 @@ def parse_args() -> argparse.Namespace:
 
 
 STAGE_PROBE_STEPS = 10
+# Idle time before the cold window of the settle phase: any idle gap of a few
+# milliseconds restarts the device's clock transient.
+SETTLE_IDLE_S = 0.05
+
+
+def settle(run_step, settle_ms: float, cold_steps: int) -> dict | None:
+    """Bring the device to its sustained clocks before a measurement.
+
+    After an idle gap of a few milliseconds an MI355X runs about the first
+    1.5 ms of work at full speed, then every kernel of the layer (the
+    latency-bound solve as much as the streaming kernels) slows by up to a
+    quarter for some tens of milliseconds before the clocks settle; a 20-step
+    run that starts after a gap measures that dip, not the sustained rate.
+    This function idles SETTLE_IDLE_S seconds, times `cold_steps` steps with
+    events (the per-step time such a run measures), then runs steps back to
+    back, with no host synchronization, for about `settle_ms` milliseconds of
+    GPU time.  The caller continues without synchronizing until the
+    synchronization that opens its timed region.  Returns the settle's record
+    for the JSON line, or None when settle_ms is 0."""
+
+    if settle_ms <= 0:
+        return None
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    time.sleep(SETTLE_IDLE_S)
+    begin.record()
+    for _ in range(cold_steps):
+        run_step()
+    end.record()
+    torch.cuda.synchronize()
+    cold_ms = begin.elapsed_time(end) / cold_steps
+    steps = max(1, int(settle_ms / cold_ms + 0.5))
+    for _ in range(steps):
+        run_step()
+    return {
+        "ms": settle_ms,
+        "steps": steps,
+        "cold_steps": cold_steps,
+        "cold_ms_per_step": cold_ms,
+        "note": (f"untimed steps run back to back before the warmup; cold_ms_per_step is the event "
+                 f"time per step of {cold_steps} steps started after {SETTLE_IDLE_S * 1e3:.0f} ms idle"),
+    }
 
 
 def copy_ceiling(mib, device):
@@ -139,6 +194,54 @@ def copy_ceiling(mib, device):
         entry["GB/s"] = entry["bytes"] / (entry["ms"] * 1e-3) / 1e9
     del source, target, sink
     return rates
+CLOCK_SPINS = 300  # about 5 us of one dependent FMA chain per clock probe
+CLOCK_WINDOWS = (0, 5, 10, 20, 50, 100, 200, 400, 1000)
+
+
+def clock_trace(run_step, make_events, slot: int, steps: int, device) -> dict:
+    """Kernel time and shader clock per step from a cold start.
+
+    After SETTLE_IDLE_S seconds idle, `steps` steps run back to back, each
+    followed by lsso_probe_clock (one wave, CLOCK_SPINS dependent FMAs between
+    two reads of the shader-clock and constant-rate counters).  Events bracket
+    stage `slot` of each step.  Returns the mean kernel time and clock over
+    the windows of steps in CLOCK_WINDOWS."""
+
+    import ctypes
+    from lsso_amd.build import probe_library_path
+
+    probe = ctypes.CDLL(str(probe_library_path()))
+    probe.lsso_probe_clock.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    rate_khz = probe.lsso_probe_wall_clock_khz()
+    if rate_khz <= 0:
+        raise RuntimeError(f"lsso_probe_wall_clock_khz failed with code {rate_khz}")
+    records = torch.zeros(steps, 4, dtype=torch.int64, device=device)
+    step_events = []
+    for _ in range(steps):
+        events = [None] * 8
+        events[2 * slot], events[2 * slot + 1] = make_events(2)
+        step_events.append(events)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    torch.cuda.synchronize()
+    time.sleep(SETTLE_IDLE_S)
+    for index in range(steps):
+        run_step(step_events[index])
+        code = probe.lsso_probe_clock(records[index].data_ptr(), CLOCK_SPINS, stream)
+        if code != 0:
+            raise RuntimeError(f"lsso_probe_clock failed with code {code}")
+    torch.cuda.synchronize()
+    counts = records.cpu().tolist()
+    kernel_us = [ev[2 * slot].elapsed_time(ev[2 * slot + 1]) * 1e3 for ev in step_events]
+    clock_ghz = [c[0] / c[1] * rate_khz / 1e6 for c in counts]
+    windows = []
+    edges = [edge for edge in CLOCK_WINDOWS if edge < steps] + [steps]
+    for low, high in zip(edges[:-1], edges[1:]):
+        windows.append({"steps": [low, high],
+                        "kernel_us": statistics.mean(kernel_us[low:high]),
+                        "clock_ghz": statistics.mean(clock_ghz[low:high])})
+    return {"steps": steps, "idle_ms": SETTLE_IDLE_S * 1e3, "probe_spins": CLOCK_SPINS, "windows": windows}
+
+
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "mixer_forward_c3_l4096_hbm_traffic.md")
 
@@ -282,6 +385,7 @@ def train_benchmark(args: argparse.Namespace) -> int:
         y = layer(x, implementation="hip")
         y.float().square().mean().backward()
 
+    settled = settle(step, args.settle_ms, args.steps)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -318,6 +422,8 @@ def train_benchmark(args: argparse.Namespace) -> int:
                    "dim": dim, "heads": heads, "rank": rank, "bias": True, "io_dtype": "fp16",
                    "grad_dtype": "fp32 parameters, fp16 x", "loss": "mean(y^2)"},
     }
+    if settled is not None:
+        result["settle"] = settled
     print(json.dumps(result), flush=True)
     return 0
 
@@ -488,27 +594,24 @@ def main() -> int:
             if not torch.equal(torch.cat(sliced_step(None), 0), check):
                 print(f"the {slices}-slice step differs from the one-call step", file=sys.stderr)
                 return 1
-        for _ in range(args.warmup):
-            timed_step(None)
         # Per-stage times from untimed steps with events on all four stages
         # (the library's kernel dispatches record them).  Events on every
         # stage still add about ten microseconds to a step, so the timed
-        # steps carry only the two of the dominant kernel.
+        # steps carry only the two of the projection + reduction stage, the
+        # longest stage of every workload here.  Every event exists before
+        # the settle, so nothing between the settle and the timed region
+        # waits on the host.
         stage_events = [recorded_events(8) for _ in range(STAGE_PROBE_STEPS)]
-        torch.cuda.synchronize()
-        for events in stage_events:
-            step(events)
-        torch.cuda.synchronize()
-        stage_ms = {
-            name: statistics.mean(ev[2 * k].elapsed_time(ev[2 * k + 1]) for ev in stage_events)
-            for k, name in enumerate(stage_names)
-        }
-        dominant = max(stage_kernels, key=lambda name: stage_ms[name])
-        slot = stage_names.index(dominant)
+        slot = stage_names.index("project_reduce")
         timed_pairs = [recorded_events(2) for _ in range(args.steps)]
         timed_events = [[None] * 8 for _ in range(args.steps)]
         for events, pair in zip(timed_events, timed_pairs):
             events[2 * slot], events[2 * slot + 1] = pair
+        settled = settle(lambda: timed_step(None), args.settle_ms, args.steps)
+        for events in stage_events:
+            step(events)
+        for _ in range(args.warmup):
+            timed_step(None)
         torch.cuda.synchronize()
         start = time.perf_counter()
         for index in range(args.steps):
@@ -516,7 +619,16 @@ def main() -> int:
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
 
+    stage_ms = {
+        name: statistics.mean(ev[2 * k].elapsed_time(ev[2 * k + 1]) for ev in stage_events)
+        for k, name in enumerate(stage_names)
+    }
+    dominant = stage_names[slot]
     copy_rates = copy_ceiling(args.copy_mib, device) if args.copy_mib > 0 else None
+    clocks = None
+    if args.clock_trace > 0:
+        with torch.inference_mode():
+            clocks = clock_trace(step, recorded_events, slot, args.clock_trace, device)
 
     ms_per_step = 1e3 * elapsed / args.steps
     value = tokens * args.steps / elapsed
@@ -591,6 +703,8 @@ def main() -> int:
             "stage_ms_source": f"{STAGE_PROBE_STEPS} untimed steps with events around every stage",
         },
     }
+    if settled is not None:
+        result["settle"] = settled
     fp32_output = None
     samples = min(args.cpu_samples, batch)
     if args.cpu_samples > 0:
@@ -600,6 +714,9 @@ def main() -> int:
         result["parity"] = parity(layer, x_cpu, check, fp32_output, samples, mask_cpu, position_ids_cpu)
     if copy_rates is not None:
         result["copy_ceiling"] = copy_rates
+    if clocks is not None:
+        clocks["kernel"] = kernel_name
+        result["clock_trace"] = clocks
     print(json.dumps(result), flush=True)
     return 0
 

@@ -55,6 +55,28 @@ __global__ __launch_bounds__(kProbeThreads) void probe_write_policy_kernel(probe
     __builtin_amdgcn_raw_buffer_store_b128(value, buffer, 16u * threadIdx.x, 0, POLICY);
 }
 
+// Shader clock of the moment: one lane runs `spins` dependent FMAs between
+// two reads of the shader-clock counter (s_memtime) and of the constant-rate
+// counter (s_memrealtime, hipDeviceAttributeWallClockRate), and stores both
+// differences in record[0] and record[1] (record[2] keeps the chain's value
+// live).  The ratio times the constant rate is the clock the probe ran at.
+__global__ __launch_bounds__(64) void probe_clock_kernel(uint64_t* __restrict__ record, int spins) {
+    if (threadIdx.x != 0) {
+        return;
+    }
+    const uint64_t clock0 = clock64();
+    const uint64_t wall0 = wall_clock64();
+    float chain = 1.0f;
+    for (int i = 0; i < spins; ++i) {
+        chain = __builtin_fmaf(chain, 1.0000001f, 1.0e-7f);
+    }
+    const uint64_t clock1 = clock64();
+    const uint64_t wall1 = wall_clock64();
+    record[0] = clock1 - clock0;
+    record[1] = wall1 - wall0;
+    record[2] = static_cast<uint64_t>(chain > 2.0f);
+}
+
 constexpr uint64_t kProbeGranule = 16u * kProbeThreads;
 
 bool probe_size_ok(uint64_t bytes) {
@@ -114,6 +136,29 @@ int lsso_probe_write_policy(void* dst, uint64_t bytes, int policy, hipStream_t s
         default: return 22;
     }
     return static_cast<int>(hipGetLastError());
+}
+
+// One probe_clock_kernel launch writing three uint64 values at record
+// (8-byte aligned); `spins` in [1, 1 << 20].  Returns 0, 22 (EINVAL) for an
+// argument it does not take, or a hipError_t code.
+int lsso_probe_clock(void* record, int spins, hipStream_t stream) {
+    if (record == nullptr || reinterpret_cast<uintptr_t>(record) % 8 != 0 || spins < 1 || spins > (1 << 20)) {
+        return 22;
+    }
+    hipLaunchKernelGGL(probe_clock_kernel, dim3(1), dim3(64), 0, stream, static_cast<uint64_t*>(record), spins);
+    return static_cast<int>(hipGetLastError());
+}
+
+// The constant counter's rate in kHz (hipDeviceAttributeWallClockRate of
+// the current device), or a negative hipError_t code.
+int lsso_probe_wall_clock_khz(void) {
+    int device = 0;
+    int rate = 0;
+    hipError_t status = hipGetDevice(&device);
+    if (status == hipSuccess) {
+        status = hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate, device);
+    }
+    return status == hipSuccess ? rate : -static_cast<int>(status);
 }
 
 // Writes `bytes` of dst.
