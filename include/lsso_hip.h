@@ -123,7 +123,12 @@ int lsso_hip_mixer_forward(const lsso_hip_mixer_shape* shape,
  * LSSO_HIP_EUNSUPPORTED (B = 64, N = 4096, H = 8, r = 32, d = 32 needs about
  * 21 MB).  All calls on one GPU share its array: calls in flight at the same
  * time on one GPU (on different streams) race, calls ordered on one stream do
- * not.  Arguments and results are those of lsso_hip_mixer_forward.
+ * not.  Arguments and results are those of lsso_hip_mixer_forward.  The
+ * stream must belong to the current device (LSSO_HIP_EINVAL otherwise).  The
+ * first call on a device looks the array's address up (hipGetSymbolAddress);
+ * make that call outside stream capture, after which calls can be captured
+ * into a HIP graph and replayed (the kernels write every scratch byte they
+ * read, so no memset is recorded).
  * No counterpart in the reference: this entry point is for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc). */

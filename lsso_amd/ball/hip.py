@@ -19,6 +19,7 @@ from threading import Lock
 
 import torch
 
+from . import ops
 from .reference import rotary_inverse_frequency
 
 _LOAD_LOCK = Lock()
@@ -205,9 +206,14 @@ def _native_contract_version(library: ctypes.CDLL | None) -> int | None:
 
 
 def is_available() -> bool:
-    """Whether the strict DYNAMIC + Rank-Rotary library is loaded (cuda.py:57-63)."""
+    """Whether the strict DYNAMIC + Rank-Rotary library is loaded and its
+    operators are registered under ``torch.ops.lsso_equilibrium`` (cuda.py:57-63)."""
 
-    return _LIBRARY is not None and _native_contract_version(_LIBRARY) == _NATIVE_CONTRACT_VERSION
+    return (
+        _LIBRARY is not None
+        and _native_contract_version(_LIBRARY) == _NATIVE_CONTRACT_VERSION
+        and ops.is_registered()
+    )
 
 
 def require_available() -> None:
@@ -281,6 +287,10 @@ def load(path: str | os.PathLike[str] | None = None, *, device: torch.device | i
         if target != requested:
             raise RuntimeError(f"the LSSO HIP library targets {target}, not requested {requested}")
         _LIBRARY = library
+        # The reference's operators appear under torch.ops.lsso_equilibrium
+        # when its extension loads (binding.cpp:79-107); these are the same
+        # schemas, backed by this library.
+        ops.register()
         _LOADED_ARCHITECTURE = requested
 
 
@@ -588,15 +598,15 @@ def backward(
 
 
 class _FastMix(torch.autograd.Function):
-    """First-order autograd boundary of the native mixer (cuda.py:220-280)."""
+    """First-order autograd boundary of the native mixer (cuda.py:220-280),
+    calling the registered operators as the reference does."""
 
     @staticmethod
     def forward(ctx, projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts):
-        with torch.no_grad():
-            output, tape = forward_train(
-                projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
-            )
-        ctx.save_for_backward(projected, core_base_raw, core_drive_weight, eta_raw, tape)
+        output, tape, pivots = torch.ops.lsso_equilibrium.forward_train(
+            projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
+        )
+        ctx.save_for_backward(projected, core_base_raw, core_drive_weight, eta_raw, tape, pivots)
         ctx.centered_positions = centered_positions
         ctx.valid_counts = valid_counts
         return output
@@ -604,14 +614,15 @@ class _FastMix(torch.autograd.Function):
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad_output):
-        projected, core_base_raw, core_drive_weight, eta_raw, tape = ctx.saved_tensors
-        grads = backward(
-            grad_output.to(dtype=torch.bfloat16),
+        projected, core_base_raw, core_drive_weight, eta_raw, tape, pivots = ctx.saved_tensors
+        grads = torch.ops.lsso_equilibrium.backward(
+            grad_output.to(dtype=torch.bfloat16).contiguous(),
             projected,
             core_base_raw,
             core_drive_weight,
             eta_raw,
             tape,
+            pivots,
             ctx.centered_positions,
             ctx.valid_counts,
         )
@@ -647,7 +658,7 @@ def fast_mix(
     if not torch.is_grad_enabled() or not _any_requires_grad(
         projected, core_base_raw, core_drive_weight, eta_raw
     ):
-        return forward_inference(
+        return torch.ops.lsso_equilibrium.forward_inference(
             projected, core_base_raw, core_drive_weight, eta_raw, centered_positions, valid_counts
         )
     return _FastMix.apply(

@@ -446,6 +446,7 @@ int run_linear(const void* x, int x_dtype, int64_t rows, int64_t in_features,
     args.tiles = ceil_div(rows, lsso_hip::linear_tile_rows(tier));
     args.column_groups = ceil_div(out_features, lsso_hip::linear_columns_per_group(tier));
     args.x_vector = (in_features % 8 == 0 && x_row_stride % 8 == 0 && aligned(x, 16)) ? 1 : 0;
+    args.w_vector = (in_features % 4 == 0 && aligned(weight, 16)) ? 1 : 0;
     args.y_vector = (out_features % 8 == 0 && aligned(y, 16)) ? 1 : 0;
     int64_t groups = units / args.column_groups;
     // With several column groups, a whole number of XCD rounds lets the
@@ -533,12 +534,25 @@ namespace {
 std::mutex g_static_scratch_lock;
 void* g_static_scratch[kStaticScratchDevices];
 
-// Device address of `scratch` on the current device.
-int static_scratch(void** address) {
+// Device address of `scratch` on the current device, which must be the
+// stream's device: hipGetSymbolAddress answers for the current device only.
+int static_scratch(hipStream_t stream, void** address) {
     int device = 0;
     hipError_t error = hipGetDevice(&device);
     if (error != hipSuccess) {
         return hip_failure(error, "hipGetDevice");
+    }
+    int stream_device = device;
+    error = hipStreamGetDevice(stream, &stream_device);
+    if (error != hipSuccess) {
+        return hip_failure(error, "hipStreamGetDevice");
+    }
+    if (stream_device != device) {
+        return fail(LSSO_HIP_EINVAL,
+                    "the stream belongs to device " + std::to_string(stream_device) + " but device " +
+                        std::to_string(device) +
+                        " is current; make the stream's device current before calling "
+                        "lsso_hip_mixer_forward_static");
     }
     if (device < 0 || device >= kStaticScratchDevices) {
         return fail(LSSO_HIP_EUNSUPPORTED,
@@ -585,7 +599,7 @@ int lsso_hip_mixer_forward_static(const lsso_hip_mixer_shape* shape, const void*
                         "; use lsso_hip_mixer_forward with a caller workspace");
     }
     void* workspace = nullptr;
-    status = static_scratch(&workspace);
+    status = static_scratch(static_cast<hipStream_t>(stream_handle), &workspace);
     if (status != LSSO_HIP_OK) {
         return status;
     }

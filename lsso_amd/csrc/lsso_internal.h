@@ -200,6 +200,7 @@ struct LinearArgs {
     int64_t tiles;              // ceil(rows / tile_rows)
     int64_t column_groups;
     int x_vector;               // 16-byte x loads are legal
+    int w_vector;               // 16-byte W loads are legal (K % 4 == 0, W 16-byte aligned)
     int y_vector;               // 16-byte y stores are legal
 };
 

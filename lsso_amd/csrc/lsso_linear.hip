@@ -435,7 +435,7 @@ __global__ __launch_bounds__(kStreamThreads) void linear_stream_kernel(LinearArg
                 }
                 xs[i] = (u32x4){v[0], v[1], v[2], v[3]};
             }
-            if (K % 4 == 0) {
+            if (a.w_vector) {
                 const bool live0 = n < N && k < K;
                 const bool live1 = n < N && k + 4 < K;
                 ws[i][0] = live0 ? *reinterpret_cast<const f32x4*>(a.weight + n * K + k) : f32x4{};

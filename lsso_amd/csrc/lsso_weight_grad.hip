@@ -117,12 +117,19 @@ __global__ __launch_bounds__(kWgThreads) void weight_grad_kernel(WeightGradArgs 
     const int wave = tid >> 6;
     const int half = lane >> 5;
     const int64_t tiles = a.tiles_n * a.tiles_k;
-    const int64_t xcd = blockIdx.x % kWgXcds;
-    const int64_t slot = blockIdx.x / kWgXcds;
-    const int64_t tile = slot % tiles;
-    const int64_t split = (slot / tiles) * kWgXcds + xcd;
-    if (split >= a.splits) {
-        return;
+    int64_t tile = blockIdx.x;
+    int64_t split = 0;
+    if (a.splits > 1) {
+        // Row splits dealt round-robin over the XCDs, each XCD walking all
+        // output tiles of its splits.  With one split the grid holds one
+        // workgroup per output tile.
+        const int64_t xcd = blockIdx.x % kWgXcds;
+        const int64_t slot = blockIdx.x / kWgXcds;
+        tile = slot % tiles;
+        split = (slot / tiles) * kWgXcds + xcd;
+        if (split >= a.splits) {
+            return;
+        }
     }
     const int64_t nt = tile / a.tiles_k;
     const int64_t kt = tile - nt * a.tiles_k;
@@ -291,10 +298,13 @@ void plan_weight_grad(int64_t rows, int64_t in_features, int64_t out_features, i
     const int64_t stages = (rows + kWgRows - 1) / kWgRows;
     // As many row splits per XCD as let all of that XCD's workgroups (its
     // splits x the output tiles) be resident at once: one more, nearly empty
-    // round of workgroups would take as long as the first.
+    // round of workgroups would take as long as the first.  When the output
+    // tiles alone fill every resident slot of the device, splitting the rows
+    // gains no occupancy and only multiplies the FP32 partials (splits x N x
+    // K floats, written and summed again), so the rows stay in one split.
     int64_t per_xcd = kWgSlotsPerXcd / tiles;
     if (per_xcd < 1) per_xcd = 1;
-    int64_t want = kWgXcds * per_xcd;
+    int64_t want = tiles >= kWgXcds * kWgSlotsPerXcd ? 1 : kWgXcds * per_xcd;
     if (want > stages) want = stages;
     if (want < 1) want = 1;
     const int64_t per = (rows + want - 1) / want;
@@ -317,7 +327,7 @@ hipError_t launch_weight_grad(const WeightGradArgs& a, int g_dtype, int x_dtype,
     }
     const int64_t tiles = a.tiles_n * a.tiles_k;
     const int64_t rounds = (a.splits + kWgXcds - 1) / kWgXcds;
-    const dim3 grid(static_cast<unsigned>(rounds * kWgXcds * tiles));
+    const dim3 grid(static_cast<unsigned>(a.splits == 1 ? tiles : rounds * kWgXcds * tiles));
     if (g_dtype == LSSO_HIP_F16) {
         if (x_dtype == LSSO_HIP_F16) {
             launch_wg<LSSO_HIP_F16, LSSO_HIP_F16>(a, grid, stream);

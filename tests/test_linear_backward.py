@@ -179,6 +179,7 @@ def test_module_trains_with_a_summed_loss_and_runs_on_expanded_x(native) -> None
         (4099, 200, 72, torch.float16, torch.float16, True, 8),        # strided rows, partial tiles
         (777, 41, 13, torch.bfloat16, torch.float16, False, 3),        # scalar loads (odd widths)
         (31, 64, 48, torch.float16, torch.float16, True, 0),           # fewer rows than one stage
+        (320, 4096, 4096, torch.bfloat16, torch.bfloat16, False, 0),   # 1,024 output tiles: one split
     ],
 )
 def test_weight_gradient_kernel_matches_fp64_of_bf16_operands(

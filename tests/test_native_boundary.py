@@ -162,6 +162,10 @@ def test_weight_gradient_validation(library) -> None:
     assert library.lsso_hip_linear_weight_grad_workspace_bytes(131072, 256, 640, ctypes.byref(size)) == 0
     assert size.value >= 640 * 256 * 4 and size.value % 256 == 0
     assert library.lsso_hip_linear_weight_grad_workspace_bytes(0, 256, 640, ctypes.byref(size)) == 0
+    # 1,024 output tiles fill every resident slot: one row split, so the
+    # FP32 partials are one [N, K] block plus one bias row, not eight.
+    assert library.lsso_hip_linear_weight_grad_workspace_bytes(131072, 4096, 4096, ctypes.byref(size)) == 0
+    assert size.value == 4096 * 4096 * 4 + 4096 * 4
     assert library.lsso_hip_linear_weight_grad_workspace_bytes(-1, 256, 640, ctypes.byref(size)) == -1
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
     status = library.lsso_hip_linear_weight_grad(fake, 1, 64, fake, 3, 64, 10, 64, 64, None, fake, None,

@@ -43,18 +43,26 @@ def _inputs(batch, length, heads, rank, head_dim, seed, masked=False):
             None if counts is None else counts.to(device))
 
 
-def _static_forward(library, projected, base, drive, eta_raw, positions, counts, record_tape):
+def _shape_of(projected, base, drive):
     batch, length, _ = projected.shape
-    heads, rank = base.shape[0], base.shape[1]
-    head_dim = drive.shape[1]
-    shape = hip.MixerShape(batch, length, heads, rank, head_dim)
-    output = torch.full((batch, length, heads * head_dim), float("nan"), dtype=torch.bfloat16,
-                        device=projected.device)
+    return hip.MixerShape(batch, length, base.shape[0], base.shape[1], drive.shape[1])
+
+
+def _static_forward(library, projected, base, drive, eta_raw, positions, counts, record_tape):
+    shape = _shape_of(projected, base, drive)
+    output = torch.full((shape.batch, shape.length, shape.heads * shape.head_dim), float("nan"),
+                        dtype=torch.bfloat16, device=projected.device)
     tape = None
     if record_tape:
         floats = ctypes.c_size_t()
         assert library.lsso_hip_mixer_tape_floats(ctypes.byref(shape), ctypes.byref(floats)) == 0
         tape = torch.full((floats.value,), float("nan"), dtype=torch.float32, device=projected.device)
+    _call_static(library, shape, projected, base, drive, eta_raw, positions, counts, output, tape)
+    return output, tape
+
+
+def _call_static(library, shape, projected, base, drive, eta_raw, positions, counts, output, tape):
+    rank = shape.rank
     mode = 0 if positions is None else (2 if positions.dim() == 2 else 1)
     status = library.lsso_hip_mixer_forward_static(
         ctypes.byref(shape),
@@ -71,7 +79,6 @@ def _static_forward(library, projected, base, drive, eta_raw, positions, counts,
         torch.cuda.current_stream(projected.device).cuda_stream,
     )
     assert status == 0, library.lsso_hip_last_error().decode()
-    return output, tape
 
 
 CASES = [
@@ -114,3 +121,32 @@ def test_static_forward_rejects_geometries_beyond_its_scratch(library) -> None:
         None, None, 0, None, dummy.data_ptr(), None, torch.cuda.current_stream().cuda_stream)
     assert status == -2
     assert "more than the static scratch" in library.lsso_hip_last_error().decode()
+
+
+def test_static_forward_replays_from_a_captured_graph(library) -> None:
+    """Outputs allocated before capture, the device's first static call made
+    outside it; every replay, with eager static calls of another geometry
+    overwriting the shared array in between, equals the workspace entry."""
+
+    projected, base, drive, eta_raw, positions, counts = _inputs(4, 700, 4, 32, 32, 9)
+    expected, _ = hip._mixer_forward(projected, base, drive, eta_raw, positions, counts, False)
+    other = _inputs(2, 333, 3, 16, 32, 10, masked=True)
+    other_expected, _ = hip._mixer_forward(*other, False)
+    shape = _shape_of(projected, base, drive)
+    output = torch.empty_like(expected)
+    _call_static(library, shape, projected, base, drive, eta_raw, positions, counts, output, None)
+    torch.cuda.synchronize()
+    assert torch.equal(output, expected)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _call_static(library, shape, projected, base, drive, eta_raw, positions, counts, output, None)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        print(f"replay {replay}", flush=True)
+        output.zero_()
+        other_out, _ = _static_forward(library, *other, False)
+        torch.cuda.synchronize()
+        assert torch.equal(other_out, other_expected)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(output, expected), f"replay {replay}"
