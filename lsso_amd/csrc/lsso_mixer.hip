@@ -161,12 +161,11 @@ struct SolveLayout {
     static constexpr int kLinv = 0;                       // L^-1 rows
     static constexpr int kLinvT = kLinv + R * kLD;        // L^-1 transposed
     static constexpr int kTheta = kLinvT + R * kLD;       // Theta
-    static constexpr int kWork = kTheta + R * kLD;        // A; F; Gauss-Jordan rows in step order
+    static constexpr int kWork = kTheta + R * kLD;        // A; F; the rank-32 pivot-row buffer
     static constexpr int kSys = kWork + R * kLD;          // I + K, then (I + K)^-1
     static constexpr int kPanelA = kSys + R * kLD;        // S panel; drive panel; X panel
     static constexpr int kPanelB = kPanelA + R * kPLD;    // Z panel; M' panel
-    static constexpr int kPivot = kPanelB + R * kPLD;     // pivot row of each step
-    static constexpr int kTotal = kPivot + R;
+    static constexpr int kTotal = kPanelB + R * kPLD;
 };
 
 // A matrix row in registers: up to four 16-float vectors that are separate
@@ -488,17 +487,17 @@ __device__ __forceinline__ f32x4 mfma_tile_f32(f32x4 acc, int k_end, LoadA a, Lo
 }
 
 // Gauss-Jordan of a rank-32 system (the in-place form of solve_kernel, same
-// pivots, factors and updates element for element) with each matrix row split
-// over the two halves of the wave: lane l holds columns 16 (l / 32) .. + 15 of
-// row l % 32, so all 64 lanes update and each updates 16 columns.  Per step:
-// the pivot search runs over the half that holds column k; the row's column-k
-// value reaches the other half by a lane swap; the pivot row's two halves go
-// through LDS (s_rows, 64 floats per step parity; one lane per half writes,
-// each lane reads its half back as a broadcast).  Row p_k ends, scaled by
-// 1 / pivot, at row k of s_out; s_pivot[k] = p_k.
+// factors and updates element for element) with each matrix row split over
+// the two halves of the wave: lane l holds columns 16 (l / 32) .. + 15 of row
+// l % 32, so all 64 lanes update and each updates 16 columns.  Step k pivots
+// on the diagonal (no row exchanges: I + K has a positive definite symmetric
+// part, so every leading minor is nonzero); the rows' column-k value reaches
+// the other half by a lane swap, and the pivot row's two halves go through
+// LDS (s_rows, 64 floats per step parity; one lane per half writes, each
+// lane reads its half back as a broadcast).  Row k ends, scaled by
+// 1 / pivot_k, at row k of s_out.
 template <int LD>
-__device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s_out, float* s_rows, int* s_pivot,
-                                                    int lane) {
+__device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s_out, float* s_rows, int lane) {
     const int half = lane >> 5;
     const int row = lane & 31;
     f32x16 t;
@@ -510,8 +509,6 @@ __device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s
             t[4 * m + e] = v[e];
         }
     }
-    bool open = true;
-    int own_step = 0;
     float own_pivot = 1.0f;
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
@@ -519,17 +516,11 @@ __device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s
         const float own = t[k & 15];
         const float other = __shfl_xor(own, 32);
         const float x = owner ? own : other;
-        const unsigned magnitude = __float_as_uint(fabsf(own));
-        const unsigned best =
-            __builtin_amdgcn_readfirstlane(__ockl_wfred_max_u32(open && owner ? magnitude : 0u));
-        const unsigned long long ties = __ballot(open && owner && magnitude == best);
-        const int source = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(ties)));
-        const int p = source & 31;
-        const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(own), source));
+        const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(own), 32 * (k >> 4) + k));
         const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
-        const float f = row == p ? 0.0f : x * inv_pivot;
+        const float f = row == k ? 0.0f : x * inv_pivot;
         float* buf = s_rows + (k & 1) * 32 + 16 * half;
-        if (row == p) {
+        if (row == k) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 *reinterpret_cast<f32x4*>(buf + 4 * m) = (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
@@ -545,22 +536,17 @@ __device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s
             }
         }
         if (owner) {
-            t[k & 15] = row == p ? 1.0f : -f;
+            t[k & 15] = row == k ? 1.0f : -f;
         }
-        if (row == p) {
-            open = false;
-            own_step = k;
+        if (row == k) {
             own_pivot = pivot;
-        }
-        if (lane == 0) {
-            s_pivot[k] = p;
         }
     }
     t = t * __builtin_amdgcn_rcpf(own_pivot);
     wave_lds_order();
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        *reinterpret_cast<f32x4*>(s_out + own_step * LD + 16 * half + 4 * m) =
+        *reinterpret_cast<f32x4*>(s_out + row * LD + 16 * half + 4 * m) =
             (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
     }
 }
@@ -582,7 +568,6 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     float* s_sys = smem + SL::kSys;
     float* s_pa = smem + SL::kPanelA;
     float* s_pb = smem + SL::kPanelB;
-    int* s_pivot = reinterpret_cast<int*>(smem + SL::kPivot);
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -860,15 +845,18 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     }
     __syncthreads();
 
-    // ---- (I + K)^-1 by Gauss-Jordan in wave 0, in place, with implicit row
-    // pivoting: step k picks the largest |a_ik| over rows not yet used (first
-    // row on ties, as the LU partial pivoting it replaces), eliminates column
-    // k from every other row with the unscaled pivot row, and keeps column k
-    // as column p_k of the growing inverse.  Row p_k ends as pi_k times row k
-    // of the inverse with its columns in step order.
+    // ---- (I + K)^-1 by Gauss-Jordan in wave 0, in place, on the diagonal
+    // pivots: I + K = I + F F^T + Omega has the symmetric part I + F F^T >= I,
+    // so every leading principal minor is positive and elimination without
+    // row exchanges exists (its growth is bounded by the skew part relative to
+    // the symmetric part: Golub and Van Loan, "Unsymmetric positive definite
+    // linear systems", Linear Algebra Appl. 28, 1979).  Step k eliminates
+    // column k from every other row with the unscaled pivot row and keeps
+    // column k as column k of the growing inverse; row k ends as pivot_k
+    // times row k of the inverse.
     if constexpr (R == 32) {
         if (wave == 0) {
-            gauss_jordan_halves<LD>(s_sys, s_work, s_work, s_pivot, lane);
+            gauss_jordan_halves<LD>(s_sys, s_sys, s_work, lane);
         }
     } else if (wave == 0) {
         const bool live = lane < R;
@@ -876,33 +864,19 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         if (live) {
             row_load(rowv, s_sys + lane * LD);
         }
-        bool open = live;
-        int own_step = 0;
         float own_pivot = 1.0f;
         auto gj_step = [&](int k) {
             const float x = row_get(rowv, k);
-            const unsigned magnitude = __float_as_uint(fabsf(x));
-            const unsigned best = __builtin_amdgcn_readfirstlane(__ockl_wfred_max_u32(open ? magnitude : 0u));
-            const unsigned long long ties = __ballot(open && magnitude == best);
-            const int p = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(ties)));
-            const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), p));
+            const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
             const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
-            const float f = lane == p ? 0.0f : x * inv_pivot;
-            row_axpy_lane(rowv, f, p);
-            row_set(rowv, k, lane == p ? 1.0f : -f);
-            if (lane == p) {
-                open = false;
-                own_step = k;
+            const float f = lane == k ? 0.0f : x * inv_pivot;
+            row_axpy_lane(rowv, f, k);
+            row_set(rowv, k, lane == k ? 1.0f : -f);
+            if (lane == k) {
                 own_pivot = pivot;
-            }
-            if (lane == 0) {
-                s_pivot[k] = p;
             }
         };
         if constexpr (R <= 32) {
-            // Unrolled, the next step's pivot search overlaps the end of the
-            // current step's row updates (from rank 48 on, the unrolled
-            // chain spills registers).  Rank 32 takes gauss_jordan_halves.
 #pragma unroll
             for (int k = 0; k < R; ++k) {
                 gj_step(k);
@@ -921,17 +895,11 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
                 }
             }
         }
+        wave_lds_order();
         if (live) {
             row_scale(rowv, __builtin_amdgcn_rcpf(own_pivot));
-            row_store(s_work + own_step * LD, rowv);
+            row_store(s_sys + lane * LD, rowv);
         }
-    }
-    __syncthreads();
-    // Column order back to row numbers: inverse[k][p_m] = work[k][m].
-    for (int e = tid; e < R * R; e += kSolveThreads) {
-        const int k = e / R;
-        const int m = e - k * R;
-        s_sys[k * LD + s_pivot[m]] = s_work[k * LD + m];
     }
     __syncthreads();
     if (tape != nullptr) {
