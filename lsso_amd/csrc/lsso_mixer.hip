@@ -168,113 +168,21 @@ struct SolveLayout {
     static constexpr int kTotal = kPanelB + R * kPLD;
 };
 
-// A matrix row in registers: up to four 16-float vectors that are separate
-// local values of the kernel, bound here by reference.  Kept apart (not an
-// aggregate) so that a wave-uniform element index compiles to a relative
-// register move rather than a private-memory array.
-template <int Q>
-struct RegRow {
-    f32x16 &c0, &c1, &c2, &c3;
-    template <int q>
-    __device__ __forceinline__ f32x16& at() const {
-        if constexpr (q == 0) {
-            return c0;
-        } else if constexpr (q == 1) {
-            return c1;
-        } else if constexpr (q == 2) {
-            return c2;
-        } else {
-            return c3;
-        }
-    }
-};
-
-// Element k of a register row for a wave-uniform k.
-template <int Q, int q = 0>
-__device__ __forceinline__ float row_get(const RegRow<Q>& r, int k, float found = 0.0f) {
-    if constexpr (q < Q) {
-        const float c = r.template at<q>()[k & 15];
-        return row_get<Q, q + 1>(r, k, (k >> 4) == q ? c : found);
-    } else {
-        return found;
+// f(std::integral_constant<int, i>) for i = I .. N - 1, unrolled at compile
+// time.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void unroll_to(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        unroll_to<N, I + 1>(f);
     }
 }
-
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_set(const RegRow<Q>& r, int k, float value) {
-    if constexpr (q < Q) {
-        f32x16 t = r.template at<q>();
-        const float old = t[k & 15];
-        t[k & 15] = (k >> 4) == q ? value : old;
-        r.template at<q>() = t;
-        row_set<Q, q + 1>(r, k, value);
-    }
-}
-
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_load(const RegRow<Q>& r, const float* p) {
-    if constexpr (q < Q) {
-        f32x16 t;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(p + 16 * q + 4 * m);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                t[4 * m + e] = v[e];
-            }
-        }
-        r.template at<q>() = t;
-        row_load<Q, q + 1>(r, p);
-    }
-}
-
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_store(float* p, const RegRow<Q>& r) {
-    if constexpr (q < Q) {
-        const f32x16 t = r.template at<q>();
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            *reinterpret_cast<f32x4*>(p + 16 * q + 4 * m) =
-                (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
-        }
-        row_store<Q, q + 1>(p, r);
-    }
-}
-
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_scale(const RegRow<Q>& r, float factor) {
-    if constexpr (q < Q) {
-        r.template at<q>() = r.template at<q>() * factor;
-        row_scale<Q, q + 1>(r, factor);
-    }
-}
-
-#define LSSO_REG_ROW(name)                                              \
-    f32x16 name##_0 = 0.0f, name##_1 = 0.0f, name##_2 = 0.0f, name##_3 = 0.0f; \
-    const RegRow<Q> name{name##_0, name##_1, name##_2, name##_3}
 
 // LDS ordering between lanes of one wave: its LDS instructions execute in
 // issue order, so only the compiler must be kept from reordering.
 __device__ __forceinline__ void wave_lds_order() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// r -= f * (row of lane `source` of r), the source row read by v_readlane
-// element by element.  The source lane must pass f = 0, so its row is the
-// same before and after each element's update.
-template <int Q, int q = 0>
-__device__ __forceinline__ void row_axpy_lane(const RegRow<Q>& r, float f, int source) {
-    if constexpr (q < Q) {
-        f32x16 t = r.template at<q>();
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const float pivot_row = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[e]), source));
-            t[e] = fmaf(-f, pivot_row, t[e]);
-        }
-        r.template at<q>() = t;
-        row_axpy_lane<Q, q + 1>(r, f, source);
-    }
 }
 
 // Blocked Cholesky of the SPD matrix in LDS (row stride LD), one row per lane
@@ -360,20 +268,54 @@ __device__ __forceinline__ void cholesky_panel(float* s_diag, float* s_panel, fl
                 *reinterpret_cast<f32x4*>(s_panel + lane * B + 4) = (f32x4){x[4], x[5], x[6], x[7]};
             }
             wave_lds_order();
+            // The panel rows are read in batches of 8, each batch's reads
+            // issued before the previous batch's FMAs (scheduling barriers
+            // keep the compiler from moving each read next to its use, which
+            // would expose one LDS latency per row).
+            constexpr int kBatch = 8;
+            constexpr int kRows = R - C0 - B;
+            constexpr int kBatches = (kRows + kBatch - 1) / kBatch;
+            f32x4 cur[kBatch][2];
+            f32x4 nxt[kBatch][2];
+            auto read_batch = [&](f32x4 (&dst)[kBatch][2], int batch) {
 #pragma unroll
-            for (int j = C0 + B; j < R; ++j) {
-                const f32x4 p0 = *reinterpret_cast<const f32x4*>(s_panel + j * B);
-                const f32x4 p1 = *reinterpret_cast<const f32x4*>(s_panel + j * B + 4);
-                float acc = l[j];
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    acc = fmaf(-x[m], p0[m], acc);
+                for (int t = 0; t < kBatch; ++t) {
+                    const int j = C0 + B + batch * kBatch + t;
+                    if (j < R) {
+                        dst[t][0] = *reinterpret_cast<const f32x4*>(s_panel + j * B);
+                        dst[t][1] = *reinterpret_cast<const f32x4*>(s_panel + j * B + 4);
+                    }
                 }
+            };
+            read_batch(cur, 0);
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    acc = fmaf(-x[4 + m], p1[m], acc);
+            for (int batch = 0; batch < kBatches; ++batch) {
+                if (batch + 1 < kBatches) {
+                    read_batch(nxt, batch + 1);
                 }
-                l[j] = acc;
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = 0; t < kBatch; ++t) {
+                    const int j = C0 + B + batch * kBatch + t;
+                    if (j < R) {
+                        float acc = l[j];
+#pragma unroll
+                        for (int m = 0; m < 4; ++m) {
+                            acc = fmaf(-x[m], cur[t][0][m], acc);
+                        }
+#pragma unroll
+                        for (int m = 0; m < 4; ++m) {
+                            acc = fmaf(-x[4 + m], cur[t][1][m], acc);
+                        }
+                        l[j] = acc;
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = 0; t < kBatch; ++t) {
+                    cur[t][0] = nxt[t][0];
+                    cur[t][1] = nxt[t][1];
+                }
             }
         }
         cholesky_panel<R, LD, C0 + B>(s_diag, s_panel, s_inv_diag, lane, l);
@@ -396,35 +338,49 @@ __device__ __forceinline__ void blocked_cholesky(const float* s_a, float* s_diag
     cholesky_panel<R, LD, 0>(s_diag, s_panel, s_inv_diag, lane, l);
 }
 
-// Column `lane` of L^-1 from L^T (row-major in LDS, row stride LD) and the
-// reciprocal diagonal (LDS), right-looking: x_i = x_i / L_ii, then x_i' -= L_i'i x_i
-// for every i' > i, so each x_i' sums its terms in ascending i.
+// Column `lane` of L^-1 from L^T (row-major in LDS, row stride LD) whose
+// diagonal holds 1 / L_ii, right-looking: x_i = x_i / L_ii, then
+// x_i' -= L_i'i x_i for every i' > i, so each x_i' sums its terms in
+// ascending i.  The reads of row I are issued as one batch as soon as step
+// I - 1 has scaled x_{I-1} (an empty asm makes their address depend on it),
+// so they are in flight during step I - 1's FMAs; left to itself the
+// compiler either places each read next to its use (one LDS latency per
+// quad) or hoists every row's reads to the start (and spills).
 template <int R, int LD, int I>
-__device__ __forceinline__ void lower_inverse_step(const float* lt, const float* inv_diag, float (&x)[R]) {
+__device__ __forceinline__ void lower_inverse_step(const float* lt, float (&x)[R]) {
     if constexpr (I < R) {
-        x[I] *= inv_diag[I];
+        constexpr int qd = I / 4;   // quad holding the diagonal
+        int zero = 0;
+        if constexpr (I > 0) {
+            asm volatile("" : "+v"(zero) : "v"(x[I - 1]));
+        }
+        const float* row_ptr = lt + I * LD + zero;
+        f32x4 row[R / 4];
 #pragma unroll
-        for (int c = (I + 1) & ~3; c < R; c += 4) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(lt + I * LD + c);
+        for (int q = qd; q < R / 4; ++q) {
+            row[q] = *reinterpret_cast<const f32x4*>(row_ptr + 4 * q);
+        }
+        x[I] *= row[qd][I % 4];
+#pragma unroll
+        for (int q = qd; q < R / 4; ++q) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                if (c + e > I) {
-                    x[c + e] = fmaf(-v[e], x[I], x[c + e]);
+                if (4 * q + e > I) {
+                    x[4 * q + e] = fmaf(-row[q][e], x[I], x[4 * q + e]);
                 }
             }
         }
-        lower_inverse_step<R, LD, I + 1>(lt, inv_diag, x);
+        lower_inverse_step<R, LD, I + 1>(lt, x);
     }
 }
 
 template <int R, int LD>
-__device__ __forceinline__ void lower_inverse_column(const float* lt, const float* inv_diag, int lane,
-                                                     float (&x)[R]) {
+__device__ __forceinline__ void lower_inverse_column(const float* lt, int lane, float (&x)[R]) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         x[i] = lane == i ? 1.0f : 0.0f;
     }
-    lower_inverse_step<R, LD, 0>(lt, inv_diag, x);
+    lower_inverse_step<R, LD, 0>(lt, x);
 }
 
 // Rows first, first + step, ... (< R) of columns c0 .. c0 + width of
@@ -548,6 +504,93 @@ __device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s
     for (int m = 0; m < 4; ++m) {
         *reinterpret_cast<f32x4*>(s_out + row * LD + 16 * half + 4 * m) =
             (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
+    }
+}
+
+// (I + K)^-1 in place by Gauss-Jordan on the diagonal pivots, with all four
+// waves of the workgroup: wave w holds columns [w CW, (w + 1) CW) of every
+// row, lane i row i, CW = R / 4 floats in registers.  Step k:
+//   1. the wave owning column k forms the multipliers f_i = a_ik / a_kk (the
+//      pivot by v_readlane from lane k) and publishes them in s_f;
+//   2. one barrier;
+//   3. every wave reads its lane's f_i and its own CW-column segment of pivot
+//      row k (written by lane k at the end of step k - 1, a broadcast read),
+//      updates a_ij -= f_i a_kj, keeps column k as column k of the inverse
+//      (1 in row k, -f_i elsewhere), and lane k + 1 writes its updated
+//      segment for the next step.
+// Buffers alternate by step parity, so one barrier per step orders every
+// write after the reads of two steps earlier.  The arithmetic (f = a_ik *
+// rcp(a_kk), one FMA per element and step, each row scaled by rcp of its own
+// pivot at the end) is that of the one-row-per-lane form, element for
+// element, with a quarter of the row per lane.  s_buf: 128 + 8 CW + R floats.
+template <int R, int LD>
+__device__ __forceinline__ void gauss_jordan_waves(float* s_sys, float* s_buf, int wave, int lane) {
+    constexpr int CW = R / 4;
+    float* s_f = s_buf;                  // [2][64] multipliers
+    float* s_seg = s_buf + 128;          // [4 waves][2][CW] pivot-row segments
+    float* s_piv = s_seg + 8 * CW;       // [R] pivots
+    const bool live = lane < R;
+    float t[CW];
+#pragma unroll
+    for (int c = 0; c < CW; c += 4) {
+        const f32x4 v = live ? *reinterpret_cast<const f32x4*>(s_sys + lane * LD + wave * CW + c)
+                             : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            t[c + e] = v[e];
+        }
+    }
+    auto write_segment = [&](int parity) {
+        float* dst = s_seg + (wave * 2 + parity) * CW;
+#pragma unroll
+        for (int c = 0; c < CW; c += 4) {
+            *reinterpret_cast<f32x4*>(dst + c) = (f32x4){t[c], t[c + 1], t[c + 2], t[c + 3]};
+        }
+    };
+    if (lane == 0) {
+        write_segment(0);
+    }
+#pragma unroll 1
+    for (int owner = 0; owner < 4; ++owner) {
+        unroll_to<CW>([&](auto kc_c) {
+            constexpr int kc = decltype(kc_c)::value;
+            constexpr int parity = kc & 1;   // CW is even, so k and kc share parity
+            const int k = owner * CW + kc;
+            if (wave == owner) {
+                const float x = t[kc];
+                const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
+                s_f[parity * 64 + lane] = lane == k ? 0.0f : x * __builtin_amdgcn_rcpf(pivot);
+                if (lane == 0) {
+                    s_piv[k] = pivot;
+                }
+            }
+            __syncthreads();
+            const float f = s_f[parity * 64 + lane];
+            const float* seg = s_seg + (wave * 2 + parity) * CW;
+#pragma unroll
+            for (int c = 0; c < CW; c += 4) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(seg + c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    t[c + e] = fmaf(-f, v[e], t[c + e]);
+                }
+            }
+            if (wave == owner) {
+                t[kc] = lane == k ? 1.0f : -f;
+            }
+            if (lane == k + 1) {
+                write_segment(parity ^ 1);
+            }
+        });
+    }
+    __syncthreads();
+    if (live) {
+        const float inv = __builtin_amdgcn_rcpf(s_piv[lane]);
+#pragma unroll
+        for (int c = 0; c < CW; c += 4) {
+            *reinterpret_cast<f32x4*>(s_sys + lane * LD + wave * CW + c) =
+                (f32x4){t[c] * inv, t[c + 1] * inv, t[c + 2] * inv, t[c + 3] * inv};
+        }
     }
 }
 
@@ -686,12 +729,15 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         // Theta's LDS is free until the Theta assembly.
         float* s_inv_diag = s_theta + 64 + 8 * R;
         blocked_cholesky<R, LD>(s_work, s_theta, s_theta + 64, s_inv_diag, lane, lrow);
-        // L^T to LDS for the substitution (A in s_work is spent).
+        // L^T to LDS for the substitution (A in s_work is spent), with
+        // 1 / L_ii in place of each diagonal entry (the substitution reads it
+        // with the row).
         wave_lds_order();
         if (live) {
+            const float own_inv = s_inv_diag[lane];
 #pragma unroll
             for (int j = 0; j < R; ++j) {
-                s_work[j * LD + lane] = lrow[j];
+                s_work[j * LD + lane] = j == lane ? own_inv : lrow[j];
             }
             if (tape != nullptr) {
 #pragma unroll
@@ -703,7 +749,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         }
         wave_lds_order();
         float x[R];
-        lower_inverse_column<R, LD>(s_work, s_inv_diag, lane, x);
+        lower_inverse_column<R, LD>(s_work, lane, x);
         if (live) {
             // Lane c holds column c of L^-1: row c of L^-T and column c of L^-1.
 #pragma unroll
@@ -845,7 +891,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     }
     __syncthreads();
 
-    // ---- (I + K)^-1 by Gauss-Jordan in wave 0, in place, on the diagonal
+    // ---- (I + K)^-1 by Gauss-Jordan on all four waves, in place, on the diagonal
     // pivots: I + K = I + F F^T + Omega has the symmetric part I + F F^T >= I,
     // so every leading principal minor is positive and elimination without
     // row exchanges exists (its growth is bounded by the skew part relative to
@@ -854,52 +900,17 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     // column k from every other row with the unscaled pivot row and keeps
     // column k as column k of the growing inverse; row k ends as pivot_k
     // times row k of the inverse.
+    // Rank 32 keeps the one-wave form with each row split over the wave's
+    // halves (no barrier per step: 20.2 against 22.3 us for the C2 solve
+    // stage, 22.7 against 25.5 at C3); from rank 48 on, where a row per
+    // lane costs R FMAs per step, the four-wave form is faster (C4 solve
+    // stage 66.4 against 75.4 us).
     if constexpr (R == 32) {
         if (wave == 0) {
             gauss_jordan_halves<LD>(s_sys, s_sys, s_work, lane);
         }
-    } else if (wave == 0) {
-        const bool live = lane < R;
-        LSSO_REG_ROW(rowv);
-        if (live) {
-            row_load(rowv, s_sys + lane * LD);
-        }
-        float own_pivot = 1.0f;
-        auto gj_step = [&](int k) {
-            const float x = row_get(rowv, k);
-            const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
-            const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
-            const float f = lane == k ? 0.0f : x * inv_pivot;
-            row_axpy_lane(rowv, f, k);
-            row_set(rowv, k, lane == k ? 1.0f : -f);
-            if (lane == k) {
-                own_pivot = pivot;
-            }
-        };
-        if constexpr (R <= 32) {
-#pragma unroll
-            for (int k = 0; k < R; ++k) {
-                gj_step(k);
-            }
-        } else {
-            // Rolled over 16-column blocks, unrolled within one: the column
-            // index within a 16-float register chunk is then a constant, and
-            // only the choice of chunk is a run-time select (a run-time
-            // element index costs a select over all 16 elements of every
-            // chunk, for the read and again for the write of column k).
-#pragma unroll 1
-            for (int kb = 0; kb < R / 16; ++kb) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    gj_step(16 * kb + j);
-                }
-            }
-        }
-        wave_lds_order();
-        if (live) {
-            row_scale(rowv, __builtin_amdgcn_rcpf(own_pivot));
-            row_store(s_sys + lane * LD, rowv);
-        }
+    } else {
+        gauss_jordan_waves<R, LD>(s_sys, s_work, wave, lane);
     }
     __syncthreads();
     if (tape != nullptr) {
