@@ -132,21 +132,17 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
 //   Z = L^-1 S / sqrt(n)             product
 //   Theta = Theta0 + Z W / sqrt(n)   product
 //   I + K = I + F F^T + Omega        product
-//   (I + K)^-1                       Gauss-Jordan with partial (row) pivoting
+//   (I + K)^-1                       Gauss-Jordan on the diagonal pivots
 //   U = (I + K)^-1 Z, X = 2U - (1 + eta) Z, M' = L^-T X / sqrt(n)   products
 //
 // The Cholesky factor is blocked in 8-column panels in wave 0 (the diagonal
-// block and the panel pass through LDS, one row per lane).  Gauss-Jordan runs
-// in wave 0 with one matrix row per lane held in registers: a step's pivot
-// row reaches the other lanes by v_readlane into scalar registers, one
-// element per column, so a step is one chain of VALU instructions with no
-// LDS round trip.  Its step loop is unrolled up to rank 32 (the next pivot
-// search then overlaps the current row updates) and rolled above, where the
-// unrolled chain spills.  At rank 32 each row is split over the two wave
-// halves instead (16 columns per lane, the pivot row through LDS).  The substitution for L^-1 has no cross-lane traffic
-// and is unrolled.  The products use all four waves on FP32 MFMA tiles.
-extern "C" __device__ unsigned int __ockl_wfred_max_u32(unsigned int);
-
+// block and the panel pass through LDS, one row per lane).  The substitution
+// for L^-1 reads each row of L^T as one batch ahead of its FMAs.  I + K has a
+// positive definite symmetric part, so Gauss-Jordan needs no row exchanges:
+// at rank 32 it runs in wave 0 with each row split over the two wave halves,
+// from rank 48 on (and at rank 16) over all four waves with a quarter of
+// every row per lane and one barrier per step.  The products use all four
+// waves on FP32 MFMA tiles.
 constexpr int kSolveThreads = 256;
 constexpr int kSolvePanel = 64;
 
