@@ -51,6 +51,20 @@ __device__ __forceinline__ int opaque_int(int value) {
     return value;
 }
 
+// Workgroups are dealt to the eight XCDs of an MI355X round robin (workgroup
+// i runs on XCD i % 8, each XCD with its own L2).  A kernel whose
+// neighbouring work items read the same rows calls this to renumber its
+// workgroups so that consecutive logical blocks run on one XCD, one after
+// the other: logical block xcd * (n / 8) + k is physical block 8 k + xcd.
+// Blocks past the last whole round of eight keep their index.
+__device__ __forceinline__ int64_t xcd_local_block(int64_t physical, int64_t blocks) {
+    const int64_t per_xcd = blocks / 8;
+    if (physical >= per_xcd * 8) {
+        return physical;
+    }
+    return (physical % 8) * per_xcd + physical / 8;
+}
+
 // Raw buffer access.  An access past a buffer's num_records bytes does not
 // touch memory: loads return zero and stores are dropped.  Tile loops use
 // this instead of branches around their edge accesses, so every memory

@@ -159,6 +159,8 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     __shared__ __attribute__((aligned(16))) uint16_t s_y[kTileRows * YP];
     // Upper-K partial accumulators of a split tile, per slice, block, element and lane.
     __shared__ float s_part[KSPLIT == 2 ? kSlices * MB * 16 * 64 : 1];
+    // Row flags of the tile being multiplied and of the next one.
+    __shared__ int s_keep[2][kTileRows];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -192,7 +194,13 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         s_bias[c] = (a.bias != nullptr && n < N) ? a.bias[n] : 0.0f;
     }
 
+    // A tile's row flags are staged with its x: thread r < kTileRows reads
+    // the mask byte of row r through a raw buffer over the tile's valid rows
+    // (rows past the matrix, and every row when there is no mask, read as
+    // zero without an access), so no load waits inside the tile loop.
     XChunk stage[kChunksPerThread];
+    uint32_t stage_mask = 0;
+    int64_t stage_rows = 0;
     auto load_stage = [&](int64_t tile) {
 #pragma unroll
         for (int c = 0; c < kChunksPerThread; ++c) {
@@ -201,6 +209,10 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
             const int cc = chunk - rr * kChunksPerRow;
             stage[c] = fetch_x_chunk<XT, XVEC>(a, tile * kTileRows + rr, 8 * cc);
         }
+        stage_rows = a.rows - tile * kTileRows;
+        const BufferRsrc mask = make_buffer(a.row_mask != nullptr ? a.row_mask + tile * kTileRows : nullptr,
+                                            a.row_mask != nullptr ? stage_rows : 0);
+        stage_mask = buffer_load_byte(mask, static_cast<uint32_t>(tid));
     };
     auto write_stage = [&](int buf) {
 #pragma unroll
@@ -209,6 +221,9 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
             const int rr = chunk / kChunksPerRow;
             const int cc = chunk - rr * kChunksPerRow;
             *reinterpret_cast<u32x4*>(&s_x[buf][rr * KP + 8 * cc]) = finish_x_chunk<XT, XVEC>(stage[c]);
+        }
+        if (tid < kTileRows) {
+            s_keep[buf][tid] = tid < stage_rows && (a.row_mask == nullptr || stage_mask != 0);
         }
     };
 
@@ -228,8 +243,7 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         bool keep[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-            const int64_t m = tile * kTileRows + mb * 32 + (lane & 31);
-            keep[mb] = m < a.rows && (a.row_mask == nullptr || a.row_mask[m < a.rows ? m : 0] != 0);
+            keep[mb] = s_keep[buf][mb * 32 + (lane & 31)] != 0;
         }
         if (next < a.tiles) {
             load_stage(next);
@@ -328,7 +342,22 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         if (next < a.tiles) {
             write_stage(buf ^ 1);
         }
-        {
+        if (a.y_vector) {
+            // 16-byte pieces through a raw buffer over the tile's valid rows:
+            // pieces past the matrix are dropped without a branch.
+            const int64_t col0 = cg * kGroupColumns;
+            const int64_t tile_rows = a.rows - tile * kTileRows < kTileRows ? a.rows - tile * kTileRows : kTileRows;
+            const BufferRsrc ybuf = make_buffer(static_cast<uint16_t*>(a.y) + tile * kTileRows * N, 2 * tile_rows * N);
+#pragma unroll
+            for (int i = 0; i < kStoreChunks; ++i) {
+                const int chunk = tid + i * kThreads;
+                const int mr = chunk / (kGroupColumns / 8);
+                const int c8 = 8 * (chunk - mr * (kGroupColumns / 8));
+                const int64_t n = col0 + c8;
+                buffer_store16(*reinterpret_cast<const u32x4*>(&s_y[mr * YP + c8]), ybuf,
+                               n < N ? 2u * static_cast<uint32_t>(mr * N + n) : kOutOfRange);
+            }
+        } else {
             const int64_t col0 = cg * kGroupColumns;
 #pragma unroll
             for (int i = 0; i < kStoreChunks; ++i) {

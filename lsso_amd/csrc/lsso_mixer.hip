@@ -59,12 +59,15 @@ __global__ __launch_bounds__(256) void phase_kernel(PhaseArgs a) {
 // ---------------------------------------------------------------------------
 // Reduce.
 template <int R, int CPW, bool VEC>
-__global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
+__global__ __launch_bounds__(256, 2) void reduce_kernel(ReduceArgs a) {
     using L = ReduceLayout<R>;
     constexpr int NRB = L::kRowBlocks;
     constexpr int NGB = L::kGramBlocks;
     const int lane = threadIdx.x & 63;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    // Wave-uniform, so the work item and the buffer bases below are scalar.
+    // (Renumbering the workgroups of one (sample, chunk) onto one XCD, as
+    // the apply does, measured slower here: 97.7 against 91.3 us at rank 64.)
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (wave >= a.total_waves) {
         return;
     }
@@ -100,19 +103,69 @@ __global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
     const int64_t end = begin + a.chunk_tokens < a.length ? begin + a.chunk_tokens : a.length;
     ReduceTile<R, CPW> tile_a;
     ReduceTile<R, CPW> tile_b;
-    reduce_load<R, CPW, VEC>(tile_a, a, b, h, cg, q, g, begin, end);
-    if (begin + 32 < end) {
-        reduce_load<R, CPW, VEC>(tile_b, a, b, h, cg, q, g, begin + 32, end);
-    }
-    for (int64_t t0 = begin; t0 < end; t0 += 64) {
-        reduce_compute<R, CPW>(tile_a, do_gram, acc_g, acc_s);
-        if (t0 + 64 < end) {
-            reduce_load<R, CPW, VEC>(tile_a, a, b, h, cg, q, g, t0 + 64, end);
+    if constexpr (VEC) {
+        // Raw-buffer loads: steps past the chunk read zeros without an access,
+        // so every load issues unconditionally, two steps ahead.
+        const ReduceLanes<R, CPW> lanes = reduce_lanes<R, CPW>(a, h, cg, q, g);
+        // The first two steps' loads go out in the loop's order (a, then b),
+        // so that the wait at the top of the loop counts only step a's.
+        reduce_load_buffer<R, CPW>(tile_a, a, lanes, b, begin, end);
+        __builtin_amdgcn_sched_barrier(0);
+        reduce_load_buffer<R, CPW>(tile_b, a, lanes, b, begin + 32, end);
+        __builtin_amdgcn_sched_barrier(0);
+        // A step past the chunk's end holds zeros, and adding their zero
+        // products leaves the accumulators' bits unchanged, so both steps
+        // are reduced without a branch (a branch in the loop made the
+        // compiler wait for every load in flight at the top of the loop).
+        // Each step's operands are rotated and split first; the loads two
+        // steps ahead then go out into the freed tile registers, before the
+        // step's MFMAs, so their latency runs under those MFMAs and the next
+        // step.
+        auto step = [&](ReduceTile<R, CPW>& tile, int64_t ahead) {
+            u32x4 a_hi[NRB];
+            u32x4 a_lo[NRB];
+            u32x4 b_c[2 * CPW];
+            reduce_relation_operands<R, CPW>(tile, a_hi, a_lo);
+            reduce_content_operands<R, CPW>(tile, b_c);
+            // Pin the operands here: left alone, the compiler sinks their
+            // arithmetic to the MFMAs, past the loads below, so that the old
+            // and the new tile are live at once and the loop carries copies
+            // that wait for every load in flight.
+#pragma unroll
+            for (int x = 0; x < NRB; ++x) {
+                asm volatile("" : "+v"(a_hi[x]), "+v"(a_lo[x]));
+            }
+#pragma unroll
+            for (int c = 0; c < 2 * CPW; ++c) {
+                asm volatile("" : "+v"(b_c[c]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            reduce_load_buffer<R, CPW>(tile, a, lanes, b, ahead, end);
+            __builtin_amdgcn_sched_barrier(0);
+            if (do_gram) {
+                reduce_gram_mfma<R>(a_hi, a_lo, acc_g);
+            }
+            reduce_cross_mfma<R, CPW>(a_hi, a_lo, b_c, acc_s);
+        };
+        for (int64_t t0 = begin; t0 < end; t0 += 64) {
+            step(tile_a, t0 + 64);
+            step(tile_b, t0 + 96);
         }
-        if (t0 + 32 < end) {
-            reduce_compute<R, CPW>(tile_b, do_gram, acc_g, acc_s);
-            if (t0 + 96 < end) {
-                reduce_load<R, CPW, VEC>(tile_b, a, b, h, cg, q, g, t0 + 96, end);
+    } else {
+        reduce_load<R, CPW, VEC>(tile_a, a, b, h, cg, q, g, begin, end);
+        if (begin + 32 < end) {
+            reduce_load<R, CPW, VEC>(tile_b, a, b, h, cg, q, g, begin + 32, end);
+        }
+        for (int64_t t0 = begin; t0 < end; t0 += 64) {
+            reduce_compute<R, CPW>(tile_a, do_gram, acc_g, acc_s);
+            if (t0 + 64 < end) {
+                reduce_load<R, CPW, VEC>(tile_a, a, b, h, cg, q, g, t0 + 64, end);
+            }
+            if (t0 + 32 < end) {
+                reduce_compute<R, CPW>(tile_b, do_gram, acc_g, acc_s);
+                if (t0 + 96 < end) {
+                    reduce_load<R, CPW, VEC>(tile_b, a, b, h, cg, q, g, t0 + 96, end);
+                }
             }
         }
     }
@@ -1012,7 +1065,11 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
     using AL = ApplyLayout<R>;
     constexpr int PAIRS = R / 2;
     const int lane = threadIdx.x & 63;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    // Wave-uniform, so the work item and the buffer bases below are scalar.
+    // The waves of one (sample, chunk) read the same rows and phases: their
+    // workgroups are renumbered onto one XCD (shared L2).
+    const int64_t wave = xcd_local_block(blockIdx.x, gridDim.x) * 4 +
+                         __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (wave >= a.total_waves) {
         return;
     }
@@ -1123,6 +1180,170 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
             }
         }
     };
+
+    if constexpr (VEC) {
+        // Raw-buffer form: a step's buffers start at its first token and end
+        // at the chunk's end, so the loads of tokens past the chunk return
+        // zeros and their stores are dropped, with no branch, and the per-lane
+        // byte offsets are the same for every step (only the scalar bases
+        // move).  Loads, products and stores are those of the pointer form
+        // below.
+        const uint32_t row_bytes = 2u * static_cast<uint32_t>(a.width);
+        const uint32_t rel_lane = static_cast<uint32_t>(q) * row_bytes + 2u * static_cast<uint32_t>(h * R);
+        const uint32_t ph_lane = 4u * static_cast<uint32_t>(q * PAIRS);
+        uint32_t con_lane[NFBW];
+        uint32_t out_lane[NFBW];
+#pragma unroll
+        for (int f = 0; f < NFBW; ++f) {
+            const int64_t feature = (fbg * NFBW + f) * 16 + 4 * g;
+            const bool fv = feature < d;
+            con_lane[f] = fv ? static_cast<uint32_t>(q) * row_bytes + 2u * static_cast<uint32_t>(content_offset + feature)
+                             : kOutOfRange;
+            out_lane[f] = fv ? 2u * static_cast<uint32_t>(q * a.out_width + h * d + feature) : kOutOfRange;
+        }
+        auto rel_buffer = [&](int64_t t0) {
+            return make_buffer(a.projected + (b * a.length + t0) * a.width, 2 * (end - t0) * a.width);
+        };
+        auto load_rotation = [&](int64_t t0, StepLoads& l) {
+            const BufferRsrc rel = rel_buffer(t0);
+            const BufferRsrc ph = make_buffer(a.phases + b * a.phase_batch_stride + t0 * PAIRS, 4 * (end - t0) * PAIRS);
+#pragma unroll
+            for (int s = 0; s < AL::kSteps32; ++s) {
+                const uint32_t first_rank = 32 * s + 8 * g;
+                l.rel32[s] = buffer_load16(rel, rel_lane + 2u * first_rank);
+                l.ph32[s] = buffer_load16(ph, ph_lane + 2u * first_rank);
+            }
+#pragma unroll
+            for (int s = 0; s < AL::kSteps16; ++s) {
+                const uint32_t first_rank = 16 * s + 4 * g;
+                l.rel16[s] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rel, rel_lane + 2u * first_rank, 0, 0));
+                l.ph16[s] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ph, ph_lane + 2u * first_rank, 0, 0));
+            }
+        };
+        auto load_content = [&](int64_t t0, StepLoads& l) {
+            const BufferRsrc rel = rel_buffer(t0);
+#pragma unroll
+            for (int f = 0; f < NFBW; ++f) {
+                l.con[f] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rel, con_lane[f], 0, 0));
+            }
+        };
+        // Steps alternate between two register stages.  A step rotates and
+        // splits its relation pairs, then (their registers free) issues the
+        // loads of the stage's next step two steps ahead, then multiplies and
+        // stores, and then issues that step's content loads: every load has a
+        // whole step of work behind it before its first use.
+        auto step = [&](StepLoads& l, int64_t t0) {
+            u32x4 b_hi32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
+            u32x4 b_lo32[AL::kSteps32 > 0 ? AL::kSteps32 : 1];
+#pragma unroll
+            for (int s = 0; s < AL::kSteps32; ++s) {
+                float v[8];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    rotate_pair(l.rel32[s][p], l.ph32[s][p], v[2 * p], v[2 * p + 1]);
+                }
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    uint32_t hi, lo;
+                    split_bf16(v[2 * p], v[2 * p + 1], hi, lo);
+                    b_hi32[s][p] = hi;
+                    b_lo32[s][p] = lo;
+                }
+                // Keep the compiler from sinking this arithmetic past the
+                // loads below (the old and new stage would then be live at
+                // once and the loop would carry copies that wait for them).
+                asm volatile("" : "+v"(b_hi32[s]), "+v"(b_lo32[s]));
+            }
+            u32x2 b_hi16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
+            u32x2 b_lo16[AL::kSteps16 > 0 ? AL::kSteps16 : 1];
+#pragma unroll
+            for (int s = 0; s < AL::kSteps16; ++s) {
+                float v[4];
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    rotate_pair(l.rel16[s][p], l.ph16[s][p], v[2 * p], v[2 * p + 1]);
+                }
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    uint32_t hi, lo;
+                    split_bf16(v[2 * p], v[2 * p + 1], hi, lo);
+                    b_hi16[s][p] = hi;
+                    b_lo16[s][p] = lo;
+                }
+                asm volatile("" : "+v"(b_hi16[s]), "+v"(b_lo16[s]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_rotation(t0 + 32, l);
+            __builtin_amdgcn_sched_barrier(0);
+            const BufferRsrc out = make_buffer(a.output + (b * a.length + t0) * a.out_width,
+                                               2 * (end - t0) * a.out_width);
+            // The feature blocks' chains interleave (each keeps its own MFMA
+            // order).  A block past the head's features has zero records and
+            // an out-of-range store, so it needs no branch.
+            f32x4 acc[NFBW];
+#pragma unroll
+            for (int f = 0; f < NFBW; ++f) {
+                acc[f] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int s = 0; s < AL::kSteps32; ++s) {
+#pragma unroll
+                for (int f = 0; f < NFBW; ++f) {
+                    acc[f] = mfma16x16x32(op.hi32[f][s], b_hi32[s], acc[f]);
+                }
+#pragma unroll
+                for (int f = 0; f < NFBW; ++f) {
+                    acc[f] = mfma16x16x32(op.hi32[f][s], b_lo32[s], acc[f]);
+                }
+#pragma unroll
+                for (int f = 0; f < NFBW; ++f) {
+                    acc[f] = mfma16x16x32(op.lo32[f][s], b_hi32[s], acc[f]);
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < AL::kSteps16; ++s) {
+#pragma unroll
+                for (int f = 0; f < NFBW; ++f) {
+                    acc[f] = mfma16x16x16(op.hi16[f][s], b_hi16[s], acc[f]);
+                }
+#pragma unroll
+                for (int f = 0; f < NFBW; ++f) {
+                    acc[f] = mfma16x16x16(op.hi16[f][s], b_lo16[s], acc[f]);
+                }
+#pragma unroll
+                for (int f = 0; f < NFBW; ++f) {
+                    acc[f] = mfma16x16x16(op.lo16[f][s], b_hi16[s], acc[f]);
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < NFBW; ++f) {
+                const u32x2 c = l.con[f];
+                u32x2 y;
+                y.x = pack_bf16(fmaf(eta, bf16_lo(c.x), acc[f][0]), fmaf(eta, bf16_hi(c.x), acc[f][1]));
+                y.y = pack_bf16(fmaf(eta, bf16_lo(c.y), acc[f][2]), fmaf(eta, bf16_hi(c.y), acc[f][3]));
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, y),
+                                                      out, out_lane[f], 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_content(t0 + 32, l);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        StepLoads stage_a;
+        StepLoads stage_b;
+        load_rotation(begin, stage_a);
+        load_content(begin, stage_a);
+        __builtin_amdgcn_sched_barrier(0);
+        load_rotation(begin + 16, stage_b);
+        load_content(begin + 16, stage_b);
+        __builtin_amdgcn_sched_barrier(0);
+        // A step past the chunk loads zeros and its stores are dropped, so
+        // the loop runs whole pairs of steps without a branch.
+        for (int64_t t0 = begin; t0 < end; t0 += 32) {
+            step(stage_a, t0);
+            step(stage_b, t0 + 16);
+        }
+        return;
+    }
 
     StepLoads next;
     if constexpr (kPipelined) {

@@ -99,6 +99,80 @@ __device__ __forceinline__ void reduce_load(ReduceTile<R, CPW>& t, const ReduceA
     }
 }
 
+// Raw-buffer form of reduce_load (rows whose relation pairs and content
+// feature pairs are whole aligned dwords).  The three token streams of a
+// step get raw buffers that start at the step's first token and end at the
+// chunk's end, so tokens past the chunk read as zeros with no access and no
+// branch, and the per-lane byte offsets (token 8 g of the step, plus a
+// constant per token j) are the same for every step: only the scalar buffer
+// bases move.  An absent pair slot or feature pair gets an offset past every
+// buffer.  Loads and zeros are those of reduce_load<R, CPW, true>.
+template <int R, int CPW>
+struct ReduceLanes {
+    uint32_t rel;
+    uint32_t ph;
+    uint32_t con[CPW];
+};
+
+template <int R, int CPW>
+__device__ __forceinline__ ReduceLanes<R, CPW> reduce_lanes(const ReduceArgs& a, int64_t h, int cg, int q,
+                                                           int g) {
+    using L = ReduceLayout<R>;
+    constexpr int PS = L::kPairSlots;
+    ReduceLanes<R, CPW> o;
+    const bool pv = PS * q < L::kPairs;
+    const uint32_t row0 = 8u * static_cast<uint32_t>(g);
+    o.rel = pv ? 2u * (row0 * static_cast<uint32_t>(a.width) + static_cast<uint32_t>(h * R) +
+                       static_cast<uint32_t>(2 * PS * q))
+               : kOutOfRange;
+    o.ph = pv ? 4u * (row0 * L::kPairs + static_cast<uint32_t>(PS * q)) : kOutOfRange;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int64_t feature = 2 * (static_cast<int64_t>(cg) * 16 * CPW + 16 * c + q);
+        o.con[c] = feature < a.head_dim
+            ? 2u * (row0 * static_cast<uint32_t>(a.content_stride) +
+                    static_cast<uint32_t>(h * a.head_dim + feature))
+            : kOutOfRange;
+    }
+    return o;
+}
+
+template <int R, int CPW>
+__device__ __forceinline__ void reduce_load_buffer(ReduceTile<R, CPW>& t, const ReduceArgs& a,
+                                                   const ReduceLanes<R, CPW>& o, int64_t b, int64_t t0,
+                                                   int64_t end) {
+    using L = ReduceLayout<R>;
+    constexpr int PS = L::kPairSlots;
+    const int64_t rows = end - t0;
+    const BufferRsrc rel = make_buffer(a.projected + (b * a.length + t0) * a.width, 2 * rows * a.width);
+    const BufferRsrc ph = make_buffer(a.phases + b * a.phase_batch_stride + t0 * L::kPairs,
+                                      4 * rows * L::kPairs);
+    const BufferRsrc con = make_buffer(a.content + (b * a.length + t0) * a.content_stride,
+                                       2 * rows * a.content_stride);
+    const uint32_t rel_step = 2u * static_cast<uint32_t>(a.width);
+    const uint32_t con_step = 2u * static_cast<uint32_t>(a.content_stride);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if constexpr (PS == 2) {
+            const u32x2 r = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(rel, o.rel + j * rel_step, 0, 0));
+            const u32x2 p = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(ph, o.ph + 4u * j * L::kPairs, 0, 0));
+            t.rel[j][0] = r.x;
+            t.rel[j][1] = r.y;
+            t.ph[j][0] = p.x;
+            t.ph[j][1] = p.y;
+        } else {
+            t.rel[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rel, o.rel + j * rel_step, 0, 0);
+            t.ph[j][0] = __builtin_amdgcn_raw_buffer_load_b32(ph, o.ph + 4u * j * L::kPairs, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            t.con[j][c] = __builtin_amdgcn_raw_buffer_load_b32(con, o.con[c] + j * con_step, 0, 0);
+        }
+    }
+}
+
 // Rotated relation operands of a 32-token step, split into BF16 hi + lo;
 // the _pair form does token pair jj (tokens 2 jj and 2 jj + 1 of the lane).
 template <int R, int CPW>
