@@ -491,6 +491,28 @@ __device__ __forceinline__ f32x4 mfma_tile_f32(f32x4 acc, int k_end, LoadA a, Lo
     return acc;
 }
 
+// One M x N block product on FP32 MFMA 16 x 16 tiles (M, N, K multiples of
+// 16, 16 and 4), tiles first, first + step, ... of the result for this wave:
+// store(i, j, sum_k a(i, k) b(k, j)) with the K terms in ascending order.
+template <typename LoadA, typename LoadB, typename Store>
+__device__ __forceinline__ void block_product(int m, int n, int k_end, int first, int step, int lane,
+                                              LoadA a, LoadB b, Store store) {
+    const int r16 = lane & 15;
+    const int q4 = lane >> 4;
+    const int tiles_n = n / 16;
+    for (int tile = first; tile < (m / 16) * tiles_n; tile += step) {
+        const int i0 = 16 * (tile / tiles_n);
+        const int j0 = 16 * (tile - (tile / tiles_n) * tiles_n);
+        const f32x4 acc = mfma_tile_f32((f32x4){0.0f, 0.0f, 0.0f, 0.0f}, k_end,
+                                        [&](int k) { return a(i0 + r16, k + q4); },
+                                        [&](int k) { return b(k + q4, j0 + r16); });
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            store(i0 + 4 * q4 + mm, j0 + r16, acc[mm]);
+        }
+    }
+}
+
 // Gauss-Jordan of a rank-32 system (the in-place form of solve_kernel, same
 // factors and updates element for element) with each matrix row split over
 // the two halves of the wave: lane l holds columns 16 (l / 32) .. + 15 of row
@@ -685,7 +707,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     // so that their latency overlaps the factorization; at larger ranks the
     // registers they would hold through it cost occupancy, and they are
     // loaded where they are used.
-    constexpr bool kPrefetch = R <= 32;
+    constexpr bool kPrefetch = true;
     auto base_tile = [&](int t) {
         const int tile = wave + 4 * t < SL::kTiles ? wave + 4 * t : 0;
         const int i0 = 16 * (tile / (R / 16)) + 4 * q4;
@@ -772,7 +794,133 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
 
     // ---- Cholesky (blocked, wave 0), then L^-1 one column per lane; waves
     // 1-3 meanwhile sum the first S panel ------------------------------------
-    if (wave == 0) {
+    if constexpr (R >= 48) {
+        // Two levels from rank 48 on: with A = [[A11, A21^T], [A21, A22]] and
+        // A11 32 x 32, L11 = chol(A11) and L11^-1 (wave 0, the one-level
+        // kernels at size 32), L21 = A21 L11^-T and A22 - L21 L21^T (MFMA,
+        // all waves), L22 = chol(A22 - L21 L21^T) and L22^-1 (wave 0, while
+        // waves 1-3 form L21 L11^-1), and L^-1's lower-left block
+        // -L22^-1 (L21 L11^-1).  Two dependent chains of 32 steps and a few
+        // products instead of one chain of R steps.
+        constexpr int H1 = 32;
+        constexpr int H2 = R - H1;
+        if (wave == 0) {
+            const bool live = lane < H1;
+            float l1[H1];
+            float* s_inv_diag = s_theta + 64 + 8 * H1;
+            blocked_cholesky<H1, LD>(s_work, s_theta, s_theta + 64, s_inv_diag, lane, l1);
+            // L11^T with 1 / L_ii on the diagonal (the substitution's operand),
+            // in L^-1's space until the substitution is done.
+            wave_lds_order();
+            if (live) {
+                const float own_inv = s_inv_diag[lane];
+#pragma unroll
+                for (int j = 0; j < H1; ++j) {
+                    s_linv[j * LD + lane] = j == lane ? own_inv : l1[j];
+                }
+                if (tape != nullptr) {
+#pragma unroll
+                    for (int j = 0; j < R; j += 4) {
+                        *reinterpret_cast<f32x4*>(tape + lane * R + j) = j < H1
+                            ? (f32x4){l1[j], l1[j + 1], l1[j + 2], l1[j + 3]}
+                            : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+                }
+            }
+            wave_lds_order();
+            float x[H1];
+            lower_inverse_column<H1, LD>(s_linv, lane, x);
+            wave_lds_order();
+            if (live) {
+#pragma unroll
+                for (int i = 0; i < H1; i += 4) {
+                    *reinterpret_cast<f32x4*>(s_linvt + lane * LD + i) = (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
+                }
+#pragma unroll
+                for (int i = 0; i < H1; ++i) {
+                    s_linv[i * LD + lane] = x[i];
+                }
+            }
+        } else {
+            load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root, s_pa,
+                                                              PLD, lane, wave - 1, 3);
+        }
+        __syncthreads();
+        // L21 = A21 L11^-T (into I + K's space, free until its assembly).
+        block_product(H2, H1, H1, wave, 4, lane,
+                      [&](int i, int k) { return s_work[(H1 + i) * LD + k]; },
+                      [&](int k, int j) { return s_linvt[k * LD + j]; },
+                      [&](int i, int j, float v) { s_sys[(H1 + i) * LD + j] = v; });
+        __syncthreads();
+        // A22 - L21 L21^T, in place.
+        block_product(H2, H2, H1, wave, 4, lane,
+                      [&](int i, int k) { return s_sys[(H1 + i) * LD + k]; },
+                      [&](int k, int j) { return s_sys[(H1 + j) * LD + k]; },
+                      [&](int i, int j, float v) { s_work[(H1 + i) * LD + H1 + j] -= v; });
+        __syncthreads();
+        if (wave == 0) {
+            const bool live = lane < H2;
+            float l2[H2];
+            float* s_inv_diag = s_theta + 64 + 8 * H2;
+            blocked_cholesky<H2, LD>(s_work + H1 * LD + H1, s_theta, s_theta + 64, s_inv_diag, lane, l2);
+            wave_lds_order();
+            if (live) {
+                const float own_inv = s_inv_diag[lane];
+#pragma unroll
+                for (int j = 0; j < H2; ++j) {
+                    s_linv[(H1 + j) * LD + H1 + lane] = j == lane ? own_inv : l2[j];
+                }
+                if (tape != nullptr) {
+                    float* row = tape + (H1 + lane) * R;
+#pragma unroll
+                    for (int j = 0; j < H1; j += 4) {
+                        *reinterpret_cast<f32x4*>(row + j) = *reinterpret_cast<const f32x4*>(s_sys + (H1 + lane) * LD + j);
+                    }
+#pragma unroll
+                    for (int j = 0; j < H2; j += 4) {
+                        *reinterpret_cast<f32x4*>(row + H1 + j) = (f32x4){l2[j], l2[j + 1], l2[j + 2], l2[j + 3]};
+                    }
+                }
+            }
+            wave_lds_order();
+            float x[H2];
+            lower_inverse_column<H2, LD>(s_linv + H1 * LD + H1, lane, x);
+            wave_lds_order();
+            if (live) {
+#pragma unroll
+                for (int i = 0; i < H2; i += 4) {
+                    *reinterpret_cast<f32x4*>(s_linvt + (H1 + lane) * LD + H1 + i) =
+                        (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
+                }
+#pragma unroll
+                for (int i = 0; i < H2; ++i) {
+                    s_linv[(H1 + i) * LD + H1 + lane] = x[i];
+                }
+            }
+        } else {
+            // L21 L11^-1 into the second panel (free until the Z products).
+            block_product(H2, H1, H1, wave - 1, 3, lane,
+                          [&](int i, int k) { return s_sys[(H1 + i) * LD + k]; },
+                          [&](int k, int j) { return s_linv[k * LD + j]; },
+                          [&](int i, int j, float v) { s_pb[i * PLD + j] = v; });
+        }
+        __syncthreads();
+        // L^-1's lower-left block -L22^-1 (L21 L11^-1), with its transpose in
+        // L^-T; the upper-right blocks are zero.
+        block_product(H2, H1, H2, wave, 4, lane,
+                      [&](int i, int k) { return s_linv[(H1 + i) * LD + H1 + k]; },
+                      [&](int k, int j) { return s_pb[k * PLD + j]; },
+                      [&](int i, int j, float v) {
+                          s_linv[(H1 + i) * LD + j] = -v;
+                          s_linvt[j * LD + H1 + i] = -v;
+                      });
+        for (int e = tid; e < H1 * H2; e += kSolveThreads) {
+            const int i = e / H2;
+            const int j = e - i * H2;
+            s_linv[i * LD + H1 + j] = 0.0f;
+            s_linvt[(H1 + j) * LD + i] = 0.0f;
+        }
+    } else if (wave == 0) {
         const bool live = lane < R;
         float lrow[R];
         // Theta's LDS is free until the Theta assembly.
@@ -958,6 +1106,56 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         if (wave == 0) {
             gauss_jordan_halves<LD>(s_sys, s_sys, s_work, lane);
         }
+    } else if constexpr (R >= 48) {
+        // From rank 48 on, by blocks: with I + K = [[P, Q], [M21, T]] and P
+        // 32 x 32, P^-1 (rank-32 elimination, wave 0), W1 = P^-1 Q and
+        // W2 = M21 P^-1, the Schur complement S = T - M21 W1 and S^-1, then
+        // (I + K)^-1 = [[P^-1 + W1 S^-1 W2, -W1 S^-1], [-S^-1 W2, S^-1]].
+        // P and S inherit the positive definite symmetric part, so neither
+        // elimination needs row exchanges.  Two chains of at most 32 steps
+        // instead of one of R steps.
+        constexpr int H1 = 32;
+        constexpr int H2 = R - H1;
+        if (wave == 0) {
+            gauss_jordan_halves<LD>(s_sys, s_sys, s_work, lane);
+        }
+        __syncthreads();
+        block_product(H1, H2, H1, wave, 4, lane,
+                      [&](int i, int k) { return s_sys[i * LD + k]; },
+                      [&](int k, int j) { return s_sys[k * LD + H1 + j]; },
+                      [&](int i, int j, float v) { s_work[i * LD + j] = v; });
+        block_product(H2, H1, H1, wave, 4, lane,
+                      [&](int i, int k) { return s_sys[(H1 + i) * LD + k]; },
+                      [&](int k, int j) { return s_sys[k * LD + j]; },
+                      [&](int i, int j, float v) { s_work[(H1 + i) * LD + j] = v; });
+        __syncthreads();
+        block_product(H2, H2, H1, wave, 4, lane,
+                      [&](int i, int k) { return s_sys[(H1 + i) * LD + k]; },
+                      [&](int k, int j) { return s_work[k * LD + j]; },
+                      [&](int i, int j, float v) { s_sys[(H1 + i) * LD + H1 + j] -= v; });
+        __syncthreads();
+        // Theta's space is free once I + K is assembled.
+        if constexpr (H2 == 32) {
+            if (wave == 0) {
+                gauss_jordan_halves<LD>(s_sys + H1 * LD + H1, s_sys + H1 * LD + H1, s_theta, lane);
+            }
+        } else {
+            gauss_jordan_waves<H2, LD>(s_sys + H1 * LD + H1, s_theta, wave, lane);
+        }
+        __syncthreads();
+        block_product(H2, H1, H2, wave, 4, lane,
+                      [&](int i, int k) { return s_sys[(H1 + i) * LD + H1 + k]; },
+                      [&](int k, int j) { return s_work[(H1 + k) * LD + j]; },
+                      [&](int i, int j, float v) { s_sys[(H1 + i) * LD + j] = -v; });
+        block_product(H1, H2, H2, wave, 4, lane,
+                      [&](int i, int k) { return s_work[i * LD + k]; },
+                      [&](int k, int j) { return s_sys[(H1 + k) * LD + H1 + j]; },
+                      [&](int i, int j, float v) { s_sys[i * LD + H1 + j] = -v; });
+        __syncthreads();
+        block_product(H1, H1, H2, wave, 4, lane,
+                      [&](int i, int k) { return s_work[i * LD + k]; },
+                      [&](int k, int j) { return s_sys[(H1 + k) * LD + j]; },
+                      [&](int i, int j, float v) { s_sys[i * LD + j] -= v; });
     } else {
         gauss_jordan_waves<R, LD>(s_sys, s_work, wave, lane);
     }
