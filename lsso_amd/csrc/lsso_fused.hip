@@ -145,12 +145,17 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
                         bias[nb][qd] = *reinterpret_cast<const f32x4*>(&s_bias[n0 + 32 * nb + 8 * qd + 4 * half]);
                     }
                 }
+                // The FP32 bias is the accumulators' starting value (element
+                // 4 qd + e of block nb is feature n0 + 32 nb + 8 qd + 4 half + e).
                 f32x16 acc[2];
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        acc[nb][i] = 0.0f;
+                    for (int qd = 0; qd < 4; ++qd) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            acc[nb][4 * qd + e] = bias[nb][qd][e];
+                        }
                     }
                 }
                 const uint16_t* xrow = xt + lane_c * kMixDPitch + 8 * half;
@@ -174,17 +179,27 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
                         }
                     }
                 }
-                // Bias, row mask and rounding into this wave's output stage,
-                // then 16-byte pieces of whole rows to HBM.
+                // Row mask (only for a tile with dropped rows) and rounding
+                // into this wave's output stage, then 16-byte pieces of whole
+                // rows to HBM.
+                if (__ballot(keep) != ~0ull) {
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            acc[nb][i] = keep ? acc[nb][i] : 0.0f;
+                        }
+                    }
+                }
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
                     for (int qd = 0; qd < 4; ++qd) {
                         const int c = 32 * nb + 8 * qd + 4 * half;
-                        const float v0 = keep ? acc[nb][4 * qd + 0] + bias[nb][qd][0] : 0.0f;
-                        const float v1 = keep ? acc[nb][4 * qd + 1] + bias[nb][qd][1] : 0.0f;
-                        const float v2 = keep ? acc[nb][4 * qd + 2] + bias[nb][qd][2] : 0.0f;
-                        const float v3 = keep ? acc[nb][4 * qd + 3] + bias[nb][qd][3] : 0.0f;
+                        const float v0 = acc[nb][4 * qd + 0];
+                        const float v1 = acc[nb][4 * qd + 1];
+                        const float v2 = acc[nb][4 * qd + 2];
+                        const float v3 = acc[nb][4 * qd + 3];
                         u32x2 packed;
                         if constexpr (YT == LSSO_HIP_BF16) {
                             packed.x = pack_bf16(v0, v1);

@@ -248,12 +248,20 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
         if (next < a.tiles) {
             load_stage(next);
         }
+        // The FP32 bias is the accumulators' starting value (in the lower-K
+        // wave of a split slice): element 4 qd + e is feature
+        // slice * 32 + 8 qd + 4 half + e of the group.
         f32x16 acc[MB];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
+        for (int qd = 0; qd < 4; ++qd) {
+            const f32x4 bias = khalf == 0 ? *reinterpret_cast<const f32x4*>(&s_bias[slice * 32 + 8 * qd + 4 * half])
+                                          : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                acc[mb][i] = 0.0f;
+            for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[mb][4 * qd + e] = bias[e];
+                }
             }
         }
         // Operand reads run one group of two K steps ahead of the MFMAs, so
@@ -319,14 +327,19 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
                 break;   // wave-uniform: the upper-K waves have handed over
             }
             const int mr = mb * 32 + (lane & 31);
+            if (__ballot(keep[mb]) != ~0ull) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    acc[mb][i] = keep[mb] ? acc[mb][i] : 0.0f;
+                }
+            }
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
                 const int c = slice * 32 + 8 * qd + 4 * half;
-                const f32x4 bias = *reinterpret_cast<const f32x4*>(&s_bias[c]);
-                const float v0 = keep[mb] ? acc[mb][4 * qd + 0] + bias[0] : 0.0f;
-                const float v1 = keep[mb] ? acc[mb][4 * qd + 1] + bias[1] : 0.0f;
-                const float v2 = keep[mb] ? acc[mb][4 * qd + 2] + bias[2] : 0.0f;
-                const float v3 = keep[mb] ? acc[mb][4 * qd + 3] + bias[3] : 0.0f;
+                const float v0 = acc[mb][4 * qd + 0];
+                const float v1 = acc[mb][4 * qd + 1];
+                const float v2 = acc[mb][4 * qd + 2];
+                const float v3 = acc[mb][4 * qd + 3];
                 u32x2 packed;
                 if constexpr (YT == LSSO_HIP_BF16) {
                     packed.x = pack_bf16(v0, v1);

@@ -264,12 +264,17 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
                 constexpr int kHalfStores = kProjStores / 2;
                 constexpr int kEvery = KSTEPS / kHalfStores;
                 u32x4 piece = read_piece(yprev, mb * kHalfStores);
+                // The FP32 bias is the accumulators' starting value (element
+                // 4 qd + e of block nb is column 8 qd + 4 half + e of it).
                 f32x16 acc[2];
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        acc[nb][i] = 0.0f;
+                    for (int qd = 0; qd < 4; ++qd) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            acc[nb][4 * qd + e] = bias[nb][qd][e];
+                        }
                     }
                 }
                 // x fragments kXAhead K steps ahead of their MFMAs.
@@ -298,19 +303,25 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                // Bias, row mask and BF16 rounding into the packed tile.
+                // Row mask (only for a tile with dropped rows) and BF16
+                // rounding into the packed tile.
+                if (!all_keep) {
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            acc[nb][i] = keep ? acc[nb][i] : 0.0f;
+                        }
+                    }
+                }
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
                     for (int qd = 0; qd < 4; ++qd) {
                         const int c = wave * 64 + nb * 32 + 8 * qd + 4 * half_k;
-                        const float v0 = keep ? acc[nb][4 * qd + 0] + bias[nb][qd][0] : 0.0f;
-                        const float v1 = keep ? acc[nb][4 * qd + 1] + bias[nb][qd][1] : 0.0f;
-                        const float v2 = keep ? acc[nb][4 * qd + 2] + bias[nb][qd][2] : 0.0f;
-                        const float v3 = keep ? acc[nb][4 * qd + 3] + bias[nb][qd][3] : 0.0f;
                         u32x2 packed;
-                        packed.x = pack_bf16(v0, v1);
-                        packed.y = pack_bf16(v2, v3);
+                        packed.x = pack_bf16(acc[nb][4 * qd + 0], acc[nb][4 * qd + 1]);
+                        packed.y = pack_bf16(acc[nb][4 * qd + 2], acc[nb][4 * qd + 3]);
                         *reinterpret_cast<u32x2*>(&yt[mr * YP + c]) = packed;
                     }
                 }
