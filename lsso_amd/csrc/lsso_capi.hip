@@ -334,6 +334,10 @@ int run_reduce(const MixerPlan& plan, const MixerBuffers& buf, const void* proje
     reduce.column_groups = plan.column_groups;
     reduce.partial_stride = plan.partial_stride;
     reduce.total_waves = plan.batch * plan.heads * plan.reduce_chunks * plan.column_groups;
+    reduce.group_heads = plan.cpw == 1 ? lsso_hip::reduce_staged_group_heads(plan.rank, plan.heads, plan.head_dim,
+                                                                              plan.column_groups, reduce.content_stride,
+                                                                              vec && plan.head_dim % 8 == 0)
+                                       : 0;
     const hipError_t error =
         lsso_hip::launch_reduce(static_cast<int>(plan.rank), reduce, plan.cpw, vec, stream);
     return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "reduce_kernel launch");
@@ -859,6 +863,10 @@ int lsso_hip_mixer_backward_ex(const lsso_hip_mixer_shape* shape, const void* gr
     reduce.column_groups = plan.column_groups;
     reduce.partial_stride = plan.partial_stride;
     reduce.total_waves = plan.batch * plan.heads * plan.reduce_chunks * plan.column_groups;
+    reduce.group_heads = plan.cpw == 1 ? lsso_hip::reduce_staged_group_heads(plan.rank, plan.heads, plan.head_dim,
+                                                                              plan.column_groups, reduce.content_stride,
+                                                                              vec && plan.head_dim % 8 == 0)
+                                       : 0;
     error = lsso_hip::launch_reduce(static_cast<int>(plan.rank), reduce, plan.cpw, vec, stream);
     if (error != hipSuccess) {
         return hip_failure(error, "reduce_kernel launch (backward)");

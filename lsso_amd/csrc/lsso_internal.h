@@ -61,6 +61,7 @@ struct ReduceArgs {
     int64_t column_groups;
     int64_t partial_stride;     // rank * rank + rank * head_dim
     int64_t total_waves;
+    int64_t group_heads;        // staged form: heads per workgroup (0: one wave per work item)
 };
 
 struct SolveArgs {
@@ -265,6 +266,10 @@ struct WeightGradArgs {
 
 hipError_t launch_phase(const PhaseArgs& a, hipStream_t stream);
 hipError_t launch_reduce(int rank, const ReduceArgs& a, int cpw, bool vec, hipStream_t stream);
+// Heads per workgroup of the staged reduce for this geometry, or 0 where it
+// does not apply (the one-wave-per-item reduce_kernel runs instead).
+int64_t reduce_staged_group_heads(int64_t rank, int64_t heads, int64_t head_dim, int64_t column_groups,
+                                  int64_t content_stride, bool vec);
 hipError_t launch_solve(int rank, const SolveArgs& a, int64_t systems, hipStream_t stream);
 hipError_t launch_apply(int rank, const ApplyArgs& a, int nfbw, bool vec, hipStream_t stream);
 

@@ -178,6 +178,254 @@ __global__ __launch_bounds__(256, 2) void reduce_kernel(ReduceArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Reduce from staged row runs.  One workgroup per (sample, chunk, group of
+// heads), one wave per (head of the group, column group).  Each 32-token step
+// loads, with every thread of the workgroup, the group's relation columns and
+// content columns of the step's rows (one contiguous run of each row per
+// stream) and the step's phase rows as 16-byte pieces into LDS, so that HBM
+// serves whole runs instead of each wave's 64- and 128-byte pieces of every
+// row; each wave then reads its head's operands from LDS in the reduce_load
+// layout and runs the reduce_kernel MFMA chains in the same token order, so
+// the partials are those of reduce_kernel bit for bit.  The loads of step
+// k + 1 are in flight during step k's reductions.
+constexpr int kStagedWaves = 8;              // at most, per workgroup
+constexpr int kStagedCols = 512;             // group columns (relation + content) per row, at most
+constexpr int kStagedRelPieces = 4;          // 16-byte pieces per thread and step, at most
+constexpr int kStagedConPieces = 4;
+constexpr int kStagedPhasePieces = 2;
+
+template <int R, int CPW>
+__global__ __launch_bounds__(kStagedWaves * 64) void reduce_staged_kernel(ReduceArgs a) {
+    using L = ReduceLayout<R>;
+    constexpr int PS = L::kPairSlots;
+    constexpr int PAIRS = R / 2;
+    constexpr int NRB = L::kRowBlocks;
+    constexpr int NGB = L::kGramBlocks;
+    constexpr int PHP = PAIRS + 2;               // phase row pitch (u32)
+    __shared__ __attribute__((aligned(16))) uint16_t s_rows[2][32 * (kStagedCols + 4)];
+    __shared__ __attribute__((aligned(16))) uint32_t s_ph[2][32 * PHP];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int threads = blockDim.x;
+    const int64_t groups = (a.heads + a.group_heads - 1) / a.group_heads;
+    int64_t rest = blockIdx.x;
+    const int64_t group = rest % groups;
+    rest /= groups;
+    const int64_t chunk = rest % a.chunks;
+    const int64_t b = rest / a.chunks;
+    const int64_t h0 = group * a.group_heads;
+    const int hg = static_cast<int>(a.group_heads < a.heads - h0 ? a.group_heads : a.heads - h0);
+    const int d = static_cast<int>(a.head_dim);
+    const int cgs = static_cast<int>(a.column_groups);
+    const int unit = wave / cgs;                 // head of the group
+    const int cg = wave - unit * cgs;
+    const bool active = unit < hg;
+    const int64_t begin = chunk * a.chunk_tokens;
+    const int64_t end = begin + a.chunk_tokens < a.length ? begin + a.chunk_tokens : a.length;
+
+    // Row runs: relation columns h0 R .. (h0 + hg) R of `projected`, content
+    // columns h0 d .. (h0 + hg) d of `content`; in LDS a row holds the
+    // relation run then the content run.  The pitch keeps rows 8 apart in
+    // different banks (2 mod 8 dwords).
+    const int rel_pieces = hg * R / 8;
+    const int con_pieces = hg * d / 8;
+    const int cols = 8 * (rel_pieces + con_pieces);
+    const int pitch = ((cols + 15) / 16) * 16 + 4;
+    uint32_t rel_off[kStagedRelPieces];
+    uint32_t con_off[kStagedConPieces];
+    uint32_t ph_off[kStagedPhasePieces];
+    int rel_lds[kStagedRelPieces];
+    int con_lds[kStagedConPieces];
+    int ph_lds[kStagedPhasePieces];
+#pragma unroll
+    for (int i = 0; i < kStagedRelPieces; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / (rel_pieces > 0 ? rel_pieces : 1);
+        const int c = piece - row * rel_pieces;
+        const bool live = piece < 32 * rel_pieces;
+        rel_off[i] = live ? 2u * static_cast<uint32_t>(row * a.width + 8 * c) : kOutOfRange;
+        rel_lds[i] = live ? row * pitch + 8 * c : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kStagedConPieces; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / (con_pieces > 0 ? con_pieces : 1);
+        const int c = piece - row * con_pieces;
+        const bool live = piece < 32 * con_pieces;
+        con_off[i] = live ? 2u * static_cast<uint32_t>(row * a.content_stride + 8 * c) : kOutOfRange;
+        con_lds[i] = live ? row * pitch + 8 * (rel_pieces + c) : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kStagedPhasePieces; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / (PAIRS / 4);
+        const int c = piece - row * (PAIRS / 4);
+        const bool live = piece < 32 * (PAIRS / 4);
+        ph_off[i] = live ? 16u * static_cast<uint32_t>(piece) : kOutOfRange;
+        ph_lds[i] = live ? row * PHP + 4 * c : -1;
+    }
+    struct Stage {
+        u32x4 rel[kStagedRelPieces];
+        u32x4 con[kStagedConPieces];
+        u32x4 ph[kStagedPhasePieces];
+    };
+    auto load = [&](Stage& st, int64_t t0) {
+        const int64_t rows = end - t0;
+        const BufferRsrc rel = make_buffer(a.projected + (b * a.length + t0) * a.width + h0 * R, 2 * rows * a.width);
+        const BufferRsrc con = make_buffer(a.content + (b * a.length + t0) * a.content_stride + h0 * d,
+                                           2 * rows * a.content_stride);
+        const BufferRsrc ph = make_buffer(a.phases + b * a.phase_batch_stride + t0 * PAIRS, 4 * rows * PAIRS);
+#pragma unroll
+        for (int i = 0; i < kStagedRelPieces; ++i) {
+            st.rel[i] = buffer_load16_stream(rel, rel_off[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kStagedConPieces; ++i) {
+            st.con[i] = buffer_load16_stream(con, con_off[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kStagedPhasePieces; ++i) {
+            st.ph[i] = buffer_load16(ph, ph_off[i]);
+        }
+    };
+    auto commit = [&](const Stage& st, int buf) {
+#pragma unroll
+        for (int i = 0; i < kStagedRelPieces; ++i) {
+            if (rel_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_rows[buf][rel_lds[i]]) = st.rel[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kStagedConPieces; ++i) {
+            if (con_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_rows[buf][con_lds[i]]) = st.con[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kStagedPhasePieces; ++i) {
+            if (ph_lds[i] >= 0) {
+                uint32_t* dst = &s_ph[buf][ph_lds[i]];
+                *reinterpret_cast<u32x2*>(dst) = (u32x2){st.ph[i][0], st.ph[i][1]};
+                *reinterpret_cast<u32x2*>(dst + 2) = (u32x2){st.ph[i][2], st.ph[i][3]};
+            }
+        }
+    };
+
+    f32x4 acc_g[NGB];
+    f32x4 acc_s[NRB][2 * CPW];
+#pragma unroll
+    for (int i = 0; i < NGB; ++i) {
+        acc_g[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int x = 0; x < NRB; ++x) {
+#pragma unroll
+        for (int c = 0; c < 2 * CPW; ++c) {
+            acc_s[x][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    const int q = lane & 15;
+    const int g = lane >> 4;
+    const bool do_gram = a.gram != 0 && cg == 0;
+    // This lane's operands in a staged step (the reduce_load layout: tokens
+    // 8 g .. 8 g + 7, pair slots PS q .., feature pairs of column group cg).
+    const bool pv = PS * q < PAIRS;
+    const int rel_col = unit * R + 2 * PS * q;
+    const int con_col = 8 * rel_pieces + unit * d + 2 * (cg * 16 * CPW + q);
+    auto read_tile = [&](ReduceTile<R, CPW>& t, int buf) {
+        const uint16_t* rows = &s_rows[buf][(8 * g) * pitch];
+        const uint32_t* phs = &s_ph[buf][(8 * g) * PHP + PS * q];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            if constexpr (PS == 2) {
+                u32x2 r = {0u, 0u};
+                u32x2 p = {0u, 0u};
+                if (pv) {
+                    r = *reinterpret_cast<const u32x2*>(rows + jj * pitch + rel_col);
+                    p = *reinterpret_cast<const u32x2*>(phs + jj * PHP);
+                }
+                t.rel[jj][0] = r.x;
+                t.rel[jj][1] = r.y;
+                t.ph[jj][0] = p.x;
+                t.ph[jj][1] = p.y;
+            } else {
+                t.rel[jj][0] = pv ? *reinterpret_cast<const uint32_t*>(rows + jj * pitch + rel_col) : 0u;
+                t.ph[jj][0] = pv ? phs[jj * PHP] : 0u;
+            }
+#pragma unroll
+            for (int c = 0; c < CPW; ++c) {
+                t.con[jj][c] = 2 * (cg * 16 * CPW + 16 * c + q) < d
+                    ? *reinterpret_cast<const uint32_t*>(rows + jj * pitch + con_col + 32 * c)
+                    : 0u;
+            }
+        }
+    };
+
+    // Two register stages: the loads of step k + 2 go out at the start of
+    // step k, so each has two steps of reductions to arrive before its
+    // commit at the end of step k + 1.  Steps past the chunk load zeros
+    // without an access and reduce to an unchanged accumulator, so the loop
+    // runs whole pairs of steps.
+    auto reduce_step = [&](int buf) {
+        if (active) {
+            ReduceTile<R, CPW> t;
+            read_tile(t, buf);
+            reduce_compute<R, CPW>(t, do_gram, acc_g, acc_s);
+        }
+    };
+    Stage stage_a;
+    Stage stage_b;
+    load(stage_a, begin);
+    __builtin_amdgcn_sched_barrier(0);
+    load(stage_b, begin + 32);
+    __builtin_amdgcn_sched_barrier(0);
+    commit(stage_a, 0);
+    __syncthreads();
+    for (int64_t t0 = begin; t0 < end; t0 += 64) {
+        load(stage_a, t0 + 64);
+        reduce_step(0);
+        commit(stage_b, 1);
+        __syncthreads();
+        load(stage_b, t0 + 96);
+        reduce_step(1);
+        commit(stage_a, 0);
+        __syncthreads();
+    }
+    if (active) {
+        float* part = a.partials + ((b * a.heads + h0 + unit) * a.chunks + chunk) * a.partial_stride;
+        if (do_gram) {
+            store_gram_partial<R>(part, acc_g, q, g);
+        }
+        store_cross_partial<R, CPW>(part + R * R, acc_s, q, g, cg, a.head_dim);
+    }
+}
+
+int64_t reduce_staged_group_heads(int64_t rank, int64_t heads, int64_t head_dim, int64_t column_groups,
+                                  int64_t content_stride, bool vec) {
+    // Rows read as 16-byte pieces: relation and content runs whole pieces.
+    if (!vec || rank < 48 || head_dim % 8 != 0 || column_groups < 1 || column_groups > kStagedWaves) {
+        return 0;
+    }
+    // Up to 8 waves and kStagedCols columns per workgroup, and at most two
+    // workgroups' worth of heads (so the grid keeps at least two workgroups
+    // per sample and chunk).
+    int64_t group = kStagedWaves / column_groups;
+    while (group > 1 && group * (rank + head_dim) > kStagedCols) --group;
+    if (group * 2 > heads && heads > 1) group = (heads + 1) / 2;
+    if (group < 1) return 0;
+    // Pieces per thread within the staging registers.
+    const int64_t threads = 64 * group * column_groups;
+    if (32 * group * rank / 8 > kStagedRelPieces * threads || 32 * group * head_dim / 8 > kStagedConPieces * threads ||
+        32 * (rank / 2) / 4 > kStagedPhasePieces * threads) {
+        return 0;
+    }
+    (void)content_stride;
+    return group;
+}
+
+// ---------------------------------------------------------------------------
 // Solve: one 256-thread workgroup per (b, h) system.
 //
 //   A = G / n + I = L L^T            blocked Cholesky
@@ -1662,6 +1910,20 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
 // Launchers.
 template <int R>
 static hipError_t launch_reduce(const ReduceArgs& a, int cpw, bool vec, hipStream_t stream) {
+    if (a.group_heads > 0) {
+        const int64_t groups = (a.heads + a.group_heads - 1) / a.group_heads;
+        const dim3 staged_grid(static_cast<unsigned>(a.batch * a.chunks * groups));
+        const dim3 block(static_cast<unsigned>(64 * a.group_heads * a.column_groups));
+        // The staged form runs from rank 48 on, where one column group of
+        // 32 features per wave is the plan.
+        if constexpr (R >= 48) {
+            if (cpw == 1) {
+                dispatch(reduce_staged_kernel<R, 1>, staged_grid, block, stream, a);
+                return hipGetLastError();
+            }
+        }
+        return hipErrorInvalidValue;
+    }
     const dim3 grid(static_cast<unsigned>((a.total_waves + 3) / 4));
     if (cpw == 1) {
         if (vec) {
