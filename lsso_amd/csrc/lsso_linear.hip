@@ -184,6 +184,7 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
     const int khalf = wave / kSlices;
     const int kofs = KW * khalf;                        // first K step of this wave
     const int64_t n0 = cg * kGroupColumns + slice * 32;
+    const bool slice_live = __builtin_amdgcn_readfirstlane(n0 < a.out_features ? 1 : 0) != 0;
     const int64_t K = a.in_features;
     const int64_t N = a.out_features;
 
@@ -278,21 +279,28 @@ __global__ __launch_bounds__(linear_waves<KSTEPS>() * 64) void linear_kernel(Lin
                 }
             }
         };
-        read_group(0, 0);
+        // A slice wholly past the output width (the last column group of an
+        // output that is not a whole number of groups: 384 or 640 columns)
+        // skips its products, which would only multiply zero weights, and
+        // leaves its SIMD to the other wave; it still stages, stores and
+        // meets every barrier.
+        if (slice_live) {
+            read_group(0, 0);
 #pragma unroll
-        for (int k2 = 0; k2 < KW; k2 += kGroup) {
-            const int slot = (k2 / kGroup) & 1;
-            if (k2 + kGroup < KW) {
-                read_group(slot ^ 1, k2 + kGroup);
-            }
-#pragma unroll
-            for (int ks = 0; ks < kGroup; ++ks) {
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    acc[mb] = mfma32x32x16(wreg[k2 + ks], xb[slot][ks][mb], acc[mb]);
+            for (int k2 = 0; k2 < KW; k2 += kGroup) {
+                const int slot = (k2 / kGroup) & 1;
+                if (k2 + kGroup < KW) {
+                    read_group(slot ^ 1, k2 + kGroup);
                 }
+#pragma unroll
+                for (int ks = 0; ks < kGroup; ++ks) {
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) {
+                        acc[mb] = mfma32x32x16(wreg[k2 + ks], xb[slot][ks][mb], acc[mb]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (KSPLIT == 2) {
             // The upper-K waves hand their accumulators to the lower-K waves
