@@ -54,8 +54,11 @@ int mix_project_tile_rows() { return kMixRows; }
 
 // HPW: heads per apply wave (1 for H <= 4, else 2); DEPTH: row tiles staged
 // in registers ahead of the one being applied (1 or 2); WMAX: the packed row
-// tier (512 or 640 columns); MIXED: also store the mixed tiles (a.mixed).
-template <int R, int NFB, int YT, int DEPTH, int HPW, int WMAX, bool MIXED>
+// tier (512 or 640 columns); MIXED: also store the mixed tiles (a.mixed);
+// MASKED: a row mask is given (a.row_mask).  Without one no mask byte is
+// loaded: its load, carried from step to step, made the compiler wait at
+// the end of every step for all the loads in flight.
+template <int R, int NFB, int YT, int DEPTH, int HPW, int WMAX, bool MIXED, bool MASKED>
 __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs a) {
     using AL = ApplyLayout<R>;
     constexpr int kMixPitch = mix_pitch<WMAX>();
@@ -307,9 +310,10 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
         const BufferRsrc ph = make_buffer(sample_phases + static_cast<int64_t>(t0) * PAIRS,
                                           int64_t{4} * rows * PAIRS);
         st.phase = buffer_load16(ph, phase_lds >= 0 ? 16u * static_cast<uint32_t>(io) : kOutOfRange);
-        const BufferRsrc mbuf = make_buffer(a.row_mask + (a.row_mask != nullptr ? b * a.length + t0 : 0),
-                                            a.row_mask != nullptr ? rows : 0);
-        st.mask = buffer_load_byte(mbuf, static_cast<uint32_t>(io < kMixRows ? io : kMixRows));
+        if constexpr (MASKED) {
+            const BufferRsrc mbuf = make_buffer(a.row_mask + b * a.length + t0, rows);
+            st.mask = buffer_load_byte(mbuf, static_cast<uint32_t>(io < kMixRows ? io : kMixRows));
+        }
     };
     auto commit = [&](const Stage& st, int t) {
         uint16_t* pk = s_pk[t & 1];
@@ -323,7 +327,7 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
             *reinterpret_cast<u32x4*>(s_ph[t & 1] + phase_lds) = st.phase;
         }
         if (io < kMixRows) {
-            s_keep[t % 3][io] = io < tile_rows(t) && (a.row_mask == nullptr || st.mask != 0);
+            s_keep[t % 3][io] = io < tile_rows(t) && (!MASKED || st.mask != 0);
         }
     };
 
@@ -448,9 +452,8 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
     Stage stage_b;
     fetch(stage_a, 0);
     if constexpr (DEPTH == 2) {
-        if (n_tiles > 1) {
-            fetch(stage_b, 1);
-        }
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(stage_b, 1);
     }
     commit(stage_a, 0);
     __syncthreads();   // bias, zero padding and tile 0's rows are in LDS
@@ -458,11 +461,14 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
         // Tile t's rows are staged in stage_a (t even) or stage_b (t odd);
         // the loop body covers an even and an odd tile so that the stages
         // keep fixed registers.
+        // The fetch two tiles ahead is issued even past the range (its
+        // buffers are then empty: zeros, no access): a fetch under a branch
+        // made the compiler wait at the next commit for every load in
+        // flight, this step's fetch included, which undid the second stage.
         auto step = [&](int k, Stage& refill, const Stage& next) {
             if (k < n_tiles) {
-                if (k + 2 < n_tiles) {
-                    fetch(refill, k + 2);
-                }
+                fetch(refill, k + 2);
+                __builtin_amdgcn_sched_barrier(0);
                 apply_tile(k);
                 if (k + 1 < n_tiles) {
                     commit(next, k + 1);
@@ -479,9 +485,7 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
     } else {
         for (int k = 0; k <= n_tiles; ++k) {
             if (k < n_tiles) {
-                if (k + 1 < n_tiles) {
-                    fetch(stage_a, k + 1);
-                }
+                fetch(stage_a, k + 1);
                 apply_tile(k);
                 if (k + 1 < n_tiles) {
                     commit(stage_a, k + 1);
@@ -497,14 +501,24 @@ __global__ __launch_bounds__(kMixThreads) void mix_project_kernel(MixProjectArgs
 template <int R, int NFB, int HPW, int WMAX>
 constexpr int mix_depth() { return HPW * NFB * ((R + 31) / 32) <= 4 && WMAX <= 512 ? 2 : 1; }
 
-template <int R, int NFB, int HPW, int WMAX, bool MIXED>
-static void launch_mix_project_m(const MixProjectArgs& a, int y_dtype, dim3 grid, hipStream_t stream) {
+template <int R, int NFB, int HPW, int WMAX, bool MIXED, bool MASKED>
+static void launch_mix_project_mm(const MixProjectArgs& a, int y_dtype, dim3 grid, hipStream_t stream) {
     constexpr int kDepth = mix_depth<R, NFB, HPW, WMAX>();
     if (y_dtype == LSSO_HIP_F16) {
-        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_F16, kDepth, HPW, WMAX, MIXED>, grid, kMixThreads, stream, a);
+        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_F16, kDepth, HPW, WMAX, MIXED, MASKED>, grid, kMixThreads,
+                 stream, a);
     } else {
-        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_BF16, kDepth, HPW, WMAX, MIXED>, grid, kMixThreads, stream,
-                 a);
+        dispatch(mix_project_kernel<R, NFB, LSSO_HIP_BF16, kDepth, HPW, WMAX, MIXED, MASKED>, grid, kMixThreads,
+                 stream, a);
+    }
+}
+
+template <int R, int NFB, int HPW, int WMAX, bool MIXED>
+static void launch_mix_project_m(const MixProjectArgs& a, int y_dtype, dim3 grid, hipStream_t stream) {
+    if (a.row_mask != nullptr) {
+        launch_mix_project_mm<R, NFB, HPW, WMAX, MIXED, true>(a, y_dtype, grid, stream);
+    } else {
+        launch_mix_project_mm<R, NFB, HPW, WMAX, MIXED, false>(a, y_dtype, grid, stream);
     }
 }
 
