@@ -48,6 +48,7 @@ size_t align_up(size_t value) { return (value + 255) & ~static_cast<size_t>(255)
 // still give 128 chunks, about one per compute unit and head group.
 constexpr int64_t kReduceChunkTokens = 512;
 constexpr int64_t kApplyTargetWaves = 4096;
+constexpr int64_t kApplyStagedTargetGroups = 512;   // workgroups of the staged apply
 
 // From 4,096 tokens on, chunks of 1,024 tokens halve the partials the
 // reductions write and the solve reads (8.4 MB each at C3) and still leave
@@ -364,6 +365,16 @@ int run_apply(const MixerPlan& plan, const MixerBuffers& buf, const void* projec
     apply.feature_blocks = plan.feature_blocks;
     apply.block_groups = plan.block_groups;
     apply.total_waves = plan.batch * plan.heads * plan.apply_chunks * plan.block_groups;
+    // From rank 48 on the apply stages whole row runs per group of heads:
+    // about two workgroups per CU, whole 32-token pairs of steps per range.
+    apply.group_heads = lsso_hip::apply_staged_group_heads(plan.rank, plan.heads, plan.head_dim, plan.nfbw,
+                                                           vec && plan.head_dim % 8 == 0);
+    if (apply.group_heads > 0) {
+        const int64_t groups = ceil_div(plan.heads, apply.group_heads);
+        apply.ranges = std::max<int64_t>(1, ceil_div(kApplyStagedTargetGroups, plan.batch * groups));
+        apply.range_tokens = ceil_div(ceil_div(plan.length, apply.ranges), 32) * 32;
+        apply.ranges = ceil_div(plan.length, apply.range_tokens);
+    }
     const hipError_t error =
         lsso_hip::launch_apply(static_cast<int>(plan.rank), apply, plan.nfbw, vec, stream);
     return error == hipSuccess ? LSSO_HIP_OK : hip_failure(error, "apply_kernel launch");

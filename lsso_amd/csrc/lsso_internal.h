@@ -100,6 +100,9 @@ struct ApplyArgs {
     int64_t feature_blocks;     // ceil(head_dim / 16)
     int64_t block_groups;       // ceil(feature_blocks / NFBW)
     int64_t total_waves;
+    int64_t group_heads;        // staged form: heads per workgroup (0: one wave per work item)
+    int64_t ranges;             // staged form: token ranges per sample
+    int64_t range_tokens;       // staged form: tokens per range (a multiple of 16)
 };
 
 // Apply fused with the output projection: y = cast(bf16(mixed) bf16(W_o)^T
@@ -272,6 +275,9 @@ int64_t reduce_staged_group_heads(int64_t rank, int64_t heads, int64_t head_dim,
                                   int64_t content_stride, bool vec);
 hipError_t launch_solve(int rank, const SolveArgs& a, int64_t systems, hipStream_t stream);
 hipError_t launch_apply(int rank, const ApplyArgs& a, int nfbw, bool vec, hipStream_t stream);
+// Heads per workgroup of the staged apply for this geometry, or 0 where it
+// does not apply.
+int64_t apply_staged_group_heads(int64_t rank, int64_t heads, int64_t head_dim, int nfbw, bool vec);
 
 // Projection launcher; k_steps = ceil(in_features / 16) rounded to a
 // compiled tier.  Returns hipErrorInvalidValue for an unsupported tier.

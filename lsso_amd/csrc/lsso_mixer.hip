@@ -1907,6 +1907,331 @@ __global__ __launch_bounds__(256) void apply_kernel(ApplyArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Apply from staged row runs (the reduce's staging, for the readout).  One
+// workgroup per (sample, token range, group of heads), one wave per head of
+// the group covering its NFB feature blocks.  Each 16-token step's relation
+// and content runs and phase rows are loaded by every thread of the
+// workgroup as 16-byte pieces two steps ahead and committed to LDS; each wave
+// reads its head's operands from LDS in the apply layout and runs the
+// apply_kernel products (same records, MFMA order and rounding, so the same
+// bits); the mixed rows of the group go out through an LDS tile as 16-byte
+// pieces of one contiguous run per row.
+constexpr int kApplyStagedWaves = 4;
+constexpr int kApplyStagedCols = 512;        // group relation + content columns, at most
+constexpr int kApplyStagedOut = 256;         // group output columns, at most
+constexpr int kApplyStagedRel = 2;           // 16-byte pieces per thread and step, at most:
+constexpr int kApplyStagedCon = 2;           //   relation, content and phase pieces,
+constexpr int kApplyStagedPh = 2;
+constexpr int kApplyStagedOutPieces = 2;     //   and stored mixed pieces
+
+template <int R, int NFB>
+__global__ __launch_bounds__(kApplyStagedWaves * 64) void apply_staged_kernel(ApplyArgs a) {
+    using AL = ApplyLayout<R>;
+    constexpr int PAIRS = R / 2;
+    constexpr int PHP = PAIRS + 4;               // phase row pitch (u32)
+    constexpr int S32 = AL::kSteps32 > 0 ? AL::kSteps32 : 1;
+    constexpr int S16 = AL::kSteps16 > 0 ? AL::kSteps16 : 1;
+    __shared__ __attribute__((aligned(16))) uint16_t s_rows[2][16 * (kApplyStagedCols + 8)];
+    __shared__ __attribute__((aligned(16))) uint32_t s_ph[2][16 * PHP];
+    __shared__ __attribute__((aligned(16))) uint16_t s_out[2][16 * (kApplyStagedOut + 8)];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int threads = blockDim.x;
+    const int64_t groups = (a.heads + a.group_heads - 1) / a.group_heads;
+    int64_t rest = blockIdx.x;
+    const int64_t group = rest % groups;
+    rest /= groups;
+    const int64_t range = rest % a.ranges;
+    const int64_t b = rest / a.ranges;
+    const int64_t h0 = group * a.group_heads;
+    const int hg = static_cast<int>(a.group_heads < a.heads - h0 ? a.group_heads : a.heads - h0);
+    const int d = static_cast<int>(a.head_dim);
+    const int unit = wave;
+    const bool active = unit < hg;
+    const int64_t h = h0 + (active ? unit : 0);
+    const int64_t begin = range * a.range_tokens;
+    const int64_t end = begin + a.range_tokens < a.length ? begin + a.range_tokens : a.length;
+    if (begin >= end) {
+        return;   // uniform over the workgroup
+    }
+    const int q = lane & 15;
+    const int g = lane >> 4;
+    const float eta = bounded_complement(a.eta_raw[h]);
+
+    // This head's operand records (as apply_kernel; blocks past the head's
+    // features read zeros).
+    u32x4 op_hi32[NFB][S32];
+    u32x4 op_lo32[NFB][S32];
+    u32x2 op_hi16[NFB][S16];
+    u32x2 op_lo16[NFB][S16];
+    {
+        const int64_t system = b * a.heads + h;
+#pragma unroll
+        for (int f = 0; f < NFB; ++f) {
+            const bool live = f < a.feature_blocks;
+            const uint16_t* record =
+                a.mop + ((system * a.feature_blocks + (live ? f : 0)) * 64 + lane) * AL::kLaneHalfs;
+#pragma unroll
+            for (int s = 0; s < AL::kSteps32; ++s) {
+                op_hi32[f][s] = live ? *reinterpret_cast<const u32x4*>(record + AL::offset32(s)) : (u32x4){0u, 0u, 0u, 0u};
+                op_lo32[f][s] = live ? *reinterpret_cast<const u32x4*>(record + AL::offset32(s) + 8) : (u32x4){0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int s = 0; s < AL::kSteps16; ++s) {
+                op_hi16[f][s] = live ? *reinterpret_cast<const u32x2*>(record + AL::offset16(s)) : (u32x2){0u, 0u};
+                op_lo16[f][s] = live ? *reinterpret_cast<const u32x2*>(record + AL::offset16(s) + 4) : (u32x2){0u, 0u};
+            }
+        }
+    }
+
+    // Staged pieces of a step: the relation run and the content run of
+    // each of its 16 rows, and its phase rows (16-byte pieces, at most
+    // kApplyStagedRel / Con / Ph per thread).
+    const int rel_pieces = hg * R / 8;
+    const int con_pieces = hg * d / 8;
+    const int pitch = ((8 * (rel_pieces + con_pieces) + 15) / 16) * 16 + 8;
+    const int out_pieces = hg * d / 8;
+    const int out_pitch = ((8 * out_pieces + 15) / 16) * 16 + 8;
+    uint32_t rel_off[kApplyStagedRel];
+    uint32_t con_off[kApplyStagedCon];
+    uint32_t ph_off[kApplyStagedPh];
+    int rel_lds[kApplyStagedRel];
+    int con_lds[kApplyStagedCon];
+    int ph_lds[kApplyStagedPh];
+#pragma unroll
+    for (int i = 0; i < kApplyStagedRel; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / rel_pieces;
+        const int c = piece - row * rel_pieces;
+        const bool live = piece < 16 * rel_pieces;
+        rel_off[i] = live ? 2u * static_cast<uint32_t>(row * a.width + 8 * c) : kOutOfRange;
+        rel_lds[i] = live ? row * pitch + 8 * c : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kApplyStagedCon; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / con_pieces;
+        const int c = piece - row * con_pieces;
+        const bool live = piece < 16 * con_pieces;
+        con_off[i] = live ? 2u * static_cast<uint32_t>(row * a.width + 8 * c) : kOutOfRange;
+        con_lds[i] = live ? row * pitch + 8 * (rel_pieces + c) : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kApplyStagedPh; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / (PAIRS / 4);
+        const int c = piece - row * (PAIRS / 4);
+        const bool live = piece < 16 * (PAIRS / 4);
+        ph_off[i] = live ? 16u * static_cast<uint32_t>(piece) : kOutOfRange;
+        ph_lds[i] = live ? row * PHP + 4 * c : -1;
+    }
+    struct Stage {
+        u32x4 rel[kApplyStagedRel];
+        u32x4 con[kApplyStagedCon];
+        u32x4 ph[kApplyStagedPh];
+    };
+    auto load = [&](Stage& st, int64_t t0) {
+        const int64_t rows = end - t0;
+        const uint16_t* row0 = a.projected + (b * a.length + t0) * a.width;
+        const BufferRsrc rel = make_buffer(row0 + h0 * R, 2 * rows * a.width);
+        const BufferRsrc con = make_buffer(row0 + a.heads * R + h0 * d, 2 * rows * a.width);
+        const BufferRsrc ph = make_buffer(a.phases + b * a.phase_batch_stride + t0 * PAIRS, 4 * rows * PAIRS);
+#pragma unroll
+        for (int i = 0; i < kApplyStagedRel; ++i) {
+            st.rel[i] = buffer_load16_stream(rel, rel_off[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kApplyStagedCon; ++i) {
+            st.con[i] = buffer_load16_stream(con, con_off[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kApplyStagedPh; ++i) {
+            st.ph[i] = buffer_load16(ph, ph_off[i]);
+        }
+    };
+    auto commit = [&](const Stage& st, int buf) {
+#pragma unroll
+        for (int i = 0; i < kApplyStagedRel; ++i) {
+            if (rel_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_rows[buf][rel_lds[i]]) = st.rel[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kApplyStagedCon; ++i) {
+            if (con_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_rows[buf][con_lds[i]]) = st.con[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kApplyStagedPh; ++i) {
+            if (ph_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_ph[buf][ph_lds[i]]) = st.ph[i];
+            }
+        }
+    };
+    // Output pieces of this thread: row, run column.
+    uint32_t out_off[kApplyStagedOutPieces];
+    int out_lds[kApplyStagedOutPieces];
+#pragma unroll
+    for (int i = 0; i < kApplyStagedOutPieces; ++i) {
+        const int piece = tid + i * threads;
+        const bool live = piece < 16 * out_pieces;
+        const int row = piece / (out_pieces > 0 ? out_pieces : 1);
+        const int c = piece - row * out_pieces;
+        out_off[i] = live ? 2u * static_cast<uint32_t>(row * a.out_width + 8 * c) : kOutOfRange;
+        out_lds[i] = live ? row * out_pitch + 8 * c : 0;
+    }
+
+    const int rel_col = unit * R;
+    const int con_col = 8 * rel_pieces + unit * d;
+    auto compute = [&](int buf, int obuf) {
+        if (!active) {
+            return;
+        }
+        const uint16_t* prow = &s_rows[buf][q * pitch];
+        const uint32_t* phrow = &s_ph[buf][q * PHP];
+        u32x4 b_hi32[S32];
+        u32x4 b_lo32[S32];
+#pragma unroll
+        for (int s = 0; s < AL::kSteps32; ++s) {
+            const int first_rank = 32 * s + 8 * g;
+            const u32x4 rel = *reinterpret_cast<const u32x4*>(prow + rel_col + first_rank);
+            const u32x4 ph = *reinterpret_cast<const u32x4*>(phrow + first_rank / 2);
+            float v[8];
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+                rotate_pair(rel[pp], ph[pp], v[2 * pp], v[2 * pp + 1]);
+            }
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+                uint32_t hi, lo;
+                split_bf16(v[2 * pp], v[2 * pp + 1], hi, lo);
+                b_hi32[s][pp] = hi;
+                b_lo32[s][pp] = lo;
+            }
+        }
+        u32x2 b_hi16[S16];
+        u32x2 b_lo16[S16];
+#pragma unroll
+        for (int s = 0; s < AL::kSteps16; ++s) {
+            const int first_rank = 16 * s + 4 * g;
+            const u32x2 rel = *reinterpret_cast<const u32x2*>(prow + rel_col + first_rank);
+            const u32x2 ph = *reinterpret_cast<const u32x2*>(phrow + first_rank / 2);
+            float v[4];
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                rotate_pair(rel[pp], ph[pp], v[2 * pp], v[2 * pp + 1]);
+            }
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                uint32_t hi, lo;
+                split_bf16(v[2 * pp], v[2 * pp + 1], hi, lo);
+                b_hi16[s][pp] = hi;
+                b_lo16[s][pp] = lo;
+            }
+        }
+        f32x4 acc[NFB];
+#pragma unroll
+        for (int f = 0; f < NFB; ++f) {
+            acc[f] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int s = 0; s < AL::kSteps32; ++s) {
+#pragma unroll
+            for (int f = 0; f < NFB; ++f) {
+                acc[f] = mfma16x16x32(op_hi32[f][s], b_hi32[s], acc[f]);
+            }
+#pragma unroll
+            for (int f = 0; f < NFB; ++f) {
+                acc[f] = mfma16x16x32(op_hi32[f][s], b_lo32[s], acc[f]);
+            }
+#pragma unroll
+            for (int f = 0; f < NFB; ++f) {
+                acc[f] = mfma16x16x32(op_lo32[f][s], b_hi32[s], acc[f]);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < AL::kSteps16; ++s) {
+#pragma unroll
+            for (int f = 0; f < NFB; ++f) {
+                acc[f] = mfma16x16x16(op_hi16[f][s], b_hi16[s], acc[f]);
+            }
+#pragma unroll
+            for (int f = 0; f < NFB; ++f) {
+                acc[f] = mfma16x16x16(op_hi16[f][s], b_lo16[s], acc[f]);
+            }
+#pragma unroll
+            for (int f = 0; f < NFB; ++f) {
+                acc[f] = mfma16x16x16(op_lo16[f][s], b_hi16[s], acc[f]);
+            }
+        }
+        uint16_t* orow = &s_out[obuf][q * out_pitch + unit * d];
+#pragma unroll
+        for (int f = 0; f < NFB; ++f) {
+            const int feature = 16 * f + 4 * g;
+            if (feature < d) {
+                const u32x2 c = *reinterpret_cast<const u32x2*>(prow + con_col + feature);
+                u32x2 y;
+                y.x = pack_bf16(fmaf(eta, bf16_lo(c.x), acc[f][0]), fmaf(eta, bf16_hi(c.x), acc[f][1]));
+                y.y = pack_bf16(fmaf(eta, bf16_lo(c.y), acc[f][2]), fmaf(eta, bf16_hi(c.y), acc[f][3]));
+                *reinterpret_cast<u32x2*>(orow + feature) = y;
+            }
+        }
+    };
+    auto store = [&](int obuf, int64_t t0) {
+        const BufferRsrc out = make_buffer(a.output + (b * a.length + t0) * a.out_width + h0 * d,
+                                           2 * (end - t0) * a.out_width);
+#pragma unroll
+        for (int i = 0; i < kApplyStagedOutPieces; ++i) {
+            buffer_store16(*reinterpret_cast<const u32x4*>(&s_out[obuf][out_lds[i]]), out, out_off[i]);
+        }
+    };
+
+    // Two register stages (loads two steps ahead), two row buffers and two
+    // output tiles: one barrier per step.  Steps past the range load zeros
+    // and store nothing.
+    Stage stage_a;
+    Stage stage_b;
+    load(stage_a, begin);
+    __builtin_amdgcn_sched_barrier(0);
+    load(stage_b, begin + 16);
+    __builtin_amdgcn_sched_barrier(0);
+    commit(stage_a, 0);
+    __syncthreads();
+    for (int64_t t0 = begin; t0 < end; t0 += 32) {
+        load(stage_a, t0 + 32);
+        compute(0, 0);
+        commit(stage_b, 1);
+        __syncthreads();
+        store(0, t0);
+        load(stage_b, t0 + 48);
+        compute(1, 1);
+        commit(stage_a, 0);
+        __syncthreads();
+        store(1, t0 + 16);
+    }
+}
+
+int64_t apply_staged_group_heads(int64_t rank, int64_t heads, int64_t head_dim, int nfbw, bool vec) {
+    if (!vec || rank < 48 || head_dim % 8 != 0 || (head_dim + 15) / 16 > nfbw) {
+        return 0;
+    }
+    int64_t group = kApplyStagedWaves;
+    while (group > 1 && (group * (rank + head_dim) > kApplyStagedCols || group * head_dim > kApplyStagedOut)) {
+        --group;
+    }
+    if (group * 2 > heads && heads > 1) group = (heads + 1) / 2;
+    const int64_t threads = 64 * group;
+    if (16 * group * rank / 8 > kApplyStagedRel * threads || 16 * group * head_dim / 8 > kApplyStagedCon * threads ||
+        16 * (rank / 2) / 4 > kApplyStagedPh * threads || 16 * group * head_dim / 8 > kApplyStagedOutPieces * threads) {
+        return 0;
+    }
+    return group;
+}
+
+// ---------------------------------------------------------------------------
 // Launchers.
 template <int R>
 static hipError_t launch_reduce(const ReduceArgs& a, int cpw, bool vec, hipStream_t stream) {
@@ -1943,6 +2268,20 @@ static hipError_t launch_reduce(const ReduceArgs& a, int cpw, bool vec, hipStrea
 
 template <int R>
 static hipError_t launch_apply(const ApplyArgs& a, int nfbw, bool vec, hipStream_t stream) {
+    if (a.group_heads > 0) {
+        const int64_t groups = (a.heads + a.group_heads - 1) / a.group_heads;
+        const dim3 staged_grid(static_cast<unsigned>(a.batch * a.ranges * groups));
+        const dim3 block(static_cast<unsigned>(64 * a.group_heads));
+        if constexpr (R >= 48) {
+            switch (nfbw) {
+                case 1: dispatch(apply_staged_kernel<R, 1>, staged_grid, block, stream, a); break;
+                case 2: dispatch(apply_staged_kernel<R, 2>, staged_grid, block, stream, a); break;
+                default: dispatch(apply_staged_kernel<R, 4>, staged_grid, block, stream, a); break;
+            }
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    }
     const dim3 grid(static_cast<unsigned>((a.total_waves + 3) / 4));
     switch (nfbw) {
         case 1:
