@@ -190,9 +190,9 @@ __global__ __launch_bounds__(256, 2) void reduce_kernel(ReduceArgs a) {
 // k + 1 are in flight during step k's reductions.
 constexpr int kStagedWaves = 8;              // at most, per workgroup
 constexpr int kStagedCols = 512;             // group columns (relation + content) per row, at most
-constexpr int kStagedRelPieces = 4;          // 16-byte pieces per thread and step, at most
-constexpr int kStagedConPieces = 4;
-constexpr int kStagedPhasePieces = 2;
+constexpr int kStagedRelPieces = 3;          // 16-byte pieces per thread and step, at most
+constexpr int kStagedConPieces = 2;
+constexpr int kStagedPhasePieces = 1;
 
 template <int R, int CPW>
 __global__ __launch_bounds__(kStagedWaves * 64) void reduce_staged_kernel(ReduceArgs a) {
