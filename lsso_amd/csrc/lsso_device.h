@@ -89,6 +89,9 @@ __device__ __forceinline__ void buffer_store16(u32x4 value, BufferRsrc buffer, u
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, value),
                                            buffer, offset, 0, 0);
 }
+__device__ __forceinline__ void buffer_store_f32(float value, BufferRsrc buffer, uint32_t offset) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(value), buffer, offset, 0, 0);
+}
 // Streaming forms: the cache-policy operand 2 sets the instruction's `nt`
 // bit, so the lines are kept in the caches as streaming (first to be
 // evicted).  Used for the bulk token tensors a kernel touches once, so

@@ -460,8 +460,9 @@ struct SolveLayout {
     static constexpr int kTheta = kLinvT + R * kLD;       // Theta
     static constexpr int kWork = kTheta + R * kLD;        // A; F; the rank-32 pivot-row buffer
     static constexpr int kSys = kWork + R * kLD;          // I + K, then (I + K)^-1
-    static constexpr int kPanelA = kSys + R * kLD;        // S panel; drive panel; X panel
-    static constexpr int kPanelB = kPanelA + R * kPLD;    // Z panel; M' panel
+    static constexpr int kPanelA = kSys + R * kLD;        // S^T panel; W^T panel; X^T panel
+    static constexpr int kPanelASize = R * kPLD > kSolvePanel * kLD ? R * kPLD : kSolvePanel * kLD;
+    static constexpr int kPanelB = kPanelA + kPanelASize; // Z panel; M' panel
     static constexpr int kTotal = kPanelB + R * kPLD;
 };
 
@@ -682,11 +683,11 @@ __device__ __forceinline__ void lower_inverse_column(const float* lt, int lane, 
 
 // Rows first, first + step, ... (< R) of columns c0 .. c0 + width of
 // S / sqrt(n), S = the cross-moment partials summed over chunks in ascending
-// order, into an LDS panel (row stride pld), one column per lane; columns
-// past the width store zero.  ROWS >= the rows per caller wave.
+// order, into an LDS panel holding S^T (row c at c * pitch), one column per
+// lane; columns past the width store zero.  ROWS >= the rows per caller wave.
 template <int R, int ROWS, int BATCH>
 __device__ __forceinline__ void load_cross_panel(const float* part, int64_t stride, int chunks, int d, int c0,
-                                                 int width, float root, float* panel, int pld, int lane,
+                                                 int width, float root, float* panel, int pitch, int lane,
                                                  int first, int step) {
     const int c = lane < width ? lane : width - 1;
     float acc[ROWS];
@@ -721,43 +722,116 @@ __device__ __forceinline__ void load_cross_panel(const float* part, int64_t stri
     for (int t = 0; t < ROWS; ++t) {
         const int i = first + step * t;
         if (i < R) {
-            panel[i * pld + lane] = lane < width ? acc[t] / root : 0.0f;
+            panel[lane * pitch + i] = lane < width ? acc[t] / root : 0.0f;
         }
     }
 }
 
-// acc + one 16 x 16 tile of A B on v_mfma_f32_16x16x4_f32, k over [0, k_end)
-// in steps of 4: lane (r, q) = (lane % 16, lane / 16) supplies A[r][k + q]
-// through a(k) and B[k + q][r] through b(k); element m of the result is row
-// 4 q + m, column r of the tile.  Each operand element is read once per
-// tile (a wave-uniform LDS read would return it to all 64 lanes).
-template <typename LoadA, typename LoadB>
-__device__ __forceinline__ f32x4 mfma_tile_f32(f32x4 acc, int k_end, LoadA a, LoadB b) {
-    for (int k = 0; k < k_end; k += 4) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a(k), b(k), acc, 0, 0, 0);
-    }
-    return acc;
-}
-
-// One M x N block product on FP32 MFMA 16 x 16 tiles (M, N, K multiples of
-// 16, 16 and 4), tiles first, first + step, ... of the result for this wave:
-// store(i, j, sum_k a(i, k) b(k, j)) with the K terms in ascending order.
-template <typename LoadA, typename LoadB, typename Store>
-__device__ __forceinline__ void block_product(int m, int n, int k_end, int first, int step, int lane,
-                                              LoadA a, LoadB b, Store store) {
-    const int r16 = lane & 15;
-    const int q4 = lane >> 4;
-    const int tiles_n = n / 16;
-    for (int tile = first; tile < (m / 16) * tiles_n; tile += step) {
-        const int i0 = 16 * (tile / tiles_n);
-        const int j0 = 16 * (tile - (tile / tiles_n) * tiles_n);
-        const f32x4 acc = mfma_tile_f32((f32x4){0.0f, 0.0f, 0.0f, 0.0f}, k_end,
-                                        [&](int k) { return a(i0 + r16, k + q4); },
-                                        [&](int k) { return b(k + q4, j0 + r16); });
+// Tiles first, first + STEP, ... (< TILES, NT tiles per block row) of a
+// product on v_mfma_f32_16x16x4_f32 with K terms (a multiple of 16), in
+// blocks of 16 terms: lane (r, q) = (lane % 16, lane / 16) reads
+// A(i0 + r, k .. k + 3) through a4(i, k) and B(k .. k + 3, j0 + r) through
+// b4(j, k), k = 16 blk + 4 q, and the block's four MFMAs take element s of
+// both, so step s sums terms 16 blk + s + {0, 4, 8, 12}.  Every call sums a
+// tile's terms in this same order.  One 16-byte read per operand and block
+// (from a row-major A and a B stored transposed; a B that is only stored
+// row-major is read as four words from rows 4 apart, which fall in different
+// LDS banks): reading a word per MFMA from rows 1 apart left a 64 x 64 x 64
+// product at more than twice its MFMA time, bound by LDS bank conflicts.
+// Each block's operands are read one block (four MFMAs) before use, across
+// tile boundaries; two tiles' accumulators alternate when the wave has an
+// even number of tiles.  init(t) is the starting accumulator of the wave's
+// t-th tile and store(t, i, j, acc) takes the lane's part of its result,
+// rows i .. i + 3 of column j; the stores run after the wave's last MFMA
+// (an epilogue between tiles leaves the matrix pipe idle while it waits on
+// its own LDS reads).  A tile index past TILES computes on tile 0's operands
+// and is not stored.  Operands must not overlap the results of the same
+// call.
+template <int TILES, int NT, int K, int STEP, typename LoadA, typename LoadB, typename Init, typename Store>
+__device__ __forceinline__ void tile_products(int first, int lane, LoadA a4, LoadB b4, Init init, Store store) {
+    static_assert(K % 16 == 0 && K > 0, "K in blocks of 16");
+    constexpr int TPW = (TILES + STEP - 1) / STEP;
+    constexpr int KB = K / 16;
+    constexpr int G = TPW % 2 == 0 ? 2 : 1;
+    constexpr int NU = TPW * KB;   // units of one tile and one block
+    // The lane index is made opaque so that the operand addresses are formed
+    // here and not hoisted out of enclosing loops, where they would stay live.
+    const int lane_o = opaque_int(lane);
+    const int r16 = lane_o & 15;
+    const int q4 = lane_o >> 4;
+    // Unit n: tile t = G (n / (G KB)) + n % G of the wave, block (n / G) % KB.
+    f32x4 ra[2];
+    f32x4 rb[2];
+    auto issue = [&](auto nc) {
+        constexpr int n = decltype(nc)::value;
+        constexpr int t = G * (n / (G * KB)) + n % G;
+        constexpr int k = 16 * ((n / G) % KB);
+        const int tile = first + STEP * t < TILES ? first + STEP * t : 0;
+        ra[n % 2] = a4(16 * (tile / NT) + r16, k + 4 * q4);
+        rb[n % 2] = b4(16 * (tile % NT) + r16, k + 4 * q4);
+    };
+    f32x4 acc[TPW];
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-            store(i0 + 4 * q4 + mm, j0 + r16, acc[mm]);
+    for (int t = 0; t < TPW; ++t) {
+        acc[t] = init(t);
+    }
+    issue(std::integral_constant<int, 0>{});
+    unroll_to<NU>([&](auto nc) {
+        constexpr int n = decltype(nc)::value;
+        constexpr int t = G * (n / (G * KB)) + n % G;
+        if constexpr (n + 1 < NU) {
+            issue(std::integral_constant<int, n + 1>{});
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[n % 2][s], rb[n % 2][s], acc[t], 0, 0, 0);
+        }
+    });
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        const int tile = first + STEP * t;
+        if (tile < TILES) {
+            store(t, 16 * (tile / NT) + 4 * q4, 16 * (tile % NT) + r16, acc[t]);
+        }
+    }
+}
+
+// Four consecutive floats of an LDS row (16-byte aligned).
+__device__ __forceinline__ f32x4 lds_quad(const float* p) {
+    return *reinterpret_cast<const f32x4*>(p);
+}
+
+// Rows k .. k + 3 of column j of a row-major LDS matrix (row stride ld).
+__device__ __forceinline__ f32x4 lds_column_quad(const float* base, int ld, int k, int j) {
+    return (f32x4){base[k * ld + j], base[(k + 1) * ld + j], base[(k + 2) * ld + j], base[(k + 3) * ld + j]};
+}
+
+// One M x N block product (M, N multiples of 16, K of 16), tiles first,
+// first + STEP, ... of the result for this wave: store(i, j, sum_k A(i, k)
+// B(k, j)) in the order of tile_products, with a4 and b4 as there.  Operands
+// and results must not overlap.
+template <int M, int N, int K, int STEP, typename LoadA, typename LoadB, typename Store>
+__device__ __forceinline__ void block_product(int first, int lane, LoadA a4, LoadB b4, Store store) {
+    tile_products<(M / 16) * (N / 16), N / 16, K, STEP>(
+        first, lane, a4, b4, [](int) { return (f32x4){0.0f, 0.0f, 0.0f, 0.0f}; },
+        [&](int, int i, int j, const f32x4& acc) {
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) {
+                store(i + mm, j, acc[mm]);
+            }
+        });
+}
+
+// f(std::integral_constant<int, n>) for the column tiles n = 1 .. 4 of a
+// 64-column panel.
+template <typename F>
+__device__ __forceinline__ void with_column_tiles(int ncols, F&& f) {
+    switch (ncols) {
+        case 1: f(std::integral_constant<int, 1>{}); break;
+        case 2: f(std::integral_constant<int, 2>{}); break;
+        case 3: f(std::integral_constant<int, 3>{}); break;
+        default: f(std::integral_constant<int, 4>{}); break;
     }
 }
 
@@ -974,11 +1048,15 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
             base_pre[t] = base_tile(t);
         }
     }
+    // Quad e of W^T's panel at drive row c0: W[c0 + 4 (e % 16) + u][e / 16]
+    // for u = 0 .. 3, zero past the width.
     auto drive_quad = [&](int c0, int width, int e) {
-        const int c = (4 * e) / R;
-        f32x4 w = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (c < width) {
-            w = *reinterpret_cast<const f32x4*>(drive + (c0 + c) * R + (4 * e - c * R));
+        const int j = e >> 4;
+        const int c = 4 * (e & 15);
+        f32x4 w;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            w[u] = c + u < width ? drive[(c0 + c + u) * R + j] : 0.0f;
         }
         return w;
     };
@@ -1091,19 +1169,20 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
             }
         } else {
             load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root, s_pa,
-                                                              PLD, lane, wave - 1, 3);
+                                                              LD, lane, wave - 1, 3);
         }
         __syncthreads();
-        // L21 = A21 L11^-T (into I + K's space, free until its assembly).
-        block_product(H2, H1, H1, wave, 4, lane,
-                      [&](int i, int k) { return s_work[(H1 + i) * LD + k]; },
-                      [&](int k, int j) { return s_linvt[k * LD + j]; },
+        // L21 = A21 L11^-T (into I + K's space, free until its assembly); the
+        // operand L11^-T is read by rows of L11^-1.
+        block_product<H2, H1, H1, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_work + (H1 + i) * LD + k); },
+                      [&](int j, int k) { return lds_quad(s_linv + j * LD + k); },
                       [&](int i, int j, float v) { s_sys[(H1 + i) * LD + j] = v; });
         __syncthreads();
         // A22 - L21 L21^T, in place.
-        block_product(H2, H2, H1, wave, 4, lane,
-                      [&](int i, int k) { return s_sys[(H1 + i) * LD + k]; },
-                      [&](int k, int j) { return s_sys[(H1 + j) * LD + k]; },
+        block_product<H2, H2, H1, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_sys + (H1 + i) * LD + k); },
+                      [&](int j, int k) { return lds_quad(s_sys + (H1 + j) * LD + k); },
                       [&](int i, int j, float v) { s_work[(H1 + i) * LD + H1 + j] -= v; });
         __syncthreads();
         if (wave == 0) {
@@ -1146,18 +1225,19 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
                 }
             }
         } else {
-            // L21 L11^-1 into the second panel (free until the Z products).
-            block_product(H2, H1, H1, wave - 1, 3, lane,
-                          [&](int i, int k) { return s_sys[(H1 + i) * LD + k]; },
-                          [&](int k, int j) { return s_linv[k * LD + j]; },
-                          [&](int i, int j, float v) { s_pb[i * PLD + j] = v; });
+            // (L21 L11^-1)^T into the second panel (free until the Z
+            // products); the operand L11^-1 is read by rows of L11^-T.
+            block_product<H2, H1, H1, 3>(wave - 1, lane,
+                          [&](int i, int k) { return lds_quad(s_sys + (H1 + i) * LD + k); },
+                          [&](int j, int k) { return lds_quad(s_linvt + j * LD + k); },
+                          [&](int i, int j, float v) { s_pb[j * PLD + i] = v; });
         }
         __syncthreads();
         // L^-1's lower-left block -L22^-1 (L21 L11^-1), with its transpose in
         // L^-T; the upper-right blocks are zero.
-        block_product(H2, H1, H2, wave, 4, lane,
-                      [&](int i, int k) { return s_linv[(H1 + i) * LD + H1 + k]; },
-                      [&](int k, int j) { return s_pb[k * PLD + j]; },
+        block_product<H2, H1, H2, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_linv + (H1 + i) * LD + H1 + k); },
+                      [&](int j, int k) { return lds_quad(s_pb + j * PLD + k); },
                       [&](int i, int j, float v) {
                           s_linv[(H1 + i) * LD + j] = -v;
                           s_linvt[j * LD + H1 + i] = -v;
@@ -1208,7 +1288,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         }
     } else {
         load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root, s_pa,
-                                                          PLD, lane, wave - 1, 3);
+                                                          LD, lane, wave - 1, 3);
     }
     __syncthreads();
     if (tape != nullptr) {
@@ -1222,6 +1302,12 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     // ---- Z panels (Z = L^-1 S / sqrt(n)) and Theta = Z W accumulation, on
     // FP32 MFMA 16 x 16 tiles; wave w takes tiles w, w + 4, ... --------------
     float* zbuf = a.zbuf + system * R * d;
+    // The product epilogues write Z and U to global memory through raw
+    // buffers (empty when not wanted): a plain store beside the epilogues'
+    // LDS stores was merged with them into generic (flat) stores, whose
+    // counter makes every later LDS wait a full drain.
+    const BufferRsrc zbuf_out = make_buffer(zbuf, d > kSolvePanel ? int64_t{4} * R * d : 0);
+    const BufferRsrc tape_out = make_buffer(tape, tape != nullptr ? int64_t{4} * a.tape_stride : 0);
     f32x4 theta_acc[SL::kTilesPerWave];
 #pragma unroll
     for (int t = 0; t < SL::kTilesPerWave; ++t) {
@@ -1231,50 +1317,43 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         const int width = d - c0 < kSolvePanel ? d - c0 : kSolvePanel;
         const int ncols = (width + 15) / 16;   // column tiles; S is zero past the width
         if (c0 > 0) {
-            load_cross_panel<R, R / 4, SL::kChunkBatch>(part, stride, chunks, d, c0, width, root, s_pa, PLD, lane,
+            load_cross_panel<R, R / 4, SL::kChunkBatch>(part, stride, chunks, d, c0, width, root, s_pa, LD, lane,
                                                         wave, 4);
             __syncthreads();
         }
-        for (int tile = wave; tile < (R / 16) * ncols; tile += 4) {
-            const int i0 = 16 * (tile / ncols);
-            const int j0 = 16 * (tile - (tile / ncols) * ncols);
-            const f32x4 z = mfma_tile_f32(
-                (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, R, [&](int k) { return s_linv[(i0 + r16) * LD + k + q4]; },
-                [&](int k) { return s_pa[(k + q4) * PLD + j0 + r16]; });
-            const int c = j0 + r16;
+        with_column_tiles(ncols, [&](auto nc) {
+            constexpr int NC = decltype(nc)::value;
+            tile_products<(R / 16) * NC, NC, R, 4>(
+                wave, lane, [&](int i, int k) { return lds_quad(s_linv + i * LD + k); },
+                [&](int j, int k) { return lds_quad(s_pa + j * LD + k); },
+                [](int) { return (f32x4){0.0f, 0.0f, 0.0f, 0.0f}; },
+                [&](int, int i4, int c, const f32x4& z) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const int i = i0 + 4 * q4 + m;
-                s_pb[i * PLD + c] = z[m];
-                if (c < width) {
-                    if (d > kSolvePanel) {
-                        zbuf[i * d + c0 + c] = z[m];
+                    for (int m = 0; m < 4; ++m) {
+                        const int i = i4 + m;
+                        s_pb[i * PLD + c] = z[m];
+                        const uint32_t at = c < width ? 4u * static_cast<uint32_t>(i * d + c0 + c) : kOutOfRange;
+                        buffer_store_f32(z[m], zbuf_out, at);
+                        buffer_store_f32(z[m], tape_out, at + (c < width ? 16u * R * R : 0u));
                     }
-                    if (tape != nullptr) {
-                        tape[4 * R * R + i * d + c0 + c] = z[m];
-                    }
-                }
-            }
-        }
+                });
+        });
         __syncthreads();
-        // Drive rows c0 .. c0 + 63 (zero past the width), row stride R.
+        // W^T of drive rows c0 .. c0 + 63 (zero past the width), row stride PLD.
 #pragma unroll
         for (int u = 0; u < kDriveQuads; ++u) {
             const int e = tid + u * kSolveThreads;
-            *reinterpret_cast<f32x4*>(s_pa + 4 * e) = kPrefetch && c0 == 0 ? drive_pre[u] : drive_quad(c0, width, e);
+            *reinterpret_cast<f32x4*>(s_pa + (e >> 4) * PLD + 4 * (e & 15)) =
+                kPrefetch && c0 == 0 ? drive_pre[u] : drive_quad(c0, width, e);
         }
         __syncthreads();
-#pragma unroll
-        for (int t = 0; t < SL::kTilesPerWave; ++t) {
-            const int tile = wave + 4 * t;
-            if (tile < SL::kTiles) {
-                const int i0 = 16 * (tile / (R / 16));
-                const int j0 = 16 * (tile % (R / 16));
-                theta_acc[t] = mfma_tile_f32(
-                    theta_acc[t], 16 * ncols, [&](int k) { return s_pb[(i0 + r16) * PLD + k + q4]; },
-                    [&](int k) { return s_pa[(k + q4) * R + j0 + r16]; });
-            }
-        }
+        with_column_tiles(ncols, [&](auto nc) {
+            constexpr int NC = decltype(nc)::value;
+            tile_products<SL::kTiles, R / 16, 16 * NC, 4>(
+                wave, lane, [&](int i, int k) { return lds_quad(s_pb + i * PLD + k); },
+                [&](int j, int k) { return lds_quad(s_pa + j * PLD + k); }, [&](int t) { return theta_acc[t]; },
+                [&](int t, int, int, const f32x4& v) { theta_acc[t] = v; });
+        });
         __syncthreads();
     }
 
@@ -1316,24 +1395,22 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
 
     // ---- I + K = I + F F^T + Omega in FP32 (reference.py:491-497); all R
     // products summed (F is lower triangular, the rest add exact zeros).
-#pragma unroll
-    for (int t = 0; t < SL::kTilesPerWave; ++t) {
-        const int tile = wave + 4 * t;
-        if (tile < SL::kTiles) {
-            const int i0 = 16 * (tile / (R / 16));
-            const int j0 = 16 * (tile % (R / 16));
-            const f32x4 sum = mfma_tile_f32(
-                (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, R, [&](int k) { return s_work[(i0 + r16) * LD + k + q4]; },
-                [&](int k) { return s_work[(j0 + r16) * LD + k + q4]; });
-            const int c = j0 + r16;
+    tile_products<SL::kTiles, R / 16, R, 4>(
+        wave, lane, [&](int i, int k) { return lds_quad(s_work + i * LD + k); },
+        [&](int j, int k) { return lds_quad(s_work + j * LD + k); },
+        [](int) { return (f32x4){0.0f, 0.0f, 0.0f, 0.0f}; },
+        [&](int, int i4, int c, const f32x4& sum) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const int i = i0 + 4 * q4 + m;
-                const float skew = c > i ? s_theta[i * LD + c] : (c < i ? -s_theta[c * LD + i] : 0.0f);
+                const int i = i4 + m;
+                // Both entries are read (in bounds) and one is selected, so
+                // the epilogue has no branches around its reads.
+                const float upper = s_theta[i * LD + c];
+                const float lower = s_theta[c * LD + i];
+                const float skew = c > i ? upper : (c < i ? -lower : 0.0f);
                 s_sys[i * LD + c] = sum[m] + skew + (c == i ? 1.0f : 0.0f);
             }
-        }
-    }
+        });
     __syncthreads();
 
     // ---- (I + K)^-1 by Gauss-Jordan on all four waves, in place, on the diagonal
@@ -1368,18 +1445,18 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
             gauss_jordan_halves<LD>(s_sys, s_sys, s_work, lane);
         }
         __syncthreads();
-        block_product(H1, H2, H1, wave, 4, lane,
-                      [&](int i, int k) { return s_sys[i * LD + k]; },
-                      [&](int k, int j) { return s_sys[k * LD + H1 + j]; },
+        block_product<H1, H2, H1, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_sys + i * LD + k); },
+                      [&](int j, int k) { return lds_column_quad(s_sys + H1, LD, k, j); },
                       [&](int i, int j, float v) { s_work[i * LD + j] = v; });
-        block_product(H2, H1, H1, wave, 4, lane,
-                      [&](int i, int k) { return s_sys[(H1 + i) * LD + k]; },
-                      [&](int k, int j) { return s_sys[k * LD + j]; },
+        block_product<H2, H1, H1, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_sys + (H1 + i) * LD + k); },
+                      [&](int j, int k) { return lds_column_quad(s_sys, LD, k, j); },
                       [&](int i, int j, float v) { s_work[(H1 + i) * LD + j] = v; });
         __syncthreads();
-        block_product(H2, H2, H1, wave, 4, lane,
-                      [&](int i, int k) { return s_sys[(H1 + i) * LD + k]; },
-                      [&](int k, int j) { return s_work[k * LD + j]; },
+        block_product<H2, H2, H1, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_sys + (H1 + i) * LD + k); },
+                      [&](int j, int k) { return lds_column_quad(s_work, LD, k, j); },
                       [&](int i, int j, float v) { s_sys[(H1 + i) * LD + H1 + j] -= v; });
         __syncthreads();
         // Theta's space is free once I + K is assembled.
@@ -1391,18 +1468,18 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
             gauss_jordan_waves<H2, LD>(s_sys + H1 * LD + H1, s_theta, wave, lane);
         }
         __syncthreads();
-        block_product(H2, H1, H2, wave, 4, lane,
-                      [&](int i, int k) { return s_sys[(H1 + i) * LD + H1 + k]; },
-                      [&](int k, int j) { return s_work[(H1 + k) * LD + j]; },
+        block_product<H2, H1, H2, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_sys + (H1 + i) * LD + H1 + k); },
+                      [&](int j, int k) { return lds_column_quad(s_work + H1 * LD, LD, k, j); },
                       [&](int i, int j, float v) { s_sys[(H1 + i) * LD + j] = -v; });
-        block_product(H1, H2, H2, wave, 4, lane,
-                      [&](int i, int k) { return s_work[i * LD + k]; },
-                      [&](int k, int j) { return s_sys[(H1 + k) * LD + H1 + j]; },
+        block_product<H1, H2, H2, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_work + i * LD + k); },
+                      [&](int j, int k) { return lds_column_quad(s_sys + H1 * LD + H1, LD, k, j); },
                       [&](int i, int j, float v) { s_sys[i * LD + H1 + j] = -v; });
         __syncthreads();
-        block_product(H1, H1, H2, wave, 4, lane,
-                      [&](int i, int k) { return s_work[i * LD + k]; },
-                      [&](int k, int j) { return s_sys[(H1 + k) * LD + j]; },
+        block_product<H1, H1, H2, 4>(wave, lane,
+                      [&](int i, int k) { return lds_quad(s_work + i * LD + k); },
+                      [&](int j, int k) { return lds_column_quad(s_sys + H1 * LD, LD, k, j); },
                       [&](int i, int j, float v) { s_sys[i * LD + j] -= v; });
     } else {
         gauss_jordan_waves<R, LD>(s_sys, s_work, wave, lane);
@@ -1429,35 +1506,37 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
             __syncthreads();
         }
         const int ncols = (width + 15) / 16;
-        for (int tile = wave; tile < (R / 16) * ncols; tile += 4) {
-            const int i0 = 16 * (tile / ncols);
-            const int j0 = 16 * (tile - (tile / ncols) * ncols);
-            const f32x4 u = mfma_tile_f32(
-                (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, R, [&](int k) { return s_sys[(i0 + r16) * LD + k + q4]; },
-                [&](int k) { return s_pb[(k + q4) * PLD + j0 + r16]; });
-            const int c = j0 + r16;
+        with_column_tiles(ncols, [&](auto nc) {
+            constexpr int NC = decltype(nc)::value;
+            tile_products<(R / 16) * NC, NC, R, 4>(
+                wave, lane, [&](int i, int k) { return lds_quad(s_sys + i * LD + k); },
+                [&](int j, int k) { return lds_column_quad(s_pb, PLD, k, j); },
+                [](int) { return (f32x4){0.0f, 0.0f, 0.0f, 0.0f}; },
+                [&](int, int i4, int c, const f32x4& u) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const int i = i0 + 4 * q4 + m;
-                if (tape != nullptr && c < width) {
-                    tape[4 * R * R + R * d + i * d + c0 + c] = u[m];
-                }
-                s_pa[i * PLD + c] = 2.0f * u[m] - (1.0f + eta) * s_pb[i * PLD + c];
-            }
-        }
+                    for (int m = 0; m < 4; ++m) {
+                        const int i = i4 + m;
+                        buffer_store_f32(u[m], tape_out,
+                                         c < width ? 4u * static_cast<uint32_t>(4 * R * R + R * d + i * d + c0 + c)
+                                                   : kOutOfRange);
+                        s_pa[c * LD + i] = 2.0f * u[m] - (1.0f + eta) * s_pb[i * PLD + c];
+                    }
+                });
+        });
         __syncthreads();
-        for (int tile = wave; tile < (R / 16) * ncols; tile += 4) {
-            const int i0 = 16 * (tile / ncols);
-            const int j0 = 16 * (tile - (tile / ncols) * ncols);
-            const f32x4 m_acc = mfma_tile_f32(
-                (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, R, [&](int k) { return s_linvt[(i0 + r16) * LD + k + q4]; },
-                [&](int k) { return s_pa[(k + q4) * PLD + j0 + r16]; });
-            const int c = j0 + r16;
+        with_column_tiles(ncols, [&](auto nc) {
+            constexpr int NC = decltype(nc)::value;
+            tile_products<(R / 16) * NC, NC, R, 4>(
+                wave, lane, [&](int i, int k) { return lds_quad(s_linvt + i * LD + k); },
+                [&](int j, int k) { return lds_quad(s_pa + j * LD + k); },
+                [](int) { return (f32x4){0.0f, 0.0f, 0.0f, 0.0f}; },
+                [&](int, int i4, int c, const f32x4& m_acc) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                s_pb[(i0 + 4 * q4 + m) * PLD + c] = c < width ? m_acc[m] / root : 0.0f;
-            }
-        }
+                    for (int m = 0; m < 4; ++m) {
+                        s_pb[(i4 + m) * PLD + c] = c < width ? m_acc[m] / root : 0.0f;
+                    }
+                });
+        });
         __syncthreads();
         {
             // Record of feature block fb, lane g4 * 16 + column % 16.
