@@ -483,8 +483,10 @@ __device__ __forceinline__ void wave_lds_order() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Blocked Cholesky of the SPD matrix in LDS (row stride LD), one row per lane
-// (lanes >= R hold zero rows), 8-column panels.  Per panel:
+// Cholesky factor of an R-column block of an SPD matrix whose rows are held
+// one per lane in l (the block's R diagonal rows in lanes 0 .. R - 1, rows
+// below the block in the lanes after them, zero rows past the matrix), by
+// 8-column panels.  Per panel:
 //   1. rows c0..c0+7 of the diagonal block go through LDS to every lane, and
 //      every lane factors the 8 x 8 block itself (right-looking, in registers);
 //   2. each lane solves its own panel entries against that factor,
@@ -495,8 +497,9 @@ __device__ __forceinline__ void wave_lds_order() {
 //      a_ij -= sum_m L_im L_jm to its columns right of the panel.
 // Two LDS round trips per panel instead of one per column.  s_diag holds 64
 // floats, s_panel 8 R, s_inv_diag R (16-byte aligned).  Panels recurse at
-// compile time so every register index is static.  On return l is row `lane`
-// of L (zero above the diagonal) and s_inv_diag[m] = 1 / L_mm.
+// compile time so every register index is static.  On return l is the lane's
+// row of L's block column (zero above the diagonal) and s_inv_diag[m] =
+// 1 / L_mm.
 template <int R, int LD, int C0>
 __device__ __forceinline__ void cholesky_panel(float* s_diag, float* s_panel, float* s_inv_diag, int lane,
                                                float (&l)[R]) {
@@ -618,22 +621,6 @@ __device__ __forceinline__ void cholesky_panel(float* s_diag, float* s_panel, fl
         }
         cholesky_panel<R, LD, C0 + B>(s_diag, s_panel, s_inv_diag, lane, l);
     }
-}
-
-template <int R, int LD>
-__device__ __forceinline__ void blocked_cholesky(const float* s_a, float* s_diag, float* s_panel, float* s_inv_diag,
-                                                 int lane, float (&l)[R]) {
-    const bool live = lane < R;
-    const float* own = s_a + (live ? lane : 0) * LD;
-#pragma unroll
-    for (int j = 0; j < R; j += 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(own + j);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            l[j + e] = live ? v[e] : 0.0f;
-        }
-    }
-    cholesky_panel<R, LD, 0>(s_diag, s_panel, s_inv_diag, lane, l);
 }
 
 // Column `lane` of L^-1 from L^T (row-major in LDS, row stride LD) whose
@@ -1115,186 +1102,153 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
                 *reinterpret_cast<f32x4*>(s_work + i * LD + j) = value;
             }
         }
+        // L^-1 and L^-T start at zero: only their lower (upper) blocks are
+        // written.
+        for (int q = tid; q < R * LD / 4; q += kSolveThreads) {
+            *reinterpret_cast<f32x4*>(s_linv + 4 * q) = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            *reinterpret_cast<f32x4*>(s_linvt + 4 * q) = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
     }
     __syncthreads();
 
-    // ---- Cholesky (blocked, wave 0), then L^-1 one column per lane; waves
-    // 1-3 meanwhile sum the first S panel ------------------------------------
-    if constexpr (R >= 48) {
-        // Two levels from rank 48 on: with A = [[A11, A21^T], [A21, A22]] and
-        // A11 32 x 32, L11 = chol(A11) and L11^-1 (wave 0, the one-level
-        // kernels at size 32), L21 = A21 L11^-T and A22 - L21 L21^T (MFMA,
-        // all waves), L22 = chol(A22 - L21 L21^T) and L22^-1 (wave 0, while
-        // waves 1-3 form L21 L11^-1), and L^-1's lower-left block
-        // -L22^-1 (L21 L11^-1).  Two dependent chains of 32 steps and a few
-        // products instead of one chain of R steps.
-        constexpr int H1 = 32;
-        constexpr int H2 = R - H1;
+    // ---- Cholesky of A and L^-1 by 16-column blocks on wave 0 (waves 1-3
+    // meanwhile sum the first S panel), then L^-1's blocks below the diagonal
+    // on all waves.  Column block j (j0 = 16 j): lane l holds row j0 + l of
+    // the block's 16 columns of A, already reduced by the earlier blocks; the
+    // 8-column panel factorization makes it row j0 + l of L's block column
+    // (rows past R hold zeros), L goes to L's space (s_sys, free until I + K
+    // is assembled); the rows below take the rank-16 update
+    // A_IC -= L_Ij L_Cj^T on MFMA tiles; and L_jj^-1 comes from L_jj^T (laid
+    // over A_jj, which is spent) one column per lane.  One wave and no
+    // barriers along the chain; the diagonal blocks' inverses then join by
+    // doubling: for neighbouring groups a (top) and b of h rows,
+    // L^-1_ba = -L^-1_bb (L_ba L^-1_aa).
+    {
+        constexpr int B = R / 16;
         if (wave == 0) {
-            const bool live = lane < H1;
-            float l1[H1];
-            float* s_inv_diag = s_theta + 64 + 8 * H1;
-            blocked_cholesky<H1, LD>(s_work, s_theta, s_theta + 64, s_inv_diag, lane, l1);
-            // L11^T with 1 / L_ii on the diagonal (the substitution's operand),
-            // in L^-1's space until the substitution is done.
-            wave_lds_order();
-            if (live) {
-                const float own_inv = s_inv_diag[lane];
+            float* s_diag = s_theta;
+            float* s_panel = s_theta + 64;
+            float* s_inv_diag = s_theta + 64 + 8 * 16;
+            unroll_to<B>([&](auto jc) {
+                constexpr int j0 = 16 * decltype(jc)::value;
+                constexpr int kRows = R - j0;
+                const bool live = lane < kRows;
+                float v[16];
+                {
+                    const float* own = s_work + (live ? j0 + lane : j0) * LD + j0;
 #pragma unroll
-                for (int j = 0; j < H1; ++j) {
-                    s_linv[j * LD + lane] = j == lane ? own_inv : l1[j];
-                }
-                if (tape != nullptr) {
+                    for (int c = 0; c < 16; c += 4) {
+                        const f32x4 q = *reinterpret_cast<const f32x4*>(own + c);
 #pragma unroll
-                    for (int j = 0; j < R; j += 4) {
-                        *reinterpret_cast<f32x4*>(tape + lane * R + j) = j < H1
-                            ? (f32x4){l1[j], l1[j + 1], l1[j + 2], l1[j + 3]}
-                            : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                        for (int e = 0; e < 4; ++e) {
+                            v[c + e] = live ? q[e] : 0.0f;
+                        }
                     }
                 }
-            }
-            wave_lds_order();
-            float x[H1];
-            lower_inverse_column<H1, LD>(s_linv, lane, x);
-            wave_lds_order();
-            if (live) {
+                cholesky_panel<16, LD, 0>(s_diag, s_panel, s_inv_diag, lane, v);
+                wave_lds_order();
+                if (live) {
 #pragma unroll
-                for (int i = 0; i < H1; i += 4) {
-                    *reinterpret_cast<f32x4*>(s_linvt + lane * LD + i) = (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
+                    for (int c = 0; c < 16; c += 4) {
+                        *reinterpret_cast<f32x4*>(s_sys + (j0 + lane) * LD + j0 + c) =
+                            (f32x4){v[c], v[c + 1], v[c + 2], v[c + 3]};
+                    }
                 }
+                if (lane < 16) {
+                    // L_jj^T with 1 / L_ii on the diagonal over A_jj.
+                    const float own_inv = s_inv_diag[lane];
 #pragma unroll
-                for (int i = 0; i < H1; ++i) {
-                    s_linv[i * LD + lane] = x[i];
+                    for (int m = 0; m < 16; ++m) {
+                        s_work[(j0 + m) * LD + j0 + lane] = m == lane ? own_inv : v[m];
+                    }
                 }
-            }
+                wave_lds_order();
+                if constexpr (kRows > 16) {
+                    constexpr int T = kRows - 16;
+                    block_product<T, T, 16, 1>(
+                        0, lane, [&](int i, int k) { return lds_quad(s_sys + (j0 + 16 + i) * LD + j0 + k); },
+                        [&](int c, int k) { return lds_quad(s_sys + (j0 + 16 + c) * LD + j0 + k); },
+                        [&](int i, int c, float value) { s_work[(j0 + 16 + i) * LD + j0 + 16 + c] -= value; });
+                    wave_lds_order();
+                }
+                float x[16];
+                lower_inverse_column<16, LD>(s_work + j0 * LD + j0, lane, x);
+                if (lane < 16) {
+#pragma unroll
+                    for (int i = 0; i < 16; i += 4) {
+                        *reinterpret_cast<f32x4*>(s_linvt + (j0 + lane) * LD + j0 + i) =
+                            (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        s_linv[(j0 + i) * LD + j0 + lane] = x[i];
+                    }
+                }
+                wave_lds_order();
+            });
         } else {
             load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root, s_pa,
                                                               LD, lane, wave - 1, 3);
         }
         __syncthreads();
-        // L21 = A21 L11^-T (into I + K's space, free until its assembly); the
-        // operand L11^-T is read by rows of L11^-1.
-        block_product<H2, H1, H1, 4>(wave, lane,
-                      [&](int i, int k) { return lds_quad(s_work + (H1 + i) * LD + k); },
-                      [&](int j, int k) { return lds_quad(s_linv + j * LD + k); },
-                      [&](int i, int j, float v) { s_sys[(H1 + i) * LD + j] = v; });
-        __syncthreads();
-        // A22 - L21 L21^T, in place.
-        block_product<H2, H2, H1, 4>(wave, lane,
-                      [&](int i, int k) { return lds_quad(s_sys + (H1 + i) * LD + k); },
-                      [&](int j, int k) { return lds_quad(s_sys + (H1 + j) * LD + k); },
-                      [&](int i, int j, float v) { s_work[(H1 + i) * LD + H1 + j] -= v; });
-        __syncthreads();
-        if (wave == 0) {
-            const bool live = lane < H2;
-            float l2[H2];
-            float* s_inv_diag = s_theta + 64 + 8 * H2;
-            blocked_cholesky<H2, LD>(s_work + H1 * LD + H1, s_theta, s_theta + 64, s_inv_diag, lane, l2);
-            wave_lds_order();
-            if (live) {
-                const float own_inv = s_inv_diag[lane];
-#pragma unroll
-                for (int j = 0; j < H2; ++j) {
-                    s_linv[(H1 + j) * LD + H1 + lane] = j == lane ? own_inv : l2[j];
-                }
-                if (tape != nullptr) {
-                    float* row = tape + (H1 + lane) * R;
-#pragma unroll
-                    for (int j = 0; j < H1; j += 4) {
-                        *reinterpret_cast<f32x4*>(row + j) = *reinterpret_cast<const f32x4*>(s_sys + (H1 + lane) * LD + j);
+        // Doubling: groups of h rows, h = 16, 32, ...; every pair of groups
+        // (a0, b0 = a0 + h, hb = min(h, R - b0) rows) in two products,
+        // T = L_ba L^-1_aa (its transpose into the Z panel, free until the Z
+        // products) and L^-1_ba = -L^-1_bb T.  Pairs of one level run on
+        // different waves.
+        unroll_to<4>([&](auto lc) {
+            constexpr int h = 16 << decltype(lc)::value;
+            if constexpr (h < R) {
+                constexpr int kPairs = (R + 2 * h - 1) / (2 * h);
+                unroll_to<kPairs>([&](auto pc) {
+                    constexpr int a0 = 2 * h * decltype(pc)::value;
+                    constexpr int b0 = a0 + h;
+                    if constexpr (b0 < R) {
+                        constexpr int hb = R - b0 < h ? R - b0 : h;
+                        constexpr int kWaves = 4 / kPairs;
+                        constexpr int w0 = decltype(pc)::value * kWaves;
+                        if (wave >= w0 && wave < w0 + kWaves) {
+                            block_product<hb, h, h, kWaves>(
+                                wave - w0, lane, [&](int i, int k) { return lds_quad(s_sys + (b0 + i) * LD + a0 + k); },
+                                [&](int c, int k) { return lds_quad(s_linvt + (a0 + c) * LD + a0 + k); },
+                                [&](int i, int c, float value) { s_pb[(a0 + c) * PLD + i] = value; });
+                        }
                     }
-#pragma unroll
-                    for (int j = 0; j < H2; j += 4) {
-                        *reinterpret_cast<f32x4*>(row + H1 + j) = (f32x4){l2[j], l2[j + 1], l2[j + 2], l2[j + 3]};
+                });
+                __syncthreads();
+                unroll_to<kPairs>([&](auto pc) {
+                    constexpr int a0 = 2 * h * decltype(pc)::value;
+                    constexpr int b0 = a0 + h;
+                    if constexpr (b0 < R) {
+                        constexpr int hb = R - b0 < h ? R - b0 : h;
+                        constexpr int kWaves = 4 / kPairs;
+                        constexpr int w0 = decltype(pc)::value * kWaves;
+                        if (wave >= w0 && wave < w0 + kWaves) {
+                            block_product<hb, h, hb, kWaves>(
+                                wave - w0, lane, [&](int i, int k) { return lds_quad(s_linv + (b0 + i) * LD + b0 + k); },
+                                [&](int c, int k) { return lds_quad(s_pb + (a0 + c) * PLD + k); },
+                                [&](int i, int c, float value) {
+                                    s_linv[(b0 + i) * LD + a0 + c] = -value;
+                                    s_linvt[(a0 + c) * LD + b0 + i] = -value;
+                                });
+                        }
                     }
-                }
+                });
+                __syncthreads();
             }
-            wave_lds_order();
-            float x[H2];
-            lower_inverse_column<H2, LD>(s_linv + H1 * LD + H1, lane, x);
-            wave_lds_order();
-            if (live) {
-#pragma unroll
-                for (int i = 0; i < H2; i += 4) {
-                    *reinterpret_cast<f32x4*>(s_linvt + (H1 + lane) * LD + H1 + i) =
-                        (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
-                }
-#pragma unroll
-                for (int i = 0; i < H2; ++i) {
-                    s_linv[(H1 + i) * LD + H1 + lane] = x[i];
-                }
-            }
-        } else {
-            // (L21 L11^-1)^T into the second panel (free until the Z
-            // products); the operand L11^-1 is read by rows of L11^-T.
-            block_product<H2, H1, H1, 3>(wave - 1, lane,
-                          [&](int i, int k) { return lds_quad(s_sys + (H1 + i) * LD + k); },
-                          [&](int j, int k) { return lds_quad(s_linvt + j * LD + k); },
-                          [&](int i, int j, float v) { s_pb[j * PLD + i] = v; });
-        }
-        __syncthreads();
-        // L^-1's lower-left block -L22^-1 (L21 L11^-1), with its transpose in
-        // L^-T; the upper-right blocks are zero.
-        block_product<H2, H1, H2, 4>(wave, lane,
-                      [&](int i, int k) { return lds_quad(s_linv + (H1 + i) * LD + H1 + k); },
-                      [&](int j, int k) { return lds_quad(s_pb + j * PLD + k); },
-                      [&](int i, int j, float v) {
-                          s_linv[(H1 + i) * LD + j] = -v;
-                          s_linvt[j * LD + H1 + i] = -v;
-                      });
-        for (int e = tid; e < H1 * H2; e += kSolveThreads) {
-            const int i = e / H2;
-            const int j = e - i * H2;
-            s_linv[i * LD + H1 + j] = 0.0f;
-            s_linvt[(H1 + j) * LD + i] = 0.0f;
-        }
-    } else if (wave == 0) {
-        const bool live = lane < R;
-        float lrow[R];
-        // Theta's LDS is free until the Theta assembly.
-        float* s_inv_diag = s_theta + 64 + 8 * R;
-        blocked_cholesky<R, LD>(s_work, s_theta, s_theta + 64, s_inv_diag, lane, lrow);
-        // L^T to LDS for the substitution (A in s_work is spent), with
-        // 1 / L_ii in place of each diagonal entry (the substitution reads it
-        // with the row).
-        wave_lds_order();
-        if (live) {
-            const float own_inv = s_inv_diag[lane];
-#pragma unroll
-            for (int j = 0; j < R; ++j) {
-                s_work[j * LD + lane] = j == lane ? own_inv : lrow[j];
-            }
-            if (tape != nullptr) {
-#pragma unroll
-                for (int j = 0; j < R; j += 4) {
-                    *reinterpret_cast<f32x4*>(tape + lane * R + j) =
-                        (f32x4){lrow[j], lrow[j + 1], lrow[j + 2], lrow[j + 3]};
-                }
-            }
-        }
-        wave_lds_order();
-        float x[R];
-        lower_inverse_column<R, LD>(s_work, lane, x);
-        if (live) {
-            // Lane c holds column c of L^-1: row c of L^-T and column c of L^-1.
-#pragma unroll
-            for (int i = 0; i < R; i += 4) {
-                *reinterpret_cast<f32x4*>(s_linvt + lane * LD + i) = (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
-            }
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                s_linv[i * LD + lane] = x[i];
-            }
-        }
-    } else {
-        load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root, s_pa,
-                                                          LD, lane, wave - 1, 3);
+        });
     }
-    __syncthreads();
     if (tape != nullptr) {
         for (int q = tid; q < R * R / 4; q += kSolveThreads) {
             const int i = (4 * q) / R;
             const int j = 4 * q - i * R;
+            const f32x4 l = *reinterpret_cast<const f32x4*>(s_sys + i * LD + j);
+            f32x4 lower;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                lower[e] = j + e <= i ? l[e] : 0.0f;
+            }
+            *reinterpret_cast<f32x4*>(tape + 4 * q) = lower;
             *reinterpret_cast<f32x4*>(tape + 3 * R * R + 4 * q) = *reinterpret_cast<const f32x4*>(s_linv + i * LD + j);
         }
     }
