@@ -1111,86 +1111,104 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     }
     __syncthreads();
 
-    // ---- Cholesky of A and L^-1 by 16-column blocks on wave 0 (waves 1-3
-    // meanwhile sum the first S panel), then L^-1's blocks below the diagonal
-    // on all waves.  Column block j (j0 = 16 j): lane l holds row j0 + l of
-    // the block's 16 columns of A, already reduced by the earlier blocks; the
-    // 8-column panel factorization makes it row j0 + l of L's block column
-    // (rows past R hold zeros), L goes to L's space (s_sys, free until I + K
-    // is assembled); the rows below take the rank-16 update
-    // A_IC -= L_Ij L_Cj^T on MFMA tiles; and L_jj^-1 comes from L_jj^T (laid
-    // over A_jj, which is spent) one column per lane.  One wave and no
-    // barriers along the chain; the diagonal blocks' inverses then join by
-    // doubling: for neighbouring groups a (top) and b of h rows,
-    // L^-1_ba = -L^-1_bb (L_ba L^-1_aa).
+    // ---- Cholesky of A and L^-1 by 16-column blocks, then L^-1's blocks
+    // below the diagonal.  Column block j (j0 = 16 j): lane l of wave 0 holds
+    // row j0 + l of the block's 16 columns of A, reduced by the earlier
+    // blocks; the 8-column panel factorization makes it row j0 + l of L's
+    // block column (rows past R hold zeros); L goes to L's space (s_sys, free
+    // until I + K is assembled) and L_jj^T, with 1 / L_ii on its diagonal,
+    // over A_jj (spent).  Steps of one barrier each, with a lookahead of one
+    // block: in step j wave 0 applies block j - 1 to column block j (the
+    // rank-16 update A_Ij -= L_I,j-1 L_j,j-1^T on MFMA tiles) and factors
+    // column block j, while wave 1 forms L_j-1,j-1^-1 one column per lane and
+    // waves 2-3 apply block j - 1 to the columns past j.  Only the panel
+    // factorizations and one block-column update per step are on the chain;
+    // in step 0 waves 1-3 sum the first S panel.
+    // The diagonal blocks' inverses then join by doubling: for neighbouring
+    // groups a (top) and b of h rows, L^-1_ba = -L^-1_bb (L_ba L^-1_aa).
     {
         constexpr int B = R / 16;
-        if (wave == 0) {
-            float* s_diag = s_theta;
-            float* s_panel = s_theta + 64;
-            float* s_inv_diag = s_theta + 64 + 8 * 16;
-            unroll_to<B>([&](auto jc) {
-                constexpr int j0 = 16 * decltype(jc)::value;
-                constexpr int kRows = R - j0;
-                const bool live = lane < kRows;
-                float v[16];
-                {
-                    const float* own = s_work + (live ? j0 + lane : j0) * LD + j0;
+        unroll_to<B + 1>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            constexpr int j0 = 16 * j;
+            if constexpr (j == 0) {
+                // Waves 1-3 sum the first S panel beside the first panel.
+                if (wave != 0) {
+                    load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root,
+                                                                      s_pa, LD, lane, wave - 1, 3);
+                }
+            }
+            if constexpr (j < B) {
+                if (wave == 0) {
+                    if constexpr (j >= 1) {
+                        block_product<R - j0, 16, 16, 1>(
+                            0, lane, [&](int i, int k) { return lds_quad(s_sys + (j0 + i) * LD + j0 - 16 + k); },
+                            [&](int c, int k) { return lds_quad(s_sys + (j0 + c) * LD + j0 - 16 + k); },
+                            [&](int i, int c, float value) { s_work[(j0 + i) * LD + j0 + c] -= value; });
+                        wave_lds_order();
+                    }
+                    constexpr int kRows = R - j0;
+                    const bool live = lane < kRows;
+                    float v[16];
+                    {
+                        const float* own = s_work + (live ? j0 + lane : j0) * LD + j0;
 #pragma unroll
-                    for (int c = 0; c < 16; c += 4) {
-                        const f32x4 q = *reinterpret_cast<const f32x4*>(own + c);
+                        for (int c = 0; c < 16; c += 4) {
+                            const f32x4 q = *reinterpret_cast<const f32x4*>(own + c);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            v[c + e] = live ? q[e] : 0.0f;
+                            for (int e = 0; e < 4; ++e) {
+                                v[c + e] = live ? q[e] : 0.0f;
+                            }
+                        }
+                    }
+                    float* s_inv_diag = s_theta + 64 + 8 * 16;
+                    cholesky_panel<16, LD, 0>(s_theta, s_theta + 64, s_inv_diag, lane, v);
+                    wave_lds_order();
+                    if (live) {
+#pragma unroll
+                        for (int c = 0; c < 16; c += 4) {
+                            *reinterpret_cast<f32x4*>(s_sys + (j0 + lane) * LD + j0 + c) =
+                                (f32x4){v[c], v[c + 1], v[c + 2], v[c + 3]};
+                        }
+                    }
+                    if (lane < 16) {
+                        const float own_inv = s_inv_diag[lane];
+#pragma unroll
+                        for (int m = 0; m < 16; ++m) {
+                            s_work[(j0 + m) * LD + j0 + lane] = m == lane ? own_inv : v[m];
                         }
                     }
                 }
-                cholesky_panel<16, LD, 0>(s_diag, s_panel, s_inv_diag, lane, v);
-                wave_lds_order();
-                if (live) {
+            }
+            if constexpr (j >= 1) {
+                constexpr int p0 = j0 - 16;   // the previous block
+                if (wave == 1) {
+                    float x[16];
+                    lower_inverse_column<16, LD>(s_work + p0 * LD + p0, lane, x);
+                    if (lane < 16) {
 #pragma unroll
-                    for (int c = 0; c < 16; c += 4) {
-                        *reinterpret_cast<f32x4*>(s_sys + (j0 + lane) * LD + j0 + c) =
-                            (f32x4){v[c], v[c + 1], v[c + 2], v[c + 3]};
+                        for (int i = 0; i < 16; i += 4) {
+                            *reinterpret_cast<f32x4*>(s_linvt + (p0 + lane) * LD + p0 + i) =
+                                (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
+                        }
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            s_linv[(p0 + i) * LD + p0 + lane] = x[i];
+                        }
                     }
                 }
-                if (lane < 16) {
-                    // L_jj^T with 1 / L_ii on the diagonal over A_jj.
-                    const float own_inv = s_inv_diag[lane];
-#pragma unroll
-                    for (int m = 0; m < 16; ++m) {
-                        s_work[(j0 + m) * LD + j0 + lane] = m == lane ? own_inv : v[m];
+                if constexpr (j + 1 < B) {
+                    constexpr int n0 = j0 + 16;   // columns past block j
+                    if (wave >= 2) {
+                        block_product<R - n0, R - n0, 16, 2>(
+                            wave - 2, lane, [&](int i, int k) { return lds_quad(s_sys + (n0 + i) * LD + p0 + k); },
+                            [&](int c, int k) { return lds_quad(s_sys + (n0 + c) * LD + p0 + k); },
+                            [&](int i, int c, float value) { s_work[(n0 + i) * LD + n0 + c] -= value; });
                     }
                 }
-                wave_lds_order();
-                if constexpr (kRows > 16) {
-                    constexpr int T = kRows - 16;
-                    block_product<T, T, 16, 1>(
-                        0, lane, [&](int i, int k) { return lds_quad(s_sys + (j0 + 16 + i) * LD + j0 + k); },
-                        [&](int c, int k) { return lds_quad(s_sys + (j0 + 16 + c) * LD + j0 + k); },
-                        [&](int i, int c, float value) { s_work[(j0 + 16 + i) * LD + j0 + 16 + c] -= value; });
-                    wave_lds_order();
-                }
-                float x[16];
-                lower_inverse_column<16, LD>(s_work + j0 * LD + j0, lane, x);
-                if (lane < 16) {
-#pragma unroll
-                    for (int i = 0; i < 16; i += 4) {
-                        *reinterpret_cast<f32x4*>(s_linvt + (j0 + lane) * LD + j0 + i) =
-                            (f32x4){x[i], x[i + 1], x[i + 2], x[i + 3]};
-                    }
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        s_linv[(j0 + i) * LD + j0 + lane] = x[i];
-                    }
-                }
-                wave_lds_order();
-            });
-        } else {
-            load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root, s_pa,
-                                                              LD, lane, wave - 1, 3);
-        }
-        __syncthreads();
+            }
+            __syncthreads();
+        });
         // Doubling: groups of h rows, h = 16, 32, ...; every pair of groups
         // (a0, b0 = a0 + h, hb = min(h, R - b0) rows) in two products,
         // T = L_ba L^-1_aa (its transpose into the Z panel, free until the Z
