@@ -828,12 +828,13 @@ __device__ __forceinline__ void with_column_tiles(int ncols, F&& f) {
 // l % 32, so all 64 lanes update and each updates 16 columns.  Step k pivots
 // on the diagonal (no row exchanges: I + K has a positive definite symmetric
 // part, so every leading minor is nonzero); the rows' column-k value reaches
-// the other half by a lane swap, and the pivot row's two halves go through
-// LDS (s_rows, 64 floats per step parity; one lane per half writes, each
-// lane reads its half back as a broadcast).  Row k ends, scaled by
-// 1 / pivot_k, at row k of s_out.
+// the other half by v_permlane32_swap, and each half reads its part of pivot row k
+// from lane k of the half with ds_swizzle (a broadcast inside each group of
+// 32 lanes, no LDS memory): the pivot row written to LDS and read back cost
+// two LDS latencies per step.  Row k ends, scaled by 1 / pivot_k, at row k of
+// s_out.
 template <int LD>
-__device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s_out, float* s_rows, int lane) {
+__device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s_out, int lane) {
     const int half = lane >> 5;
     const int row = lane & 31;
     f32x16 t;
@@ -846,30 +847,28 @@ __device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s
         }
     }
     float own_pivot = 1.0f;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) {
+    unroll_to<32>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
         const bool owner = half == (k >> 4);
         const float own = t[k & 15];
-        const float other = __shfl_xor(own, 32);
+        // The other half's value by v_permlane32_swap (a VALU lane swap):
+        // element 1 of the result holds lanes 32-63 in lanes 0-31, element 0
+        // lanes 0-31 in lanes 32-63.
+        const auto swapped = __builtin_amdgcn_permlane32_swap(__float_as_uint(own), __float_as_uint(own), false, false);
+        const float other = __uint_as_float(half != 0 ? swapped[0] : swapped[1]);
         const float x = owner ? own : other;
         const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(own), 32 * (k >> 4) + k));
         const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
         const float f = row == k ? 0.0f : x * inv_pivot;
-        float* buf = s_rows + (k & 1) * 32 + 16 * half;
-        if (row == k) {
+        // Bit mode: source lane ((i & 0) | k) ^ 0 of each 32-lane group.
+        f32x16 pivot_row;
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                *reinterpret_cast<f32x4*>(buf + 4 * m) = (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
-            }
+        for (int e = 0; e < 16; ++e) {
+            pivot_row[e] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(t[e]), k << 5));
         }
-        wave_lds_order();
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(buf + 4 * m);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                t[4 * m + e] = fmaf(-f, v[e], t[4 * m + e]);
-            }
+        for (int e = 0; e < 16; ++e) {
+            t[e] = fmaf(-f, pivot_row[e], t[e]);
         }
         if (owner) {
             t[k & 15] = row == k ? 1.0f : -f;
@@ -877,7 +876,7 @@ __device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s
         if (row == k) {
             own_pivot = pivot;
         }
-    }
+    });
     t = t * __builtin_amdgcn_rcpf(own_pivot);
     wave_lds_order();
 #pragma unroll
@@ -1401,7 +1400,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     // stage 66.4 against 75.4 us).
     if constexpr (R == 32) {
         if (wave == 0) {
-            gauss_jordan_halves<LD>(s_sys, s_sys, s_work, lane);
+            gauss_jordan_halves<LD>(s_sys, s_sys, lane);
         }
     } else if constexpr (R >= 48) {
         // From rank 48 on, by blocks: with I + K = [[P, Q], [M21, T]] and P
@@ -1414,7 +1413,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         constexpr int H1 = 32;
         constexpr int H2 = R - H1;
         if (wave == 0) {
-            gauss_jordan_halves<LD>(s_sys, s_sys, s_work, lane);
+            gauss_jordan_halves<LD>(s_sys, s_sys, lane);
         }
         __syncthreads();
         block_product<H1, H2, H1, 4>(wave, lane,
@@ -1434,7 +1433,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         // Theta's space is free once I + K is assembled.
         if constexpr (H2 == 32) {
             if (wave == 0) {
-                gauss_jordan_halves<LD>(s_sys + H1 * LD + H1, s_sys + H1 * LD + H1, s_theta, lane);
+                gauss_jordan_halves<LD>(s_sys + H1 * LD + H1, s_sys + H1 * LD + H1, lane);
             }
         } else {
             gauss_jordan_waves<H2, LD>(s_sys + H1 * LD + H1, s_theta, wave, lane);
