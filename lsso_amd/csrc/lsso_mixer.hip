@@ -886,91 +886,46 @@ __device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s
     }
 }
 
-// (I + K)^-1 in place by Gauss-Jordan on the diagonal pivots, with all four
-// waves of the workgroup: wave w holds columns [w CW, (w + 1) CW) of every
-// row, lane i row i, CW = R / 4 floats in registers.  Step k:
-//   1. the wave owning column k forms the multipliers f_i = a_ik / a_kk (the
-//      pivot by v_readlane from lane k) and publishes them in s_f;
-//   2. one barrier;
-//   3. every wave reads its lane's f_i and its own CW-column segment of pivot
-//      row k (written by lane k at the end of step k - 1, a broadcast read),
-//      updates a_ij -= f_i a_kj, keeps column k as column k of the inverse
-//      (1 in row k, -f_i elsewhere), and lane k + 1 writes its updated
-//      segment for the next step.
-// Buffers alternate by step parity, so one barrier per step orders every
-// write after the reads of two steps earlier.  The arithmetic (f = a_ik *
-// rcp(a_kk), one FMA per element and step, each row scaled by rcp of its own
-// pivot at the end) is that of the one-row-per-lane form, element for
-// element, with a quarter of the row per lane.  s_buf: 128 + 8 CW + R floats.
-template <int R, int LD>
-__device__ __forceinline__ void gauss_jordan_waves(float* s_sys, float* s_buf, int wave, int lane) {
-    constexpr int CW = R / 4;
-    float* s_f = s_buf;                  // [2][64] multipliers
-    float* s_seg = s_buf + 128;          // [4 waves][2][CW] pivot-row segments
-    float* s_piv = s_seg + 8 * CW;       // [R] pivots
-    const bool live = lane < R;
-    float t[CW];
-#pragma unroll
-    for (int c = 0; c < CW; c += 4) {
-        const f32x4 v = live ? *reinterpret_cast<const f32x4*>(s_sys + lane * LD + wave * CW + c)
-                             : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+// Gauss-Jordan of a rank-16 system, the rank-32 form with each row split
+// over the wave's four quarters: lane l holds columns 4 (l / 16) .. + 3 of row
+// l % 16.  Step k: the rows' column-k value comes from the quarter holding it
+// by ds_bpermute, and each quarter reads its part of pivot row k from lane
+// k of the quarter by ds_swizzle (inside each 32-lane group, keeping the
+// quarter bit).  Row k ends, scaled by 1 / pivot_k, at row k of s_out.
+template <int LD>
+__device__ __forceinline__ void gauss_jordan_quarters(const float* s_sys, float* s_out, int lane) {
+    const int quarter = lane >> 4;
+    const int row = lane & 15;
+    f32x4 t = *reinterpret_cast<const f32x4*>(s_sys + row * LD + 4 * quarter);
+    float own_pivot = 1.0f;
+    unroll_to<16>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const bool owner = quarter == (k >> 2);
+        const float own = t[k & 3];
+        const float x = __shfl(own, row + 16 * (k >> 2));
+        const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(own), 16 * (k >> 2) + k));
+        const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
+        const float f = row == k ? 0.0f : x * inv_pivot;
+        // Bit mode: source lane ((i & 16) | k) of each 32-lane group.
+        f32x4 pivot_row;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            t[c + e] = v[e];
+            pivot_row[e] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(t[e]), 16 | (k << 5)));
         }
-    }
-    auto write_segment = [&](int parity) {
-        float* dst = s_seg + (wave * 2 + parity) * CW;
 #pragma unroll
-        for (int c = 0; c < CW; c += 4) {
-            *reinterpret_cast<f32x4*>(dst + c) = (f32x4){t[c], t[c + 1], t[c + 2], t[c + 3]};
+        for (int e = 0; e < 4; ++e) {
+            t[e] = fmaf(-f, pivot_row[e], t[e]);
         }
-    };
-    if (lane == 0) {
-        write_segment(0);
-    }
-#pragma unroll 1
-    for (int owner = 0; owner < 4; ++owner) {
-        unroll_to<CW>([&](auto kc_c) {
-            constexpr int kc = decltype(kc_c)::value;
-            constexpr int parity = kc & 1;   // CW is even, so k and kc share parity
-            const int k = owner * CW + kc;
-            if (wave == owner) {
-                const float x = t[kc];
-                const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k));
-                s_f[parity * 64 + lane] = lane == k ? 0.0f : x * __builtin_amdgcn_rcpf(pivot);
-                if (lane == 0) {
-                    s_piv[k] = pivot;
-                }
-            }
-            __syncthreads();
-            const float f = s_f[parity * 64 + lane];
-            const float* seg = s_seg + (wave * 2 + parity) * CW;
-#pragma unroll
-            for (int c = 0; c < CW; c += 4) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(seg + c);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    t[c + e] = fmaf(-f, v[e], t[c + e]);
-                }
-            }
-            if (wave == owner) {
-                t[kc] = lane == k ? 1.0f : -f;
-            }
-            if (lane == k + 1) {
-                write_segment(parity ^ 1);
-            }
-        });
-    }
-    __syncthreads();
-    if (live) {
-        const float inv = __builtin_amdgcn_rcpf(s_piv[lane]);
-#pragma unroll
-        for (int c = 0; c < CW; c += 4) {
-            *reinterpret_cast<f32x4*>(s_sys + lane * LD + wave * CW + c) =
-                (f32x4){t[c] * inv, t[c + 1] * inv, t[c + 2] * inv, t[c + 3] * inv};
+        if (owner) {
+            t[k & 3] = row == k ? 1.0f : -f;
         }
-    }
+        if (row == k) {
+            own_pivot = pivot;
+        }
+    });
+    t = t * __builtin_amdgcn_rcpf(own_pivot);
+    wave_lds_order();
+    *reinterpret_cast<f32x4*>(s_out + row * LD + 4 * quarter) = t;
 }
 
 template <int R>
@@ -1393,11 +1348,10 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     // column k from every other row with the unscaled pivot row and keeps
     // column k as column k of the growing inverse; row k ends as pivot_k
     // times row k of the inverse.
-    // Rank 32 keeps the one-wave form with each row split over the wave's
-    // halves (no barrier per step: 20.2 against 22.3 us for the C2 solve
-    // stage, 22.7 against 25.5 at C3); from rank 48 on, where a row per
-    // lane costs R FMAs per step, the four-wave form is faster (C4 solve
-    // stage 66.4 against 75.4 us).
+    // Every elimination runs on one wave with each row split over the wave's
+    // halves (32 x 32) or quarters (16 x 16), with no barrier per step
+    // (against a four-wave form with one barrier per step: 20.2 against
+    // 22.3 us for the C2 solve stage); ranks past 32 go by 2 x 2 blocks.
     if constexpr (R == 32) {
         if (wave == 0) {
             gauss_jordan_halves<LD>(s_sys, s_sys, lane);
@@ -1436,7 +1390,9 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
                 gauss_jordan_halves<LD>(s_sys + H1 * LD + H1, s_sys + H1 * LD + H1, lane);
             }
         } else {
-            gauss_jordan_waves<H2, LD>(s_sys + H1 * LD + H1, s_theta, wave, lane);
+            if (wave == 0) {
+                gauss_jordan_quarters<LD>(s_sys + H1 * LD + H1, s_sys + H1 * LD + H1, lane);
+            }
         }
         __syncthreads();
         block_product<H2, H1, H2, 4>(wave, lane,
@@ -1453,7 +1409,9 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
                       [&](int j, int k) { return lds_column_quad(s_sys + H1 * LD, LD, k, j); },
                       [&](int i, int j, float v) { s_sys[i * LD + j] -= v; });
     } else {
-        gauss_jordan_waves<R, LD>(s_sys, s_work, wave, lane);
+        if (wave == 0) {
+            gauss_jordan_quarters<LD>(s_sys, s_sys, lane);
+        }
     }
     __syncthreads();
     if (tape != nullptr) {
