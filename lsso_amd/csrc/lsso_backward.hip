@@ -1198,6 +1198,408 @@ __global__ __launch_bounds__(256) void bwd_apply_resident_kernel(BwdApplyArgs a)
     }
 }
 
+// Token map from staged row runs (the forward apply's staging): one
+// workgroup per (sample, chunk, group of heads), one wave per head with that
+// head's records in registers, as in the resident map.  Each 16-token step's
+// relation, content and dY runs of the group and its phase rows are loaded
+// by every thread as 16-byte pieces two steps ahead and committed to LDS;
+// each wave reads its head's operands from LDS in the resident map's layout
+// and runs its products (same records, MFMA order, rounding and <dY, C>
+// order, so the same bits), and the group's dR and dC rows go out through an
+// LDS tile as 16-byte pieces of their two contiguous runs per token.  The
+// resident map reads each head's 16-token runs with per-wave loads of 8 to
+// 16 bytes per row.
+constexpr int kBwdStagedWaves = 4;
+constexpr int kBwdStagedCols = 448;     // group relation + content + dY columns, at most
+constexpr int kBwdStagedOut = 320;      // group dR + dC columns, at most
+constexpr int kBwdStagedRel = 2;        // 16-byte pieces per thread and step, at most:
+constexpr int kBwdStagedCon = 1;        //   relation, content, dY and phase pieces,
+constexpr int kBwdStagedDy = 1;
+constexpr int kBwdStagedPh = 1;
+constexpr int kBwdStagedOutPieces = 3;  //   and stored dR / dC pieces
+
+template <int R, int D16>
+__global__ __launch_bounds__(kBwdStagedWaves * 64) void bwd_apply_staged_kernel(BwdApplyArgs a, int group_heads) {
+    using In = BwdTokenInputs<R, D16>;
+    using RR = typename In::RR;
+    using RD = typename In::RD;
+    using RankOp = typename In::RankOp;
+    using FeatOp = typename In::FeatOp;
+    constexpr int RBLK = R / 16;
+    constexpr int RSTEPS = In::kRankSteps;
+    constexpr int DSTEPS = In::kFeatSteps;
+    constexpr int D = 16 * D16;
+    constexpr int PAIRS = R / 2;
+    constexpr int PHP = PAIRS + 4;                       // phase row pitch (u32)
+    __shared__ __attribute__((aligned(16))) uint16_t s_rows[2][16 * (kBwdStagedCols + 8)];
+    __shared__ __attribute__((aligned(16))) uint32_t s_ph[2][16 * PHP];
+    __shared__ __attribute__((aligned(16))) uint16_t s_out[2][16 * (kBwdStagedOut + 8)];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int threads = blockDim.x;
+    const int64_t groups = (a.heads + group_heads - 1) / group_heads;
+    int64_t rest = blockIdx.x;
+    const int64_t group = rest % groups;
+    rest /= groups;
+    const int64_t chunk = rest % a.chunks;
+    const int64_t b = rest / a.chunks;
+    const int64_t h0 = group * group_heads;
+    const int hg = static_cast<int>(group_heads < a.heads - h0 ? group_heads : a.heads - h0);
+    const int unit = wave;
+    const bool active = unit < hg;
+    const int64_t h = h0 + (active ? unit : 0);
+    const int64_t begin = chunk * a.chunk_tokens;
+    const int64_t end = begin + a.chunk_tokens < a.length ? begin + a.chunk_tokens : a.length;
+    if (begin >= end) {
+        return;   // uniform over the workgroup
+    }
+    const int q = lane & 15;
+    const int g = lane >> 4;
+    const int64_t system = b * a.heads + h;
+    const float eta = bounded_complement(a.eta_raw[h]);
+    const uint16_t* rec = a.records + system * a.record_stride;
+
+    // Records: dA^T = M dY + E C + G A (rank row blocks), dC^T = F A.
+    FeatOp m_hi[RBLK][DSTEPS], m_lo[RBLK][DSTEPS], e_hi[RBLK][DSTEPS], e_lo[RBLK][DSTEPS];
+    RankOp g_hi[RBLK][RSTEPS], g_lo[RBLK][RSTEPS], f_hi[D16][RSTEPS], f_lo[D16][RSTEPS];
+#pragma unroll
+    for (int rb = 0; rb < RBLK; ++rb) {
+#pragma unroll
+        for (int s = 0; s < DSTEPS; ++s) {
+            const int64_t o = ((rb * DSTEPS + s) * 64 + lane) * RD::kLaneHalfs;
+            m_hi[rb][s] = *reinterpret_cast<const FeatOp*>(rec + a.off_m + o);
+            m_lo[rb][s] = *reinterpret_cast<const FeatOp*>(rec + a.off_m + o + RD::kPerLane);
+            e_hi[rb][s] = *reinterpret_cast<const FeatOp*>(rec + a.off_e + o);
+            e_lo[rb][s] = *reinterpret_cast<const FeatOp*>(rec + a.off_e + o + RD::kPerLane);
+        }
+#pragma unroll
+        for (int s = 0; s < RSTEPS; ++s) {
+            const int64_t o = ((rb * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
+            g_hi[rb][s] = *reinterpret_cast<const RankOp*>(rec + a.off_g + o);
+            g_lo[rb][s] = *reinterpret_cast<const RankOp*>(rec + a.off_g + o + RR::kPerLane);
+        }
+    }
+#pragma unroll
+    for (int fb = 0; fb < D16; ++fb) {
+#pragma unroll
+        for (int s = 0; s < RSTEPS; ++s) {
+            const int64_t o = ((fb * RSTEPS + s) * 64 + lane) * RR::kLaneHalfs;
+            f_hi[fb][s] = *reinterpret_cast<const RankOp*>(rec + a.off_f + o);
+            f_lo[fb][s] = *reinterpret_cast<const RankOp*>(rec + a.off_f + o + RR::kPerLane);
+        }
+    }
+
+    // Row layout of a staged step: [relation runs | content runs | dY runs]
+    // of the group's heads, and the output tile's rows [dR runs | dC runs].
+    const int rel_pieces = hg * R / 8;
+    const int con_pieces = hg * D / 8;
+    const int pitch = 8 * (rel_pieces + 2 * con_pieces) + 8;
+    const int out_pieces = rel_pieces + con_pieces;
+    const int out_pitch = 8 * out_pieces + 8;
+    const int con_col = 8 * rel_pieces;
+    const int dy_col = con_col + 8 * con_pieces;
+    uint32_t rel_off[kBwdStagedRel], con_off[kBwdStagedCon], dy_off[kBwdStagedDy], ph_off[kBwdStagedPh];
+    int rel_lds[kBwdStagedRel], con_lds[kBwdStagedCon], dy_lds[kBwdStagedDy], ph_lds[kBwdStagedPh];
+#pragma unroll
+    for (int i = 0; i < kBwdStagedRel; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / rel_pieces;
+        const int c = piece - row * rel_pieces;
+        const bool live = piece < 16 * rel_pieces;
+        rel_off[i] = live ? 2u * static_cast<uint32_t>(row * a.width + 8 * c) : kOutOfRange;
+        rel_lds[i] = live ? row * pitch + 8 * c : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kBwdStagedCon; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / con_pieces;
+        const int c = piece - row * con_pieces;
+        const bool live = piece < 16 * con_pieces;
+        con_off[i] = live ? 2u * static_cast<uint32_t>(row * a.width + 8 * c) : kOutOfRange;
+        con_lds[i] = live ? row * pitch + con_col + 8 * c : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kBwdStagedDy; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / con_pieces;
+        const int c = piece - row * con_pieces;
+        const bool live = piece < 16 * con_pieces;
+        dy_off[i] = live ? 2u * static_cast<uint32_t>(row * a.grad_stride + 8 * c) : kOutOfRange;
+        dy_lds[i] = live ? row * pitch + dy_col + 8 * c : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kBwdStagedPh; ++i) {
+        const int piece = tid + i * threads;
+        const int row = piece / (PAIRS / 4);
+        const int c = piece - row * (PAIRS / 4);
+        const bool live = piece < 16 * (PAIRS / 4);
+        ph_off[i] = live ? 16u * static_cast<uint32_t>(piece) : kOutOfRange;
+        ph_lds[i] = live ? row * PHP + 4 * c : -1;
+    }
+    struct Stage {
+        u32x4 rel[kBwdStagedRel];
+        u32x4 con[kBwdStagedCon];
+        u32x4 dy[kBwdStagedDy];
+        u32x4 ph[kBwdStagedPh];
+    };
+    auto load = [&](Stage& st, int64_t t0) {
+        const int64_t rows = end - t0;
+        const uint16_t* row0 = a.projected + (b * a.length + t0) * a.width;
+        const BufferRsrc rel = make_buffer(row0 + h0 * R, 2 * rows * a.width);
+        const BufferRsrc con = make_buffer(row0 + a.heads * R + h0 * D, 2 * rows * a.width);
+        const BufferRsrc dy = make_buffer(a.grad_output + (b * a.length + t0) * a.grad_stride + h0 * D,
+                                          2 * rows * a.grad_stride);
+        const BufferRsrc ph = make_buffer(a.phases + b * a.phase_batch_stride + t0 * PAIRS, 4 * rows * PAIRS);
+#pragma unroll
+        for (int i = 0; i < kBwdStagedRel; ++i) {
+            st.rel[i] = buffer_load16_stream(rel, rel_off[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kBwdStagedCon; ++i) {
+            st.con[i] = buffer_load16_stream(con, con_off[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kBwdStagedDy; ++i) {
+            st.dy[i] = buffer_load16_stream(dy, dy_off[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kBwdStagedPh; ++i) {
+            st.ph[i] = buffer_load16(ph, ph_off[i]);
+        }
+    };
+    auto commit = [&](const Stage& st, int buf) {
+#pragma unroll
+        for (int i = 0; i < kBwdStagedRel; ++i) {
+            if (rel_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_rows[buf][rel_lds[i]]) = st.rel[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kBwdStagedCon; ++i) {
+            if (con_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_rows[buf][con_lds[i]]) = st.con[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kBwdStagedDy; ++i) {
+            if (dy_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_rows[buf][dy_lds[i]]) = st.dy[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kBwdStagedPh; ++i) {
+            if (ph_lds[i] >= 0) {
+                *reinterpret_cast<u32x4*>(&s_ph[buf][ph_lds[i]]) = st.ph[i];
+            }
+        }
+    };
+    // Output pieces of this thread: row and column of the group's runs.
+    uint32_t out_off[kBwdStagedOutPieces];
+    int out_lds[kBwdStagedOutPieces];
+#pragma unroll
+    for (int i = 0; i < kBwdStagedOutPieces; ++i) {
+        const int piece = tid + i * threads;
+        const bool live = piece < 16 * out_pieces;
+        const int row = piece / out_pieces;
+        const int c = piece - row * out_pieces;
+        const int64_t column = c < rel_pieces ? h0 * R + 8 * c : a.heads * R + h0 * D + 8 * (c - rel_pieces);
+        out_off[i] = live ? 2u * static_cast<uint32_t>(row * a.width + column) : kOutOfRange;
+        out_lds[i] = live ? row * out_pitch + 8 * c : 0;
+    }
+
+    float dot = 0.0f;
+    // Column sums of this head's [dR | dC] columns over the chunk, from the
+    // output tiles: lane j holds columns 2 j, 2 j + 1.
+    constexpr int kPairColumns = (R + D) / 2;
+    static_assert(kPairColumns <= 64, "one column pair per lane");
+    float col_even = 0.0f;
+    float col_odd = 0.0f;
+    const int rel_col = unit * R;
+    const int my_con = con_col + unit * D;
+    const int my_dy = dy_col + unit * D;
+    auto compute = [&](int buf, int obuf, int64_t t0) {
+        if (!active) {
+            return;
+        }
+        const uint16_t* prow = &s_rows[buf][q * pitch];
+        const uint32_t* phrow = &s_ph[buf][q * PHP];
+        uint16_t* orow = &s_out[obuf][q * out_pitch];
+        In cur;
+#pragma unroll
+        for (int s = 0; s < RSTEPS; ++s) {
+            const int first = RR::kWidth * s + RR::kPerLane * g;
+            cur.rel[s] = *reinterpret_cast<const RankOp*>(prow + rel_col + first);
+            cur.ph[s] = *reinterpret_cast<const RankOp*>(phrow + first / 2);
+        }
+#pragma unroll
+        for (int s = 0; s < DSTEPS; ++s) {
+            const int first = RD::kWidth * s + RD::kPerLane * g;
+            cur.y[s] = *reinterpret_cast<const FeatOp*>(prow + my_dy + first);
+            cur.c[s] = *reinterpret_cast<const FeatOp*>(prow + my_con + first);
+        }
+        RankOp a_hi[RSTEPS];
+        RankOp a_lo[RSTEPS];
+#pragma unroll
+        for (int s = 0; s < RSTEPS; ++s) {
+#pragma unroll
+            for (int pp = 0; pp < RR::kPerLane / 2; ++pp) {
+                float e, o;
+                rotate_pair(cur.rel[s][pp], cur.ph[s][pp], e, o);
+                uint32_t hi, lo;
+                split_bf16(e, o, hi, lo);
+                a_hi[s][pp] = hi;
+                a_lo[s][pp] = lo;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < DSTEPS; ++s) {
+#pragma unroll
+            for (int pp = 0; pp < RD::kPerLane / 2; ++pp) {
+                dot = fmaf(bf16_lo(cur.y[s][pp]), bf16_lo(cur.c[s][pp]), dot);
+                dot = fmaf(bf16_hi(cur.y[s][pp]), bf16_hi(cur.c[s][pp]), dot);
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < RBLK; ++rb) {
+            f32x4 acc_d = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 acc_r = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < DSTEPS; ++s) {
+                if constexpr (In::kDK32) {
+                    acc_d = mfma16x16x32(m_hi[rb][s], cur.y[s], acc_d);
+                    acc_d = mfma16x16x32(m_lo[rb][s], cur.y[s], acc_d);
+                    acc_d = mfma16x16x32(e_hi[rb][s], cur.c[s], acc_d);
+                    acc_d = mfma16x16x32(e_lo[rb][s], cur.c[s], acc_d);
+                } else {
+                    acc_d = mfma16x16x16(m_hi[rb][s], cur.y[s], acc_d);
+                    acc_d = mfma16x16x16(m_lo[rb][s], cur.y[s], acc_d);
+                    acc_d = mfma16x16x16(e_hi[rb][s], cur.c[s], acc_d);
+                    acc_d = mfma16x16x16(e_lo[rb][s], cur.c[s], acc_d);
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < RSTEPS; ++s) {
+                if constexpr (In::kRK32) {
+                    acc_r = mfma16x16x32(g_hi[rb][s], a_hi[s], acc_r);
+                    acc_r = mfma16x16x32(g_hi[rb][s], a_lo[s], acc_r);
+                    acc_r = mfma16x16x32(g_lo[rb][s], a_hi[s], acc_r);
+                } else {
+                    acc_r = mfma16x16x16(g_hi[rb][s], a_hi[s], acc_r);
+                    acc_r = mfma16x16x16(g_hi[rb][s], a_lo[s], acc_r);
+                    acc_r = mfma16x16x16(g_lo[rb][s], a_hi[s], acc_r);
+                }
+            }
+            // Lane holds dA[token q][ranks 16 rb + 4 g .. +3]: rotate back.
+            const int rank0 = 16 * rb + 4 * g;
+            const u32x2 ph = *reinterpret_cast<const u32x2*>(phrow + rank0 / 2);
+            float gradv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                gradv[i] = acc_d[i] + acc_r[i];
+            }
+            u32x2 packed;
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                const float cosine = f16_lo(ph[pp]);
+                const float sine = f16_hi(ph[pp]);
+                const float even = gradv[2 * pp] * cosine + gradv[2 * pp + 1] * sine;
+                const float odd = gradv[2 * pp + 1] * cosine - gradv[2 * pp] * sine;
+                packed[pp] = pack_bf16(even, odd);
+            }
+            *reinterpret_cast<u32x2*>(orow + rel_col + rank0) = packed;
+        }
+        // dC^T blocks: eta dY + (ds / sqrt(n))^T A^T.
+#pragma unroll
+        for (int fb = 0; fb < D16; ++fb) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < RSTEPS; ++s) {
+                if constexpr (In::kRK32) {
+                    acc = mfma16x16x32(f_hi[fb][s], a_hi[s], acc);
+                    acc = mfma16x16x32(f_hi[fb][s], a_lo[s], acc);
+                    acc = mfma16x16x32(f_lo[fb][s], a_hi[s], acc);
+                } else {
+                    acc = mfma16x16x16(f_hi[fb][s], a_hi[s], acc);
+                    acc = mfma16x16x16(f_hi[fb][s], a_lo[s], acc);
+                    acc = mfma16x16x16(f_lo[fb][s], a_hi[s], acc);
+                }
+            }
+            const int f0 = 16 * fb + 4 * g;
+            const u32x2 dyv = *reinterpret_cast<const u32x2*>(prow + my_dy + f0);
+            u32x2 packed;
+            packed.x = pack_bf16(fmaf(eta, bf16_lo(dyv.x), acc[0]), fmaf(eta, bf16_hi(dyv.x), acc[1]));
+            packed.y = pack_bf16(fmaf(eta, bf16_lo(dyv.y), acc[2]), fmaf(eta, bf16_hi(dyv.y), acc[3]));
+            *reinterpret_cast<u32x2*>(orow + con_col + unit * D + f0) = packed;
+        }
+        if (a.column_part != nullptr && lane < kPairColumns) {
+            // The wave's own tile rows: its reads follow its writes in order.
+            const int c = 2 * lane;
+            const int col = c < R ? rel_col + c : con_col + unit * D + (c - R);
+            float even = 0.0f;
+            float odd = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if (t0 + r < end) {
+                    const uint32_t v = *reinterpret_cast<const uint32_t*>(&s_out[obuf][r * out_pitch + col]);
+                    even += bf16_lo(v);
+                    odd += bf16_hi(v);
+                }
+            }
+            col_even += even;
+            col_odd += odd;
+        }
+    };
+    auto store = [&](int obuf, int64_t t0) {
+        const BufferRsrc out = make_buffer(a.grad_projected + (b * a.length + t0) * a.width,
+                                           2 * (end - t0) * a.width);
+#pragma unroll
+        for (int i = 0; i < kBwdStagedOutPieces; ++i) {
+            buffer_store16(*reinterpret_cast<const u32x4*>(&s_out[obuf][out_lds[i]]), out, out_off[i]);
+        }
+    };
+
+    // Two register stages (loads two steps ahead), two row buffers and two
+    // output tiles: one barrier per step.  Steps past the chunk load zeros
+    // and store nothing.
+    Stage stage_a;
+    Stage stage_b;
+    load(stage_a, begin);
+    __builtin_amdgcn_sched_barrier(0);
+    load(stage_b, begin + 16);
+    __builtin_amdgcn_sched_barrier(0);
+    commit(stage_a, 0);
+    __syncthreads();
+    for (int64_t t0 = begin; t0 < end; t0 += 32) {
+        load(stage_a, t0 + 32);
+        compute(0, 0, t0);
+        commit(stage_b, 1);
+        __syncthreads();
+        store(0, t0);
+        load(stage_b, t0 + 48);
+        compute(1, 1, t0 + 16);
+        commit(stage_a, 0);
+        __syncthreads();
+        store(1, t0 + 16);
+    }
+    if (active) {
+        if (a.column_part != nullptr && lane < kPairColumns) {
+            const int c = 2 * lane;
+            const int64_t column = c < R ? h * R + c : a.heads * R + h * D + c - R;
+            float* row = a.column_part + (b * a.chunks + chunk) * a.width + column;
+            row[0] = col_even;
+            row[1] = col_odd;
+        }
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            dot += __shfl_xor(dot, offset);
+        }
+        if (lane == 0) {
+            a.dot_part[system * a.chunks + chunk] = dot;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Parameter gradients.  One thread per element of dTheta0 and dW sums the
 // batch in ascending order (sixteen samples' loads issued together); one wave
@@ -1347,21 +1749,53 @@ bool bwd_apply_resident(int rank, int64_t head_dim, bool vec) {
     return vec && head_dim % 16 == 0 && d16 >= 1 && d16 <= resident_max_d16(rank);
 }
 
+// Heads per workgroup of the staged token map (0 when it does not apply):
+// up to four, so that a step's runs and output tile fit the staging limits,
+// and at most half the heads, so that a sample has at least two groups.
+static int bwd_staged_group_heads(int rank, const BwdApplyArgs& a) {
+    const int64_t d = a.head_dim;
+    int64_t group = kBwdStagedWaves < a.heads ? kBwdStagedWaves : a.heads;
+    while (group > 1 && (group * (rank + 2 * d) > kBwdStagedCols || group * (rank + d) > kBwdStagedOut)) {
+        --group;
+    }
+    if (group * 2 > a.heads && a.heads > 1) group = (a.heads + 1) / 2;
+    const int64_t threads = 64 * kBwdStagedWaves;
+    if (group * (rank + 2 * d) > kBwdStagedCols || group * (rank + d) > kBwdStagedOut ||
+        16 * group * rank / 8 > kBwdStagedRel * threads || 16 * group * d / 8 > kBwdStagedCon * threads ||
+        16 * (rank / 2) / 4 > kBwdStagedPh * threads ||
+        16 * group * (rank + d) / 8 > kBwdStagedOutPieces * threads || a.chunk_tokens % 16 != 0) {
+        return 0;
+    }
+    return static_cast<int>(group);
+}
+
+template <int R, int D16>
+static hipError_t launch_bwd_apply_token_map(const BwdApplyArgs& a, hipStream_t stream) {
+    const int group = bwd_staged_group_heads(R, a);
+    if (group > 0) {
+        const int64_t groups = (a.heads + group - 1) / group;
+        const dim3 grid(static_cast<unsigned>(a.batch * a.chunks * groups));
+        bwd_apply_staged_kernel<R, D16><<<grid, kBwdStagedWaves * 64, 0, stream>>>(a, group);
+        return hipGetLastError();
+    }
+    return launch_bwd_apply_resident<R, D16>(a, stream);
+}
+
 hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, bool vec, hipStream_t stream) {
     const int d16 = static_cast<int>(a.head_dim / 16);
     if (bwd_apply_resident(rank, a.head_dim, vec)) {
         switch (rank * 8 + d16) {
-            case 16 * 8 + 1: return launch_bwd_apply_resident<16, 1>(a, stream);
-            case 16 * 8 + 2: return launch_bwd_apply_resident<16, 2>(a, stream);
-            case 16 * 8 + 3: return launch_bwd_apply_resident<16, 3>(a, stream);
-            case 16 * 8 + 4: return launch_bwd_apply_resident<16, 4>(a, stream);
-            case 32 * 8 + 1: return launch_bwd_apply_resident<32, 1>(a, stream);
-            case 32 * 8 + 2: return launch_bwd_apply_resident<32, 2>(a, stream);
-            case 32 * 8 + 3: return launch_bwd_apply_resident<32, 3>(a, stream);
-            case 32 * 8 + 4: return launch_bwd_apply_resident<32, 4>(a, stream);
-            case 48 * 8 + 1: return launch_bwd_apply_resident<48, 1>(a, stream);
-            case 48 * 8 + 2: return launch_bwd_apply_resident<48, 2>(a, stream);
-            default: return launch_bwd_apply_resident<64, 1>(a, stream);
+            case 16 * 8 + 1: return launch_bwd_apply_token_map<16, 1>(a, stream);
+            case 16 * 8 + 2: return launch_bwd_apply_token_map<16, 2>(a, stream);
+            case 16 * 8 + 3: return launch_bwd_apply_token_map<16, 3>(a, stream);
+            case 16 * 8 + 4: return launch_bwd_apply_token_map<16, 4>(a, stream);
+            case 32 * 8 + 1: return launch_bwd_apply_token_map<32, 1>(a, stream);
+            case 32 * 8 + 2: return launch_bwd_apply_token_map<32, 2>(a, stream);
+            case 32 * 8 + 3: return launch_bwd_apply_token_map<32, 3>(a, stream);
+            case 32 * 8 + 4: return launch_bwd_apply_token_map<32, 4>(a, stream);
+            case 48 * 8 + 1: return launch_bwd_apply_token_map<48, 1>(a, stream);
+            case 48 * 8 + 2: return launch_bwd_apply_token_map<48, 2>(a, stream);
+            default: return launch_bwd_apply_token_map<64, 1>(a, stream);
         }
     }
     switch (rank) {
