@@ -822,76 +822,17 @@ __device__ __forceinline__ void with_column_tiles(int ncols, F&& f) {
     }
 }
 
-// Gauss-Jordan of a rank-32 system (the in-place form of solve_kernel, same
-// factors and updates element for element) with each matrix row split over
-// the two halves of the wave: lane l holds columns 16 (l / 32) .. + 15 of row
-// l % 32, so all 64 lanes update and each updates 16 columns.  Step k pivots
-// on the diagonal (no row exchanges: I + K has a positive definite symmetric
-// part, so every leading minor is nonzero); the rows' column-k value reaches
-// the other half by v_permlane32_swap, and each half reads its part of pivot row k
-// from lane k of the half with ds_swizzle (a broadcast inside each group of
-// 32 lanes, no LDS memory): the pivot row written to LDS and read back cost
-// two LDS latencies per step.  Row k ends, scaled by 1 / pivot_k, at row k of
-// s_out.
-template <int LD>
-__device__ __forceinline__ void gauss_jordan_halves(const float* s_sys, float* s_out, int lane) {
-    const int half = lane >> 5;
-    const int row = lane & 31;
-    f32x16 t;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(s_sys + row * LD + 16 * half + 4 * m);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            t[4 * m + e] = v[e];
-        }
-    }
-    float own_pivot = 1.0f;
-    unroll_to<32>([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        const bool owner = half == (k >> 4);
-        const float own = t[k & 15];
-        // The other half's value by v_permlane32_swap (a VALU lane swap):
-        // element 1 of the result holds lanes 32-63 in lanes 0-31, element 0
-        // lanes 0-31 in lanes 32-63.
-        const auto swapped = __builtin_amdgcn_permlane32_swap(__float_as_uint(own), __float_as_uint(own), false, false);
-        const float other = __uint_as_float(half != 0 ? swapped[0] : swapped[1]);
-        const float x = owner ? own : other;
-        const float pivot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(own), 32 * (k >> 4) + k));
-        const float inv_pivot = __builtin_amdgcn_rcpf(pivot);
-        const float f = row == k ? 0.0f : x * inv_pivot;
-        // Bit mode: source lane ((i & 0) | k) ^ 0 of each 32-lane group.
-        f32x16 pivot_row;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            pivot_row[e] = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(t[e]), k << 5));
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            t[e] = fmaf(-f, pivot_row[e], t[e]);
-        }
-        if (owner) {
-            t[k & 15] = row == k ? 1.0f : -f;
-        }
-        if (row == k) {
-            own_pivot = pivot;
-        }
-    });
-    t = t * __builtin_amdgcn_rcpf(own_pivot);
-    wave_lds_order();
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        *reinterpret_cast<f32x4*>(s_out + row * LD + 16 * half + 4 * m) =
-            (f32x4){t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
-    }
-}
-
-// Gauss-Jordan of a rank-16 system, the rank-32 form with each row split
+// Gauss-Jordan of a rank-16 system on one wave (the in-place form, pivots on
+// the diagonal: I + K has a positive definite symmetric part, so every
+// leading minor is nonzero and no row exchanges are needed), each row split
 // over the wave's four quarters: lane l holds columns 4 (l / 16) .. + 3 of row
 // l % 16.  Step k: the rows' column-k value comes from the quarter holding it
-// by ds_bpermute, and each quarter reads its part of pivot row k from lane
-// k of the quarter by ds_swizzle (inside each 32-lane group, keeping the
-// quarter bit).  Row k ends, scaled by 1 / pivot_k, at row k of s_out.
+// by ds_bpermute, the pivot by v_readlane, and each quarter reads its part of
+// pivot row k from lane k of the quarter by ds_swizzle (inside each 32-lane
+// group, keeping the quarter bit), so no step makes an LDS memory round
+// trip; each step eliminates column k from every other row with the
+// unscaled pivot row and keeps column k as column k of the growing inverse.
+// Row k ends, scaled by 1 / pivot_k, at row k of s_out.
 template <int LD>
 __device__ __forceinline__ void gauss_jordan_quarters(const float* s_sys, float* s_out, int lane) {
     const int quarter = lane >> 4;
@@ -926,6 +867,59 @@ __device__ __forceinline__ void gauss_jordan_quarters(const float* s_sys, float*
     t = t * __builtin_amdgcn_rcpf(own_pivot);
     wave_lds_order();
     *reinterpret_cast<f32x4*>(s_out + row * LD + 4 * quarter) = t;
+}
+
+// (I + K)^-1 of a 32 x 32 block in place (row stride LD) by 2 x 2 blocks of
+// 16: with the block [[P, Q], [M21, T]], P^-1 and S^-1 = (T - M21 W1)^-1 by
+// the rank-16 elimination and the four corners from W1 = P^-1 Q and
+// W2 = M21 P^-1, as in the rank-48 and rank-64 solve.  Wave 0 runs the
+// chain (P^-1; W1; S; S^-1; then the bottom-left and top-left corners) while
+// wave 1 forms W2 and then the top-right corner, with two barriers in all;
+// W1 and W2 go to rows 0-15 and 16-31 of scratch.  Every wave of the
+// workgroup calls it.
+template <int LD>
+__device__ __forceinline__ void invert32_by_blocks(float* m, float* scratch, int wave, int lane) {
+    float* p = m;
+    float* q = m + 16;
+    float* m21 = m + 16 * LD;
+    float* t = m + 16 * LD + 16;
+    float* w1 = scratch;
+    float* w2 = scratch + 16 * LD;
+    if (wave == 0) {
+        gauss_jordan_quarters<LD>(p, p, lane);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        block_product<16, 16, 16, 1>(0, lane, [&](int i, int k) { return lds_quad(p + i * LD + k); },
+                                     [&](int j, int k) { return lds_column_quad(q, LD, k, j); },
+                                     [&](int i, int j, float v) { w1[i * LD + j] = v; });
+        wave_lds_order();
+        block_product<16, 16, 16, 1>(0, lane, [&](int i, int k) { return lds_quad(m21 + i * LD + k); },
+                                     [&](int j, int k) { return lds_column_quad(w1, LD, k, j); },
+                                     [&](int i, int j, float v) { t[i * LD + j] -= v; });
+        wave_lds_order();
+        gauss_jordan_quarters<LD>(t, t, lane);
+    } else if (wave == 1) {
+        block_product<16, 16, 16, 1>(0, lane, [&](int i, int k) { return lds_quad(m21 + i * LD + k); },
+                                     [&](int j, int k) { return lds_column_quad(p, LD, k, j); },
+                                     [&](int i, int j, float v) { w2[i * LD + j] = v; });
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // Bottom-left -S^-1 W2 over M21, then top-left P^-1 - W1 (bottom-left).
+        block_product<16, 16, 16, 1>(0, lane, [&](int i, int k) { return lds_quad(t + i * LD + k); },
+                                     [&](int j, int k) { return lds_column_quad(w2, LD, k, j); },
+                                     [&](int i, int j, float v) { m21[i * LD + j] = -v; });
+        wave_lds_order();
+        block_product<16, 16, 16, 1>(0, lane, [&](int i, int k) { return lds_quad(w1 + i * LD + k); },
+                                     [&](int j, int k) { return lds_column_quad(m21, LD, k, j); },
+                                     [&](int i, int j, float v) { p[i * LD + j] -= v; });
+    } else if (wave == 1) {
+        // Top-right -W1 S^-1 over Q.
+        block_product<16, 16, 16, 1>(0, lane, [&](int i, int k) { return lds_quad(w1 + i * LD + k); },
+                                     [&](int j, int k) { return lds_column_quad(t, LD, k, j); },
+                                     [&](int i, int j, float v) { q[i * LD + j] = -v; });
+    }
 }
 
 template <int R>
@@ -1348,14 +1342,13 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     // column k from every other row with the unscaled pivot row and keeps
     // column k as column k of the growing inverse; row k ends as pivot_k
     // times row k of the inverse.
-    // Every elimination runs on one wave with each row split over the wave's
-    // halves (32 x 32) or quarters (16 x 16), with no barrier per step
-    // (against a four-wave form with one barrier per step: 20.2 against
-    // 22.3 us for the C2 solve stage); ranks past 32 go by 2 x 2 blocks.
+    // The eliminations are 16 x 16, on one wave with each row split over the
+    // wave's quarters and no barrier per step; 32 x 32 blocks go by 2 x 2
+    // blocks of 16 (invert32_by_blocks: 6.7k cycles against 10.4k for a
+    // one-wave rank-32 elimination with rows split over the wave's halves),
+    // and ranks past 32 by 2 x 2 blocks of those.
     if constexpr (R == 32) {
-        if (wave == 0) {
-            gauss_jordan_halves<LD>(s_sys, s_sys, lane);
-        }
+        invert32_by_blocks<LD>(s_sys, s_work, wave, lane);
     } else if constexpr (R >= 48) {
         // From rank 48 on, by blocks: with I + K = [[P, Q], [M21, T]] and P
         // 32 x 32, P^-1 (rank-32 elimination, wave 0), W1 = P^-1 Q and
@@ -1366,9 +1359,8 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         // instead of one of R steps.
         constexpr int H1 = 32;
         constexpr int H2 = R - H1;
-        if (wave == 0) {
-            gauss_jordan_halves<LD>(s_sys, s_sys, lane);
-        }
+        // Theta's space is free once I + K is assembled.
+        invert32_by_blocks<LD>(s_sys, s_theta, wave, lane);
         __syncthreads();
         block_product<H1, H2, H1, 4>(wave, lane,
                       [&](int i, int k) { return lds_quad(s_sys + i * LD + k); },
@@ -1384,11 +1376,8 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
                       [&](int j, int k) { return lds_column_quad(s_work, LD, k, j); },
                       [&](int i, int j, float v) { s_sys[(H1 + i) * LD + H1 + j] -= v; });
         __syncthreads();
-        // Theta's space is free once I + K is assembled.
         if constexpr (H2 == 32) {
-            if (wave == 0) {
-                gauss_jordan_halves<LD>(s_sys + H1 * LD + H1, s_sys + H1 * LD + H1, lane);
-            }
+            invert32_by_blocks<LD>(s_sys + H1 * LD + H1, s_theta, wave, lane);
         } else {
             if (wave == 0) {
                 gauss_jordan_quarters<LD>(s_sys + H1 * LD + H1, s_sys + H1 * LD + H1, lane);
