@@ -1071,7 +1071,7 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
     // column block j, while wave 1 forms L_j-1,j-1^-1 one column per lane and
     // waves 2-3 apply block j - 1 to the columns past j.  Only the panel
     // factorizations and one block-column update per step are on the chain;
-    // in step 0 waves 1-3 sum the first S panel.
+    // in steps 0 and 1 the other waves also sum the first S panel.
     // The diagonal blocks' inverses then join by doubling: for neighbouring
     // groups a (top) and b of h rows, L^-1_ba = -L^-1_bb (L_ba L^-1_aa).
     {
@@ -1079,11 +1079,20 @@ __global__ __launch_bounds__(kSolveThreads, 2) void solve_kernel(SolveArgs a) {
         unroll_to<B + 1>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             constexpr int j0 = 16 * j;
+            // The first S panel is summed beside the first two steps: rows
+            // 0 .. 3 kRows0 - 1 by waves 1-3 in step 0, the rest by waves 2-3
+            // in step 1 (beside wave 1's first inverse).
+            constexpr int kRows0 = (R / 2 + 2) / 3;
             if constexpr (j == 0) {
-                // Waves 1-3 sum the first S panel beside the first panel.
                 if (wave != 0) {
-                    load_cross_panel<R, (R + 2) / 3, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root,
-                                                                      s_pa, LD, lane, wave - 1, 3);
+                    load_cross_panel<R, kRows0, SL::kChunkBatch>(part, stride, chunks, d, 0, first_width, root, s_pa,
+                                                                 LD, lane, wave - 1, 3);
+                }
+            }
+            if constexpr (j == 1) {
+                if (wave >= 2) {
+                    load_cross_panel<R, (R - 3 * kRows0 + 1) / 2, SL::kChunkBatch>(
+                        part, stride, chunks, d, 0, first_width, root, s_pa, LD, lane, 3 * kRows0 + wave - 2, 2);
                 }
             }
             if constexpr (j < B) {
