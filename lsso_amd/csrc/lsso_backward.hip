@@ -164,61 +164,110 @@ __global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) 
     const float* drive = a.drive + h * d * R;
 
     // ---- loads: every load of a thread is issued before its first LDS store
-    // (the loads are latency-bound; a rolled loop would wait for each); L is
-    // held in registers until its phase.
-    constexpr int kSquare = (R * R + kBwdThreads - 1) / kBwdThreads;
-    float l_pre[kSquare];
+    // (the loads are latency-bound; a rolled loop would wait for each), as
+    // 16-byte pieces of the tape's rows (and of the r x d rows and partials
+    // when head_dim is a multiple of 4); L is held in registers until its
+    // phase.
+    constexpr int kSquare = (R * R / 4 + kBwdThreads - 1) / kBwdThreads;   // quads per thread
+    f32x4 l_pre[kSquare];
     {
-        float linv[kSquare];
-        float inv[kSquare];
-        float theta[kSquare];
+        f32x4 linv[kSquare];
+        f32x4 inv[kSquare];
+        f32x4 theta[kSquare];
 #pragma unroll
         for (int t = 0; t < kSquare; ++t) {
-            const int idx = tid + t * kBwdThreads < R * R ? tid + t * kBwdThreads : 0;
-            linv[t] = tape[3 * R * R + idx];
-            inv[t] = tape[2 * R * R + idx];
-            theta[t] = tape[R * R + idx];
-            l_pre[t] = tape[idx];
+            const int q = tid + t * kBwdThreads;
+            const int idx = 4 * (q < R * R / 4 ? q : 0);
+            linv[t] = *reinterpret_cast<const f32x4*>(tape + 3 * R * R + idx);
+            inv[t] = *reinterpret_cast<const f32x4*>(tape + 2 * R * R + idx);
+            theta[t] = *reinterpret_cast<const f32x4*>(tape + R * R + idx);
+            l_pre[t] = *reinterpret_cast<const f32x4*>(tape + idx);
         }
-        constexpr int kRect = (R * kBwdMaxHeadDim + kBwdThreads - 1) / kBwdThreads;
-        float zv[kRect];
-        float uv[kRect];
-        float dmv[kRect];
-#pragma unroll
-        for (int t = 0; t < kRect; ++t) {
-            const int idx = tid + t * kBwdThreads < R * d ? tid + t * kBwdThreads : 0;
-            zv[t] = tape[4 * R * R + idx];
-            uv[t] = tape[4 * R * R + R * d + idx];
-            dmv[t] = 0.0f;
-        }
-        for (int ch = 0; ch < a.chunks; ++ch) {
+        // z, u and the chunk sums of dm (r x d), W floats per item.
+        auto rect = [&](auto vec_c) {
+            constexpr int W = decltype(vec_c)::value ? 4 : 1;
+            using T = typename std::conditional<W == 4, f32x4, float>::type;
+            constexpr int kRect = (R * kBwdMaxHeadDim / W + kBwdThreads - 1) / kBwdThreads;
+            const int items = R * d / W;
+            auto at = [&](int t) {
+                const int item = tid + t * kBwdThreads;
+                return W * (item < items ? item : 0);
+            };
+            auto elem = [](const T& v, int e) {
+                if constexpr (W == 4) {
+                    return v[e];
+                } else {
+                    return v;
+                }
+            };
+            T zv[kRect];
+            T uv[kRect];
+            T dmv[kRect];
 #pragma unroll
             for (int t = 0; t < kRect; ++t) {
-                const int idx = tid + t * kBwdThreads < R * d ? tid + t * kBwdThreads : 0;
-                dmv[t] += part[ch * a.partial_stride + idx];
+                zv[t] = *reinterpret_cast<const T*>(tape + 4 * R * R + at(t));
+                uv[t] = *reinterpret_cast<const T*>(tape + 4 * R * R + R * d + at(t));
+                dmv[t] = T{};
             }
+            // Chunk partials in ascending order, four chunks' loads in flight
+            // (one chunk at a time waited out each chunk's load latency).
+            constexpr int kChunkBatch = 4;
+            for (int ch0 = 0; ch0 < a.chunks; ch0 += kChunkBatch) {
+                T pv[kChunkBatch][kRect];
+#pragma unroll
+                for (int u = 0; u < kChunkBatch; ++u) {
+                    const int64_t ch = ch0 + u < a.chunks ? ch0 + u : a.chunks - 1;
+#pragma unroll
+                    for (int t = 0; t < kRect; ++t) {
+                        pv[u][t] = *reinterpret_cast<const T*>(part + ch * a.partial_stride + at(t));
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kChunkBatch; ++u) {
+                    if (ch0 + u < a.chunks) {
+#pragma unroll
+                        for (int t = 0; t < kRect; ++t) {
+                            dmv[t] += pv[u][t];
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < kRect; ++t) {
+                const int item = tid + t * kBwdThreads;
+                if (item < items) {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) {
+                        const int idx = W * item + e;
+                        const int i = idx / d;
+                        const int f = idx - i * d;
+                        const float z = elem(zv[t], e);
+                        const float u = elem(uv[t], e);
+                        s_z[i * PD + f] = z;
+                        s_u[i * PD + f] = u;
+                        s_x[i * PD + f] = 2.0f * u - (1.0f + eta) * z;
+                        s_v[i * PD + f] = elem(dmv[t], e) / root;
+                    }
+                }
+            }
+        };
+        if (d % 4 == 0) {
+            rect(std::true_type{});
+        } else {
+            rect(std::false_type{});
         }
 #pragma unroll
         for (int t = 0; t < kSquare; ++t) {
-            const int idx = tid + t * kBwdThreads;
-            if (idx < R * R) {
-                const int i = idx / R;
-                const int j = idx - i * R;
-                s_linv[i * PR + j] = linv[t];
-                s_k[i * PR + j] = inv[t];
-                s_f[i * PR + j] = theta[t];
-            }
-        }
+            const int q = tid + t * kBwdThreads;
+            if (q < R * R / 4) {
+                const int i = (4 * q) / R;
+                const int j = 4 * q - i * R;
 #pragma unroll
-        for (int t = 0; t < kRect; ++t) {
-            const int idx = tid + t * kBwdThreads;
-            if (idx < R * d) {
-                const int i = idx / d;
-                const int f = idx - i * d;
-                s_z[i * PD + f] = zv[t];
-                s_u[i * PD + f] = uv[t];
-                s_x[i * PD + f] = 2.0f * uv[t] - (1.0f + eta) * zv[t];
-                s_v[i * PD + f] = dmv[t] / root;
+                for (int e = 0; e < 4; ++e) {
+                    s_linv[i * PR + j + e] = linv[t][e];
+                    s_k[i * PR + j + e] = inv[t][e];
+                    s_f[i * PR + j + e] = theta[t][e];
+                }
             }
         }
     }
@@ -332,11 +381,14 @@ __global__ __launch_bounds__(kBwdThreads) void bwd_solve_kernel(BwdSolveArgs a) 
                         [&](int i, int j, float v) { s_f[i * PR + j] = j <= i ? -(s_f[i * PR + j] + v) : 0.0f; });
 #pragma unroll
     for (int t = 0; t < kSquare; ++t) {
-        const int idx = tid + t * kBwdThreads;
-        if (idx < R * R) {
-            const int i = idx / R;
-            const int j = idx - i * R;
-            s_k[i * PR + j] = l_pre[t];
+        const int q = tid + t * kBwdThreads;
+        if (q < R * R / 4) {
+            const int i = (4 * q) / R;
+            const int j = 4 * q - i * R;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s_k[i * PR + j + e] = l_pre[t][e];
+            }
         }
     }
     __syncthreads();
