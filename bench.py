@@ -81,6 +81,11 @@ def parse_args() -> argparse.Namespace:
                         help="after the timed region, run one torch device copy of this many MiB "
                              "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE), then "
                              "the copy/read/write probes, and report their rates as copy_ceiling")
+    parser.add_argument("--gemm-yardstick", type=int, default=0,
+                        help="forward only: after the timed region, time this many calls each of the "
+                             "input projection alone as a plain GEMM at the layer's shape (tokens x D "
+                             "-> H (r + d)): torch's BF16 mm and linear (hipBLASLt) and this "
+                             "library's linear_kernel, and report them as gemm_yardstick")
     return parser.parse_args()
 
 
@@ -195,6 +200,52 @@ def copy_ceiling(mib, device):
         entry["GB/s"] = entry["bytes"] / (entry["ms"] * 1e-3) / 1e9
     del source, target, sink
     return rates
+def gemm_yardstick(x, weight, bias, calls: int) -> dict:
+    """The input projection alone as a plain GEMM at the layer's shape.
+
+    x [B, L, D] (FP16 or BF16), weight [W, D] and bias [W] (FP32): torch's
+    BF16 `mm` and `linear` (hipBLASLt kernels on ROCm) on BF16 copies of the
+    operands, and this library's `linear_kernel` (x as given, BF16 output,
+    FP32 bias, the unfused input projection of the layer).  Each case runs
+    `calls` untimed calls, then `calls` calls with events around each one on
+    torch's current stream.  Returns {case: {"median_us", "mean_us", "GB/s",
+    "TFLOP/s"}} with bytes = x read + output written (2 bytes each) and
+    flops = 2 M N K.
+    """
+    from lsso_amd.ball import hip
+
+    rows, depth = x.shape[0] * x.shape[1], x.shape[2]
+    width = weight.shape[0]
+    x_bf16 = x.reshape(rows, depth).bfloat16()
+    w_bf16 = weight.bfloat16()
+    w_t = w_bf16.t().contiguous()
+    b_bf16 = bias.bfloat16()
+    cases = {
+        "torch_mm_bf16": lambda: torch.mm(x_bf16, w_t),
+        "torch_linear_bf16": lambda: torch.nn.functional.linear(x_bf16, w_bf16, b_bf16),
+        "lsso_linear_kernel": lambda: hip.linear(x, weight, bias, torch.bfloat16),
+    }
+    moved = rows * depth * 2 + rows * width * 2
+    flops = 2 * rows * width * depth
+    out = {}
+    with torch.inference_mode():
+        for name, call in cases.items():
+            for _ in range(calls):
+                call()
+            events = [torch.cuda.Event(enable_timing=True) for _ in range(2 * calls)]
+            for i in range(calls):
+                events[2 * i].record()
+                call()
+                events[2 * i + 1].record()
+            torch.cuda.synchronize()
+            times = [events[2 * i].elapsed_time(events[2 * i + 1]) * 1e3 for i in range(calls)]
+            median = statistics.median(times)
+            out[name] = {"median_us": median, "mean_us": statistics.mean(times),
+                         "GB/s": moved / (median * 1e-6) / 1e9, "TFLOP/s": flops / (median * 1e-6) / 1e12}
+    del x_bf16, w_bf16, w_t, b_bf16
+    return out
+
+
 CLOCK_SPINS = 300  # about 5 us of one dependent FMA chain per clock probe
 CLOCK_WINDOWS = (0, 5, 10, 20, 50, 100, 200, 400, 1000)
 
@@ -630,6 +681,7 @@ def main() -> int:
     }
     dominant = stage_names[slot]
     copy_rates = copy_ceiling(args.copy_mib, device) if args.copy_mib > 0 else None
+    yardstick = gemm_yardstick(x, w_bc, b_bc, args.gemm_yardstick) if args.gemm_yardstick > 0 else None
     clocks = None
     if args.clock_trace > 0:
         with torch.inference_mode():
@@ -720,6 +772,8 @@ def main() -> int:
         result["parity"] = parity(layer, x_cpu, check, fp32_output, samples, mask_cpu, position_ids_cpu)
     if copy_rates is not None:
         result["copy_ceiling"] = copy_rates
+    if yardstick is not None:
+        result["gemm_yardstick"] = yardstick
     if clocks is not None:
         clocks["kernel"] = kernel_name
         result["clock_trace"] = clocks
