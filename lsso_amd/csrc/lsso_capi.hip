@@ -1424,12 +1424,15 @@ int lsso_hip_layer_forward_train(const lsso_hip_mixer_shape* shape, const void* 
 
 namespace {
 
-// The fused projection + reduce reads x once per head group.  From rank 48
-// on (three or more groups at H*d = 256, and register spills in those
-// instantiations) the separate projection and reduce are faster: at B = 64,
-// N = 2048, H = 8, d = 32 the projection, phase table, reduce and solve took
-// 125 / 154 / 349 / 463 us fused against 143 / 172 / 272 / 397 us separate for
-// rank 16 / 32 / 48 / 64.
+// The fused projection + reduce reads x once per head group and runs one
+// head's reductions per wave beside the projection.  From rank 48 on the
+// separate projection and staged reduce are faster: a group holds three heads
+// (one reduction wave idle) and each head's reduction, with two pair slots per
+// lane, sets the tile's pace.  Measured on one MI355X with the spill-free
+// rank-48/64 kernels: at B = 64, N = 2048, H = 8, r = 48, d = 32 (the
+// training forward) 146.5 us fused against 75.3 + 53.5 us for the projection
+// and the staged reduce; at B = 32, N = 4096, H = 6, r = 64, D = 384 the stage
+// took 284.7 us fused against 169.6 us.
 bool fused_projection_pays(const MixerPlan& plan) { return plan.rank <= 32; }
 
 // The input projection and the token reductions: writes `packed` (bitwise

@@ -593,6 +593,74 @@ __global__ __launch_bounds__(pr_waves<KSTEPS>() * 64) void project_reduce_kernel
         __syncthreads();
     };
 
+    if constexpr (R > 32) {
+        // From rank 48 on the reductions hold more registers than two
+        // stages leave free, so one stage serves: a step first commits tile
+        // k + 1 (loaded during the previous step) to LDS, then issues the
+        // loads of tile k + 2 into the same registers, then reduces tile
+        // k - 1.  The loads have one step to arrive.
+        Stage st;
+        Cursor cur = open_item(static_cast<int>(slot));
+        Cursor nx1 = advance(cur);
+        load_stage(st, cur, 0);
+        load_stage(st, cur, 1);
+        write_stage(st, 0, 0);
+        load_stage(st, nx1, 0);
+        load_stage(st, nx1, 1);
+        __syncthreads();   // s_bias, s_col and tile 0 are in LDS
+        Cursor prev = cur;
+        prev.item = n_items;
+        int k2 = 0;
+        int k3 = 0;
+        while (true) {
+            const Cursor nx2 = advance(nx1);
+            if (nx1.item < n_items) {
+                write_stage(st, k2 ^ 1, k3 == 2 ? 0 : k3 + 1);
+            }
+            load_stage(st, nx2, 0);
+            load_stage(st, nx2, 1);
+            if (prev.item < n_items) {
+                const uint16_t* yt = s_y[k2 ^ 1];
+                const uint32_t* pt = s_ph[k3 == 0 ? 2 : k3 - 1];
+                if (unit_active) {
+#pragma unroll 1
+                    for (int half = 0; half < 2; ++half) {
+                        if (prev.t0 + 32 * half < prev.end) {
+                            ReduceTile<R, CPW> t;
+                            lds_tile(t, yt, pt, half);
+                            reduce_compute<R, CPW>(t, true, acc_g, acc_s);
+                        }
+                    }
+                }
+                if (cur.item != prev.item) {
+                    if (unit_active) {
+                        // The store offsets are formed here, once per chunk,
+                        // rather than kept in registers across the loop.
+                        const int lane_o = opaque_int(lane);
+                        const int q = lane_o & 15;
+                        const int g = lane_o >> 4;
+                        float* part = a.partials +
+                                      ((prev.b * a.heads + h0 + unit_head) * a.chunks + prev.chunk) *
+                                          a.partial_stride;
+                        store_gram_partial<R>(part, acc_g, q, g);
+                        store_cross_partial<R, CPW>(part + R * R, acc_s, q, g, 0, d);
+                    }
+                    clear_units();
+                }
+            }
+            __syncthreads();
+            if (cur.item >= n_items) {
+                break;
+            }
+            prev = cur;
+            cur = nx1;
+            nx1 = nx2;
+            k2 ^= 1;
+            k3 = k3 == 2 ? 0 : k3 + 1;
+        }
+        return;
+    }
+
     Stage stage_a;
     Stage stage_b;
     Cursor cur = open_item(static_cast<int>(slot));
