@@ -550,9 +550,11 @@ def main() -> int:
     with torch.inference_mode():
         centered_positions, valid_counts, row_mask = layer._native_geometry(x, mask, position_ids)
     # Which kernels the layer call runs: the input projection is fused with
-    # the reductions up to rank 32, and the apply with the output projection
-    # inside the fused readout's envelope (lsso_hip_mixer_projected_supported).
-    fused_in = rank <= 32
+    # the reductions up to rank 32 (LSSO_HIP_FUSED_PROJECTION=1 or 0 makes the
+    # library fuse at every rank or never), and the apply with the output
+    # projection inside the fused readout's envelope
+    # (lsso_hip_mixer_projected_supported).
+    fused_in = {"1": True, "0": False}.get(os.environ.get("LSSO_HIP_FUSED_PROJECTION", ""), rank <= 32)
     probe = torch.empty(1, 1, width, dtype=torch.bfloat16, device=device)
     fused_out = hip.mix_project_supported(probe, layer.core_base_raw, layer.core_drive_weight,
                                           layer.eta_raw)

@@ -6,6 +6,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -1433,7 +1434,20 @@ namespace {
 // training forward) 146.5 us fused against 75.3 + 53.5 us for the projection
 // and the staged reduce; at B = 32, N = 4096, H = 6, r = 64, D = 384 the stage
 // took 284.7 us fused against 169.6 us.
-bool fused_projection_pays(const MixerPlan& plan) { return plan.rank <= 32; }
+//
+// LSSO_HIP_FUSED_PROJECTION overrides the rule for A/B measurements and
+// tests: "1" fuses at every rank the fused kernel supports, "0" never fuses.
+// Either way the results are the same bits.
+bool fused_projection_pays(const MixerPlan& plan) {
+    const char* mode = std::getenv("LSSO_HIP_FUSED_PROJECTION");
+    if (mode != nullptr && mode[0] == '1' && mode[1] == '\0') {
+        return true;
+    }
+    if (mode != nullptr && mode[0] == '0' && mode[1] == '\0') {
+        return false;
+    }
+    return plan.rank <= 32;
+}
 
 // The input projection and the token reductions: writes `packed` (bitwise
 // lsso_hip_linear's output) and the reduce partials of buf (bitwise

@@ -193,6 +193,51 @@ def test_project_mix_is_bitwise_linear_then_forward_train(native, batch, rank, h
     assert torch.equal(tape, expected_tape)
 
 
+@pytest.mark.parametrize(
+    ("mode", "batch", "rank", "heads", "head_dim", "length", "masked"),
+    [
+        ("1", 2, 48, 8, 32, 333, False),   # C5 geometry fused: 3 head groups, the last with 2 heads
+        ("1", 1, 64, 6, 64, 300, True),    # C4 geometry fused: D = 384 (4-wave tier), masked
+        ("1", 1, 48, 2, 64, 130, True),    # rank 48 with 64-feature heads (two content blocks)
+        ("0", 2, 32, 8, 32, 1000, True),   # headline geometry with the separate kernels
+    ],
+)
+def test_fused_projection_override_keeps_the_bits(native, monkeypatch, mode, batch, rank, heads, head_dim,
+                                                  length, masked):
+    """LSSO_HIP_FUSED_PROJECTION=1 runs the fused projection + reduce kernel at
+    ranks where the library would otherwise run the projection and the reduce
+    separately (and =0 the reverse); the layer forward and the training forward
+    must still equal the separate calls bit for bit."""
+    x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(
+        batch, rank, heads, head_dim, length, seed=7000 + rank + length
+    )
+    positions, counts, mask = None, None, None
+    if masked:
+        generator = torch.Generator().manual_seed(length + 1)
+        valid = torch.randint(length // 4, length + 1, (batch,), generator=generator)
+        mask = (torch.arange(length)[None, :] < valid[:, None]).cuda()
+        counts = valid.float().cuda()
+        starts = torch.randint(0, 1024, (batch, 1), generator=generator).float()
+        raw = starts + torch.arange(length, dtype=torch.float32)[None, :]
+        centre = (raw * mask.cpu()).sum(dim=1, keepdim=True) / valid[:, None]
+        positions = (raw - centre).cuda()
+    with torch.no_grad():
+        expected = _three_calls(native, x, in_w, in_b, base, drive, eta_raw, positions, counts, out_w, out_b, mask)
+        projected = native.linear(x, in_w, in_b, torch.bfloat16, row_mask=mask)
+        expected_mixed, expected_tape = native.forward_train(projected, base, drive, eta_raw, positions, counts)
+        monkeypatch.setenv("LSSO_HIP_FUSED_PROJECTION", mode)
+        y = native.layer_forward(x, in_w, in_b, base, drive, eta_raw, positions, counts, out_w, out_b,
+                                 row_mask=mask)
+        packed, mixed, tape = native._project_mix_forward(
+            x, in_w, in_b, base, drive, eta_raw, positions, counts, mask, True
+        )
+    torch.cuda.synchronize()
+    assert torch.equal(y, expected)
+    assert torch.equal(packed, projected)
+    assert torch.equal(mixed, expected_mixed)
+    assert torch.equal(tape, expected_tape)
+
+
 def test_project_mix_gradients_equal_the_two_call_path(native):
     x, in_w, in_b, base, drive, eta_raw, out_w, out_b = _layer_inputs(2, 48, 8, 32, 300, seed=77)
     mask = torch.ones(2, 300, dtype=torch.bool, device="cuda")
