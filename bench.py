@@ -16,6 +16,10 @@ Prints one JSON line with the driver's fields plus
                 per-step time of the same number of steps started cold;
   cpu_baseline  the CPU oracle (FP32 restatement of the reference CPU path)
                 timed on this host on a bounded sample of the same workload.
+On request (flags below) it also carries copy_ceiling (HBM copy, read and
+write probes), clock_trace (shader clock after an idle gap) and
+gemm_yardstick (the input projection alone as a plain GEMM, in hipBLASLt and
+in this library).
 """
 
 from __future__ import annotations
