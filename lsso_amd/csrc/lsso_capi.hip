@@ -1191,16 +1191,13 @@ int lsso_hip_linear_weight_grad(const void* g, int g_dtype, int64_t g_row_stride
     if (error != hipSuccess) {
         return hip_failure(error, "weight_grad_kernel launch");
     }
-    error = lsso_hip::launch_column_sum(partials, plan.splits, out_features * in_features,
-                                        grad_weight, stream);
+    // The weight's and the bias's split partials are summed in one launch.
+    error = lsso_hip::launch_column_sums(partials, out_features * in_features, grad_weight,
+                                         grad_bias != nullptr ? bias_partials : nullptr,
+                                         grad_bias != nullptr ? out_features : 0, grad_bias, plan.splits,
+                                         stream);
     if (error != hipSuccess) {
-        return hip_failure(error, "column_sum_kernel launch (weight gradient)");
-    }
-    if (grad_bias != nullptr) {
-        error = lsso_hip::launch_column_sum(bias_partials, plan.splits, out_features, grad_bias, stream);
-        if (error != hipSuccess) {
-            return hip_failure(error, "column_sum_kernel launch (bias gradient)");
-        }
+        return hip_failure(error, "column_sum_kernel launch (weight and bias gradients)");
     }
     return LSSO_HIP_OK;
 }

@@ -299,6 +299,10 @@ hipError_t launch_bwd_apply(int rank, const BwdApplyArgs& a, bool dk32, bool vec
 bool bwd_apply_resident(int rank, int64_t head_dim, bool vec);
 hipError_t launch_column_sum(const float* partials, int64_t splits, int64_t cols, float* out,
                              hipStream_t stream);
+// Two column sums over the same number of splits in one launch (partials2
+// may be null when cols2 is 0).
+hipError_t launch_column_sums(const float* partials, int64_t cols, float* out, const float* partials2,
+                              int64_t cols2, float* out2, int64_t splits, hipStream_t stream);
 hipError_t launch_param_reduce(const ParamReduceArgs& a, hipStream_t stream);
 
 hipError_t launch_linear(const LinearArgs& a, int k_steps, int x_dtype, int y_dtype,

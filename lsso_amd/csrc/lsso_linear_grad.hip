@@ -132,14 +132,25 @@ __global__ __launch_bounds__(kGradThreads) void grad_columns_kernel(GradColumnsA
 
 // out[c] = sum over splits s of partials[s][c]: 32 columns x 8 split lanes
 // per workgroup; split lane l adds splits l, l + 8, ... in order (sixteen
-// loads in flight), then the lanes are added in lane order.
+// loads in flight), then the lanes are added in lane order.  One launch can
+// serve two such sums over the same splits (a weight gradient and its bias):
+// the first `blocks` workgroups take the first, the rest the second.
 __global__ __launch_bounds__(kGradThreads) void column_sum_kernel(const float* partials, int64_t splits,
-                                                                  int64_t cols, float* out) {
+                                                                  int64_t cols, float* out,
+                                                                  const float* partials2, int64_t cols2,
+                                                                  float* out2, int64_t blocks) {
     constexpr int kLanes = kGradThreads / 32;
     constexpr int kLoads = 16;
     const int c = threadIdx.x & 31;
     const int lane = threadIdx.x >> 5;
-    const int64_t column = static_cast<int64_t>(blockIdx.x) * 32 + c;
+    int64_t block = blockIdx.x;
+    if (block >= blocks) {   // uniform over the workgroup
+        block -= blocks;
+        partials = partials2;
+        cols = cols2;
+        out = out2;
+    }
+    const int64_t column = block * 32 + c;
     const int64_t safe_column = column < cols ? column : 0;
     float acc = 0.0f;
     for (int64_t s0 = lane; s0 < splits; s0 += kLanes * kLoads) {
@@ -171,8 +182,16 @@ __global__ __launch_bounds__(kGradThreads) void column_sum_kernel(const float* p
 
 hipError_t launch_column_sum(const float* partials, int64_t splits, int64_t cols, float* out,
                              hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>((cols + 31) / 32));
-    column_sum_kernel<<<grid, kGradThreads, 0, stream>>>(partials, splits, cols, out);
+    return launch_column_sums(partials, cols, out, nullptr, 0, nullptr, splits, stream);
+}
+
+hipError_t launch_column_sums(const float* partials, int64_t cols, float* out, const float* partials2,
+                              int64_t cols2, float* out2, int64_t splits, hipStream_t stream) {
+    const int64_t blocks = (cols + 31) / 32;
+    const int64_t blocks2 = (cols2 + 31) / 32;
+    const dim3 grid(static_cast<unsigned>(blocks + blocks2));
+    column_sum_kernel<<<grid, kGradThreads, 0, stream>>>(partials, splits, cols, out, partials2, cols2, out2,
+                                                         blocks);
     return hipGetLastError();
 }
 
@@ -198,9 +217,7 @@ hipError_t launch_grad_columns(const GradColumnsArgs& a, int g_dtype, bool vec, 
     if (error != hipSuccess || column_sums == nullptr) {
         return error;
     }
-    const dim3 sum_grid(static_cast<unsigned>((a.cols + 31) / 32));
-    column_sum_kernel<<<sum_grid, kGradThreads, 0, stream>>>(a.partials, splits, a.cols, column_sums);
-    return hipGetLastError();
+    return launch_column_sum(a.partials, splits, a.cols, column_sums, stream);
 }
 
 }  // namespace lsso_hip
